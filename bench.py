@@ -1,0 +1,277 @@
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Headline workload (the decode target "KV length 4096"):
+a 28-layer stack of GQA decode attention, Qwen3-1.7B layer shape (16 q / 8 kv heads,
+head_dim 128), B = 16 independent streams, base KV length L = 4096, bf16 KV in 16-token
+pages with per-stream page tables.  One step = for each of the 28 layers: append the new
+token's K/V to the paged cache, then attend S = L + t + 1 keys.  Inputs are synthetic and
+resident in HBM before timing.
+
+`value` = decode-attention algorithmic bytes / wall time of the K timed steps, where the
+bytes per (stream, layer, step) are 2*S*Hkv*Dh*2 (K and V read once) + Hq*Dh*4 (q) +
+Hq*Dh*4 (out) + 4 B per page-table entry.  The roofline object divides the same bytes
+per launch by the decode kernel's average launch duration (HIP events around each launch
+on its stream).  The CPU baseline is the oracle's scalar decode on the host cores, over a
+bounded sample of the same workload.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
+
+LAYERS, B, HQ, HKV, DH, L_BASE, PAGE = 28, 16, 16, 8, 128, 4096, 16
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def decode_bytes(S: int, n_pages: int) -> int:
+    return 2 * S * HKV * DH * 2 + HQ * DH * 4 * 2 + 4 * n_pages
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def run_decode(steps: int, warmup: int):
+    from orator_amd import decoder_attn as da
+    from orator_amd.runtime import DeviceBuffer, Event, Stream, synchronize
+
+    total_tok = L_BASE + warmup + steps + 1
+    max_pages = (total_tok + PAGE - 1) // PAGE
+    n_pages = B * max_pages
+    pool_elems = n_pages * PAGE * HKV * DH
+    log(f"decode: {LAYERS} layers x B={B} x L={L_BASE}, {max_pages} pages/stream, "
+        f"{2 * LAYERS * pool_elems * 2 / 1e9:.2f} GB of KV")
+
+    rng = np.random.default_rng(1234)
+    # One random block, tiled over every pool with device copies: contents do not change
+    # the traffic, and host generation of 7.8 GB would dominate the run.
+    block = (rng.standard_normal(1 << 22).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    dblock = DeviceBuffer.from_array(block)
+    stream = Stream()
+
+    def filled_pool():
+        buf = DeviceBuffer(pool_elems * 2)
+        off = 0
+        while off < buf.nbytes:
+            n = min(dblock.nbytes, buf.nbytes - off)
+            from orator_amd._lib import call
+            call("orator_memcpy_dtod", buf.ptr + off, dblock.ptr, n, stream.handle)
+            off += n
+        return buf
+
+    kpools = [filled_pool() for _ in range(LAYERS)]
+    vpools = [filled_pool() for _ in range(LAYERS)]
+    stream.synchronize()
+    # page tables: a random permutation of the pool per layer
+    tables = []
+    for _ in range(LAYERS):
+        perm = rng.permutation(n_pages).astype(np.int32).reshape(B, max_pages)
+        tables.append(DeviceBuffer.from_array(perm))
+    n_var = 4
+    qs = [DeviceBuffer.from_array(rng.standard_normal((B, HQ, DH)).astype(np.float32))
+          for _ in range(n_var)]
+    ks = [DeviceBuffer.from_array(rng.standard_normal((B, 1, HKV, DH)).astype(np.float32))
+          for _ in range(n_var)]
+    vs = [DeviceBuffer.from_array(rng.standard_normal((B, 1, HKV, DH)).astype(np.float32))
+          for _ in range(n_var)]
+    outs = DeviceBuffer(B * HQ * DH * 4)
+    n_all = warmup + steps
+    pos_all = (L_BASE + np.arange(n_all, dtype=np.int32))[:, None].repeat(B, 1)
+    dpos = DeviceBuffer.from_array(np.ascontiguousarray(pos_all))
+    scale = 1.0 / math.sqrt(DH)
+
+    def step(t, evs=None):
+        pos_ptr = dpos.ptr + t * B * 4
+        v = t % n_var
+        for l in range(LAYERS):
+            da.WriteKvCachePaged(ks[v], vs[v], kpools[l], vpools[l], tables[l], max_pages, PAGE,
+                                 n_pages, B, 1, HKV, DH, pos_ptr, stream)
+            if evs is not None:
+                evs[l][0].record(stream)
+            da.GqaDecodeAttnPaged(qs[v], kpools[l], vpools[l], tables[l], max_pages, PAGE, pos_ptr,
+                                  outs, B, HQ, HKV, DH, scale, stream)
+            if evs is not None:
+                evs[l][1].record(stream)
+
+    for t in range(warmup):
+        step(t)
+    stream.synchronize()
+    synchronize()
+
+    # ---- whole-job timing: exactly `steps` steps between two device syncs ----
+    e0, e1 = Event(), Event()
+    t_wall0 = time.perf_counter()
+    e0.record(stream)
+    for t in range(warmup, warmup + steps):
+        step(t)
+    e1.record(stream)
+    stream.synchronize()
+    synchronize()
+    wall_s = time.perf_counter() - t_wall0
+    gpu_ms = e0.elapsed_ms(e1)
+    step_bytes = sum(B * decode_bytes(L_BASE + t + 1, (L_BASE + t + 1 + PAGE - 1) // PAGE)
+                     for t in range(warmup, warmup + steps)) * LAYERS
+    elapsed_s = max(wall_s, gpu_ms / 1e3)
+    value_gbs = step_bytes / elapsed_s / 1e9
+
+    # ---- decode kernel launch durations (events on the launch stream) ----
+    n_kstep = min(steps, 16)
+    evs = [(Event(), Event()) for _ in range(LAYERS)]
+    durs, kbytes = [], []
+    for i in range(n_kstep):
+        t = warmup + steps - n_kstep + i
+        step(t, evs)
+        stream.synchronize()
+        S = L_BASE + t + 1
+        for l in range(LAYERS):
+            durs.append(evs[l][0].elapsed_ms(evs[l][1]))
+            kbytes.append(B * decode_bytes(S, (S + PAGE - 1) // PAGE))
+    avg_ms = float(np.mean(durs))
+    achieved = float(np.mean(kbytes)) / (avg_ms / 1e3) / 1e9
+
+    # ---- spot parity of the last launch against the oracle (stream 0..1, layer 27) ----
+    parity = spot_check(kpools[-1], vpools[-1], tables[-1], max_pages, qs, outs,
+                        L_BASE + warmup + steps - 1, (warmup + steps - 1) % n_var, scale)
+    return {
+        "gpu_ms": gpu_ms, "wall_s": wall_s, "ms_per_step": elapsed_s * 1e3 / steps,
+        "value_gbs": value_gbs, "kernel_avg_us": avg_ms * 1e3,
+        "kernel_bytes": float(np.mean(kbytes)), "achieved_gbs": achieved,
+        "max_pages": max_pages, "parity": parity,
+    }
+
+
+def spot_check(kpool, vpool, table, max_pages, qs, outs, last_pos, var, scale):
+    """Recomputes streams 0-1 of the last decode launch with the oracle."""
+    try:
+        sys.path.insert(0, str(ROOT / "tests"))
+        import oracle_lib as orc
+        from helpers import rel_err
+    except Exception as e:  # the oracle is the checker only
+        return {"skipped": str(e)}
+    nb = 2
+    tab = table.download(np.int32, (B, max_pages))[:nb]
+    need = sorted(set(tab[:, : (last_pos + PAGE) // PAGE].ravel().tolist()))
+    page_elems = PAGE * HKV * DH
+    remap = {p: i for i, p in enumerate(need)}
+    kp = np.stack([kpool.download(np.uint16, (page_elems,), p * page_elems * 2) for p in need])
+    vp = np.stack([vpool.download(np.uint16, (page_elems,), p * page_elems * 2) for p in need])
+    kp = kp.reshape(len(need), PAGE, HKV, DH)
+    vp = vp.reshape(len(need), PAGE, HKV, DH)
+    t2 = np.vectorize(lambda p: remap.get(int(p), 0))(tab).astype(np.int32)
+    q = qs[var].download(np.float32, (B, HQ, DH))[:nb]
+    got = outs.download(np.float32, (B, HQ, DH))[:nb]
+    ref = orc.gqa_decode_paged(q, kp, vp, t2, PAGE, np.full(nb, last_pos, np.int32), scale,
+                               threads=min(8, os.cpu_count() or 1))
+    return {"streams": nb, "max_rel_err": rel_err(got, ref, 0.05), "floor": 0.05}
+
+
+def cpu_baseline(seconds: float):
+    """Oracle decode (scalar C, -O2) over one layer of the workload, repeated for a bounded
+    time on the host cores."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as orc
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = max(1, min(16, cores))
+    S = L_BASE + 1
+    max_pages = (S + PAGE - 1) // PAGE
+    n_pages = B * max_pages
+    rng = np.random.default_rng(7)
+    block = (rng.standard_normal(1 << 22).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    pool_elems = n_pages * PAGE * HKV * DH
+    reps = -(-pool_elems // block.size)
+    kp = np.tile(block, reps)[:pool_elems].reshape(n_pages, PAGE, HKV, DH)
+    vp = np.roll(np.tile(block, reps)[:pool_elems], 12345).reshape(n_pages, PAGE, HKV, DH)
+    table = rng.permutation(n_pages).astype(np.int32).reshape(B, max_pages)
+    q = rng.standard_normal((B, HQ, DH)).astype(np.float32)
+    pos = np.full(B, S - 1, np.int32)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        orc.gqa_decode_paged(q, kp, vp, table, PAGE, pos, 1.0 / math.sqrt(DH), threads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 400:
+            break
+    gbs = n * B * decode_bytes(S, max_pages) / el / 1e9
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{n} layer-steps of B={B} paged decode at S={S} "
+                      f"(oracle orc_gqa_decode_paged_mt, {threads} threads, {el:.1f} s, "
+                      f"{cores} cores visible, {model})"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        sys.exit(2)
+    from orator_amd.runtime import device_name
+    log("device:", device_name())
+    dec = run_decode(args.steps, args.warmup)
+    log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value_gbs']:.1f} GB/s; kernel "
+        f"{dec['kernel_avg_us']:.1f} us avg -> {dec['achieved_gbs']:.1f} GB/s; parity {dec['parity']}")
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": "GQA decode-attn HBM GB/s (% peak); prefill-attn TFLOP/s (% MFMA peak)",
+        "value": round(dec["value_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "decode sweep (configs[2]): 28-layer GQA decode, B=16, L=4096, "
+                               "16q/8kv heads, Dh=128, bf16 paged KV (16-token pages), fp32 q/acc",
+                   "layers": LAYERS, "batch": B, "kv_len": L_BASE, "page_size": PAGE,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gqa_decode_kernel", "kernel_avg_us": round(dec["kernel_avg_us"], 2),
+                     "bytes_per_launch": int(dec["kernel_bytes"])},
+        "cpu_baseline": cpu,
+        "parity": dec["parity"],
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

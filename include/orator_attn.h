@@ -1,0 +1,122 @@
+/*
+ * orator_attn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Every entry point takes plain device pointers and sizes, a HIP stream passed as
+ * `void*` (NULL = the default stream) and returns an int status (ORATOR_OK = 0).
+ * On failure orator_last_error() returns a message for the calling thread.
+ *
+ * Conventions carried over from the reference launchers:
+ *   - non-positive sizes are a silent no-op returning ORATOR_OK
+ *     (src/model/asr_ops.cu:201,208,220,227,254,330);
+ *   - launches are asynchronous on the given stream; RopeInterleaved and
+ *     GqaAttention use the default stream, as the reference's do
+ *     (src/model/asr_ops.cu:213,246-247);
+ *   - positions are device-resident ints so a captured graph can replay at any
+ *     position (src/model/asr_text_decoder.cu:60-61,159);
+ *   - the caller owns every buffer; in-place use is allowed where the reference
+ *     allows it (include/model/asr_ops.cuh:23,37).
+ * New here: shapes the kernels do not support, and capacity overruns the host can
+ * see, are rejected before launch with ORATOR_ERR_UNSUPPORTED / _CAPACITY.
+ *
+ * Layouts: q/out [T, Hq, Dh] fp32; k/v [T, Hkv, Dh]; a KV cache is bf16 bits
+ * (uint16_t) [rows, Hkv, Dh].  A paged pool is [n_pages, page_size, Hkv, Dh] with
+ * page_table[b * max_pages + i] naming the page that holds positions
+ * [i*page_size, (i+1)*page_size) of stream b; contiguous pages in order are
+ * exactly the reference layout [max_seq_len, Hkv, Dh]
+ * (src/model/asr_text_decoder.cu:60-77,309-318).
+ */
+#ifndef ORATOR_ATTN_H_
+#define ORATOR_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORATOR_OK 0
+#define ORATOR_ERR_INVALID (-1)     /* bad argument (null pointer, inconsistent sizes)   */
+#define ORATOR_ERR_UNSUPPORTED (-2) /* shape outside what the kernels are built for      */
+#define ORATOR_ERR_CAPACITY (-3)    /* request exceeds a cache / workspace capacity      */
+#define ORATOR_ERR_HIP (-4)         /* HIP runtime error                                  */
+
+/* ---------------------------------------------------------------- runtime ---- */
+/* Message for the last failing call on this thread ("" if none). */
+const char* orator_last_error(void);
+int orator_version(void);
+/* Device plumbing for hosts without their own HIP code (tests, bench).  Mirrors the
+ * reference's gpu runtime (include/gpu/memory.h:26-168, src/gpu/memory.cc:139-147). */
+int orator_device_count(int* count);
+int orator_set_device(int device);
+int orator_device_name(char* buf, int len);
+int orator_malloc(void** ptr, size_t bytes);
+int orator_free(void* ptr);
+int orator_memcpy_htod(void* dst, const void* src, size_t bytes);
+int orator_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int orator_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream);
+int orator_memset(void* ptr, int value, size_t bytes, void* stream);
+int orator_stream_create(void** stream);
+int orator_stream_destroy(void* stream);
+int orator_stream_synchronize(void* stream);
+int orator_device_synchronize(void);
+/* Event timing: creates/records/reads hipEvents on a stream. */
+int orator_event_create(void** event);
+int orator_event_destroy(void* event);
+int orator_event_record(void* event, void* stream);
+int orator_event_elapsed_ms(float* ms, void* start, void* stop);
+/* Pre-sizes the library workspace of `stream` (used by the split-K decode combine)
+ * so that later calls do not allocate, e.g. before hipGraph capture. */
+int orator_workspace_reserve(size_t bytes, void* stream);
+
+/* ------------------------------------------------------- asr_ops family ---- */
+/* asr_ops::RmsNorm (include/model/asr_ops.cuh:21-25; src/model/asr_ops.cu:21-51,199-204).
+ * out[r,d] = x[r,d] * rsqrt(mean_d(x[r,:]^2) + eps) * weight[d]; in-place allowed. */
+int orator_rms_norm(const float* x, const float* weight, float* out, int rows, int dim,
+                    float eps, void* stream);
+/* asr_ops::RopeInterleaved (include/model/asr_ops.cuh:27-34; src/model/asr_ops.cu:57-75,206-216).
+ * Default stream, in place. */
+int orator_rope_interleaved(float* x, const int* positions, int n_tokens, int n_heads,
+                            int head_dim, float theta_base);
+/* asr_ops::SwiGLU (include/model/asr_ops.cuh:36-39; src/model/asr_ops.cu:80-87,218-223). */
+int orator_swiglu(const float* gate, const float* up, float* out, int n, void* stream);
+/* asr_ops::RopeHalf (include/model/asr_ops.cuh:41-48; src/model/asr_ops.cu:92-111,225-235).
+ * rotate_half RoPE in place. */
+int orator_rope_half(float* x, const int* positions, int n_tokens, int n_heads, int head_dim,
+                     float theta_base, void* stream);
+/* asr_ops::ArgmaxBanned (include/model/asr_ops.cuh:58-62; src/model/asr_ops.cu:300-333).
+ * Same tie rule: ties keep the candidate of the lower scan slot. */
+int orator_argmax_banned(const float* logits, int n, int ban0, int ban1, int* out_idx,
+                         void* stream);
+/* asr_gemm::F32ToBf16 / Bf16ToF32 (include/model/asr_gemm.h:23-25; src/model/asr_gemm.cu:45-57). */
+int orator_f32_to_bf16(const float* in, uint16_t* out, long n, void* stream);
+int orator_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream);
+
+/* ------------------------------------------------- decoder KV + attention ---- */
+/* WriteKvCacheKernel (src/model/asr_text_decoder.cu:62-77): cache[pos0 + t] = bf16(k/v[t]),
+ * pos0 read from *d_pos0 on the device.  New: rows at or past `capacity` are not written. */
+int orator_kv_write(const float* k, const float* v, uint16_t* kc, uint16_t* vc, int Tq, int Hkv,
+                    int Dh, const int* d_pos0, int capacity, void* stream);
+/* Paged form: stream b's Tq rows go to positions d_pos0[b] + t through its page-table row.
+ * k/v are [B, Tq, Hkv, Dh]; page indices at or past n_pages are not written. */
+int orator_kv_write_paged(const float* k, const float* v, uint16_t* kpool, uint16_t* vpool,
+                          const int* page_table, int max_pages, int page_size, int n_pages,
+                          int B, int Tq, int Hkv, int Dh, const int* d_pos0, void* stream);
+
+/* GqaDecodeAttnKernel (src/model/asr_text_decoder.cu:149-213, launch :416-418):
+ * q [Hq, Dh] fp32 attends the S = *d_pos + 1 keys of the bf16 cache kc/vc.
+ * `capacity` (the cache's max_seq_len) sizes the split-K grid; S is clamped to it.
+ * Any S is supported (the reference stops at 2048). */
+int orator_gqa_decode(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int Hq,
+                      int Hkv, int Dh, const int* d_pos, int capacity, float scale, void* stream);
+/* Batched paged decode: stream b's q [Hq, Dh] attends d_pos[b] + 1 keys through page-table
+ * row b.  q/out [B, Hq, Dh]. */
+int orator_gqa_decode_paged(const float* q, const uint16_t* kpool, const uint16_t* vpool,
+                            const int* page_table, int max_pages, int page_size,
+                            const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
+                            float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ORATOR_ATTN_H_ */

@@ -1,0 +1,102 @@
+"""Loads liborator_attn.so (the gfx950 HIP library) and declares its C ABI for ctypes.
+
+There is no CPU fallback: if the library was not built, importing the operator modules
+raises.  Device pointers are plain ints.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "liborator_attn.so"
+
+ORATOR_OK = 0
+ORATOR_ERR_INVALID = -1
+ORATOR_ERR_UNSUPPORTED = -2
+ORATOR_ERR_CAPACITY = -3
+ORATOR_ERR_HIP = -4
+
+
+class GpuError(RuntimeError):
+    """A failed launch or HIP call; mirrors the reference's GpuMemoryException
+    (src/gpu/memory.cc:14-21), a std::runtime_error."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+_p = C.c_void_p
+_i = C.c_int
+_l = C.c_long
+_f = C.c_float
+_sz = C.c_size_t
+
+# name -> argument types (all return int status)
+SIGNATURES: dict[str, list] = {
+    # runtime
+    "orator_version": [],
+    "orator_device_count": [C.POINTER(_i)],
+    "orator_set_device": [_i],
+    "orator_device_name": [C.c_char_p, _i],
+    "orator_malloc": [C.POINTER(_p), _sz],
+    "orator_free": [_p],
+    "orator_memcpy_htod": [_p, _p, _sz],
+    "orator_memcpy_dtoh": [_p, _p, _sz],
+    "orator_memcpy_dtod": [_p, _p, _sz, _p],
+    "orator_memset": [_p, _i, _sz, _p],
+    "orator_stream_create": [C.POINTER(_p)],
+    "orator_stream_destroy": [_p],
+    "orator_stream_synchronize": [_p],
+    "orator_device_synchronize": [],
+    "orator_event_create": [C.POINTER(_p)],
+    "orator_event_destroy": [_p],
+    "orator_event_record": [_p, _p],
+    "orator_event_elapsed_ms": [C.POINTER(_f), _p, _p],
+    "orator_workspace_reserve": [_sz, _p],
+    # asr_ops family
+    "orator_rms_norm": [_p, _p, _p, _i, _i, _f, _p],
+    "orator_rope_interleaved": [_p, _p, _i, _i, _i, _f],
+    "orator_swiglu": [_p, _p, _p, _i, _p],
+    "orator_rope_half": [_p, _p, _i, _i, _i, _f, _p],
+    "orator_argmax_banned": [_p, _i, _i, _i, _p, _p],
+    "orator_f32_to_bf16": [_p, _p, _l, _p],
+    "orator_bf16_to_f32": [_p, _p, _l, _p],
+    # decoder KV + attention
+    "orator_kv_write": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _p],
+    "orator_kv_write_paged": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p],
+    "orator_gqa_decode": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
+    "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Returns the loaded library, loading it on first use; raises if it is missing."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `python -m orator_amd.build` "
+                "(the HIP path has no CPU fallback)")
+        handle = C.CDLL(str(LIB_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = _i
+        handle.orator_last_error.argtypes = []
+        handle.orator_last_error.restype = C.c_char_p
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != ORATOR_OK:
+        msg = lib().orator_last_error().decode(errors="replace")
+        raise GpuError(status, msg)
+
+
+def call(name: str, *args) -> None:
+    """Calls an entry point and raises GpuError on a non-zero status."""
+    check(getattr(lib(), name)(*args))

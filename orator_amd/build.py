@@ -1,0 +1,92 @@
+"""Builds the gfx950 HIP library (orator_amd/liborator_attn.so) and the CPU oracle.
+
+Every HIP source under orator_amd/csrc is compiled by hipcc for gfx950 only, with
+packed-fp32 instruction selection disabled, and linked into one shared library whose
+C ABI is declared in include/orator_attn.h.  The build always recompiles (it is the
+"does it build" check); objects go to orator_amd/_build and are not committed.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+OUT_DIR = PKG / "_build"
+LIB = PKG / "liborator_attn.so"
+ORACLE_DIR = ROOT / "oracle"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM_LIB = "/opt/rocm/lib"
+
+COMMON_FLAGS = [
+    "-O3",
+    "-std=c++20",
+    f"--offload-arch={ARCH}",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-I", str(ROOT / "include"),
+    # Packed-fp32 selection is off for all device code (v_pk_*_f32 forms are avoided).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _sources() -> list[Path]:
+    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+
+
+def _compile(src: Path) -> Path:
+    obj = OUT_DIR / (src.name + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature and says so; that line is noise.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    msgs = "\n".join(l for l in (proc.stdout + proc.stderr).splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{msgs}")
+    if msgs.strip():
+        print(msgs, file=sys.stderr)
+    return obj
+
+
+def build_hip(jobs: int | None = None) -> Path:
+    OUT_DIR.mkdir(exist_ok=True)
+    srcs = _sources()
+    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4) // 2))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+           *map(str, objs), f"-Wl,-rpath,{ROCM_LIB}", f"-L{ROCM_LIB}", "-lamdhip64"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> Path:
+    make = shutil.which("make")
+    if make is None:
+        raise RuntimeError("make not found")
+    proc = subprocess.run([make, "-B", "-C", str(ORACLE_DIR)], capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{proc.stdout}{proc.stderr}")
+    return ORACLE_DIR / "liborator_oracle.so"
+
+
+def build_all() -> None:
+    build_oracle()
+    build_hip()
+
+
+if __name__ == "__main__":
+    build_all()
+    print(f"built {LIB}")

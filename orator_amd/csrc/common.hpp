@@ -1,0 +1,94 @@
+// Device-side helpers shared by the gfx950 kernels: bf16 bit conversions, wave64
+// DPP/shuffle reductions and the paged-KV row addressing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace orator_hip {
+
+constexpr int kWave = 64;
+
+// ---- bf16 <-> fp32 (bf16 is the high half of an fp32; RNE on the way down) ----
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+  uint32_t u = __float_as_uint(x);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+// Packs two fp32 into one dword of two RNE bf16 (lo in bits 0..15).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// ---- DPP lane exchanges (gfx9 encodings) ----
+// quad_perm [1,0,3,2] = 0xB1 (xor 1), [2,3,0,1] = 0x4E (xor 2),
+// row_half_mirror = 0x141, row_mirror = 0x140.
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  return v;
+}
+
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  return v;
+}
+
+// All-lane reductions over the full wave64.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Raw v_exp_f32 (2^x); 2^-inf = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---- KV addressing ----
+// A cache is a pool of rows [row][Hkv][Dh].  Paged: absolute position j lives in page
+// page_table[j >> page_shift], row (page << page_shift) | (j & mask).  Contiguous:
+// row j of the stream's own cache.  With an identity page table the two coincide, which
+// is how the reference's [max_seq_len][Hkv][Dh] layout is a special case of the pool.
+struct KvMap {
+  const int* page_table;  // nullptr => contiguous
+  int page_shift;
+  long stream_base;       // element offset of this stream's cache (contiguous only)
+
+  __device__ __forceinline__ long row_offset(int j, int Hkv, int kvh, int dh) const {
+    long row;
+    if (page_table) {
+      const long page = page_table[j >> page_shift];
+      row = (page << page_shift) | (j & ((1 << page_shift) - 1));
+    } else {
+      row = j;
+    }
+    return stream_base + (row * Hkv + kvh) * static_cast<long>(dh);
+  }
+};
+
+}  // namespace orator_hip

@@ -1,0 +1,325 @@
+// Small operators of the asr_ops / asr_gemm family and the decoder's KV write, gfx950.
+//
+// These are memory- or launch-bound; the point of each design is one pass over HBM with
+// wide loads and no idle lanes:
+//  * RmsNorm: one wave64 per row (the reference's 256-thread block left half its
+//    threads idle on the 128-wide QK-norm rows), float4 loads, DPP reduction.
+//  * RoPE: one lane per rotation pair; inv_freq, sin and cos are evaluated in fp64 from
+//    the fp32 exponent and fp32 angle the reference forms, and rounded once.
+//  * ArgmaxBanned keeps the reference's 256-slot strided scan + halving tree, because
+//    its tie rule is part of the observable result.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace orator_hip {
+namespace {
+
+constexpr int kBlock = 256;
+
+inline int blocks_for(long n, int per_block = kBlock) {
+  return static_cast<int>((n + per_block - 1) / per_block);
+}
+
+// ------------------------------------------------------------------ RmsNorm ----
+template <bool VEC>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ w,
+                                                       float* out, int rows, int dim,
+                                                       float eps) {
+#pragma clang fp contract(off)
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* xr = x + static_cast<long>(row) * dim;
+  float* yr = out + static_cast<long>(row) * dim;
+  float local = 0.0f;
+  if (VEC) {
+    for (int d = lane * 4; d < dim; d += 256) {
+      const float4 v = *reinterpret_cast<const float4*>(xr + d);
+      local += v.x * v.x;
+      local += v.y * v.y;
+      local += v.z * v.z;
+      local += v.w * v.w;
+    }
+  } else {
+    for (int d = lane; d < dim; d += 64) local += xr[d] * xr[d];
+  }
+  const float sum = wave_sum(local);
+  const float ms = sum / static_cast<float>(dim) + eps;
+  const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+  if (VEC) {
+    for (int d = lane * 4; d < dim; d += 256) {
+      const float4 v = *reinterpret_cast<const float4*>(xr + d);
+      const float4 g = *reinterpret_cast<const float4*>(w + d);
+      *reinterpret_cast<float4*>(yr + d) =
+          make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+    }
+  } else {
+    for (int d = lane; d < dim; d += 64) yr[d] = xr[d] * inv * w[d];
+  }
+}
+
+// --------------------------------------------------------------------- RoPE ----
+__device__ __forceinline__ void rope_cs(float p, float base, int j, int head_dim, float* c,
+                                        float* s) {
+  const float e = -2.0f * static_cast<float>(j) / static_cast<float>(head_dim);
+  const float inv_freq = static_cast<float>(pow(static_cast<double>(base), static_cast<double>(e)));
+  const float angle = p * inv_freq;
+  double sd, cd;
+  sincos(static_cast<double>(angle), &sd, &cd);
+  *c = static_cast<float>(cd);
+  *s = static_cast<float>(sd);
+}
+
+template <bool HALF>
+__global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x,
+                                                   const int* __restrict__ pos, int T, int H,
+                                                   int Dh, float base) {
+#pragma clang fp contract(off)
+  const int half = Dh / 2;
+  const long idx = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const long total = static_cast<long>(T) * H * half;
+  if (idx >= total) return;
+  const int j = static_cast<int>(idx % half);
+  const long th = idx / half;
+  const int t = static_cast<int>(th / H);
+  float* xr = x + th * Dh;
+  float c, s;
+  rope_cs(static_cast<float>(pos[t]), base, j, Dh, &c, &s);
+  if (HALF) {
+    const float a = xr[j];
+    const float b = xr[j + half];
+    xr[j] = a * c - b * s;
+    xr[j + half] = b * c + a * s;
+  } else {
+    const float a = xr[2 * j];
+    const float b = xr[2 * j + 1];
+    xr[2 * j] = a * c - b * s;
+    xr[2 * j + 1] = a * s + b * c;
+  }
+}
+
+// ------------------------------------------------------------------- SwiGLU ----
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* g, const float* u, float* o,
+                                                     int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float gv = g[i];
+  o[i] = (gv / (1.0f + expf(-gv))) * u[i];
+}
+
+// -------------------------------------------------------------------- casts ----
+__global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ in,
+                                                          uint16_t* __restrict__ out, long n) {
+  const long i = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    const float4 v = *reinterpret_cast<const float4*>(in + i);
+    *reinterpret_cast<uint2*>(out + i) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+  } else {
+    for (long k = i; k < n; ++k) out[k] = f32_to_bf16(in[k]);
+  }
+}
+
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __restrict__ in,
+                                                          float* __restrict__ out, long n) {
+  const long i = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    const uint2 v = *reinterpret_cast<const uint2*>(in + i);
+    *reinterpret_cast<float4*>(out + i) =
+        make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+  } else {
+    for (long k = i; k < n; ++k) out[k] = bf16_to_f32(in[k]);
+  }
+}
+
+// ----------------------------------------------------------- ArgmaxBanned ----
+__global__ __launch_bounds__(256) void argmax_banned_kernel(const float* __restrict__ x, int n,
+                                                            int ban0, int ban1,
+                                                            int* __restrict__ out_idx) {
+  __shared__ float sval[256];
+  __shared__ int sidx[256];
+  float best = -1e30f;
+  int bi = 0;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    if (i == ban0 || i == ban1) continue;
+    const float v = x[i];
+    if (v > best) {
+      best = v;
+      bi = i;
+    }
+  }
+  sval[threadIdx.x] = best;
+  sidx[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s && sval[threadIdx.x + s] > sval[threadIdx.x]) {
+      sval[threadIdx.x] = sval[threadIdx.x + s];
+      sidx[threadIdx.x] = sidx[threadIdx.x + s];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out_idx = sidx[0];
+}
+
+// ----------------------------------------------------------------- KV write ----
+// One lane per 4 elements of one (t, h) row; both K and V rows are converted in the
+// same lane.  Rows at or past the capacity (or with an out-of-range page) are dropped.
+__global__ __launch_bounds__(256) void kv_write_kernel(const float* __restrict__ k,
+                                                       const float* __restrict__ v,
+                                                       uint16_t* __restrict__ kc,
+                                                       uint16_t* __restrict__ vc, int Tq,
+                                                       int Hkv, int Dh,
+                                                       const int* __restrict__ pos0p,
+                                                       int capacity, const int* page_table,
+                                                       int max_pages, int page_shift, int n_pages,
+                                                       int B) {
+  const int q4 = Dh / 4;
+  const long idx = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const long total = static_cast<long>(B) * Tq * Hkv * q4;
+  if (idx >= total) return;
+  const int d = static_cast<int>(idx % q4) * 4;
+  const long row = idx / q4;  // ((b*Tq + t)*Hkv + h)
+  const int h = static_cast<int>(row % Hkv);
+  const long bt = row / Hkv;
+  const int t = static_cast<int>(bt % Tq);
+  const int b = static_cast<int>(bt / Tq);
+  const int p = pos0p[b] + t;
+  long dst_row;
+  if (page_table) {
+    const int pi = p >> page_shift;
+    if (p < 0 || pi >= max_pages) return;
+    const int page = page_table[static_cast<long>(b) * max_pages + pi];
+    if (page < 0 || page >= n_pages) return;
+    dst_row = (static_cast<long>(page) << page_shift) | (p & ((1 << page_shift) - 1));
+  } else {
+    if (p < 0 || p >= capacity) return;
+    dst_row = p;
+  }
+  const long src = row * Dh + d;
+  const long dst = (dst_row * Hkv + h) * Dh + d;
+  const float4 kv = *reinterpret_cast<const float4*>(k + src);
+  const float4 vv = *reinterpret_cast<const float4*>(v + src);
+  *reinterpret_cast<uint2*>(kc + dst) = make_uint2(pack_bf16x2(kv.x, kv.y), pack_bf16x2(kv.z, kv.w));
+  *reinterpret_cast<uint2*>(vc + dst) = make_uint2(pack_bf16x2(vv.x, vv.y), pack_bf16x2(vv.z, vv.w));
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace orator_hip
+
+using namespace orator_hip;
+
+extern "C" {
+
+int orator_rms_norm(const float* x, const float* weight, float* out, int rows, int dim, float eps,
+                    void* stream) {
+  if (rows <= 0 || dim <= 0) return ORATOR_OK;
+  if (!x || !weight || !out) return fail(ORATOR_ERR_INVALID, "rms_norm: null pointer");
+  const bool vec = (dim % 4 == 0) && aligned16(x) && aligned16(weight) && aligned16(out);
+  const dim3 grid(blocks_for(rows, 4));
+  if (vec)
+    hipLaunchKernelGGL(rms_norm_kernel<true>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                       x, weight, out, rows, dim, eps);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel<false>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                       x, weight, out, rows, dim, eps);
+  return check_launch("rms_norm");
+}
+
+int orator_rope_interleaved(float* x, const int* positions, int n_tokens, int n_heads, int head_dim,
+                            float theta_base) {
+  if (n_tokens <= 0 || n_heads <= 0 || head_dim <= 0) return ORATOR_OK;
+  if (!x || !positions) return fail(ORATOR_ERR_INVALID, "rope_interleaved: null pointer");
+  if (head_dim % 2) return fail(ORATOR_ERR_UNSUPPORTED, "rope_interleaved: head_dim must be even");
+  const long total = static_cast<long>(n_tokens) * n_heads * (head_dim / 2);
+  hipLaunchKernelGGL(rope_kernel<false>, dim3(blocks_for(total)), dim3(kBlock), 0, nullptr, x,
+                     positions, n_tokens, n_heads, head_dim, theta_base);
+  return check_launch("rope_interleaved");
+}
+
+int orator_rope_half(float* x, const int* positions, int n_tokens, int n_heads, int head_dim,
+                     float theta_base, void* stream) {
+  if (n_tokens <= 0 || n_heads <= 0 || head_dim <= 0) return ORATOR_OK;
+  if (!x || !positions) return fail(ORATOR_ERR_INVALID, "rope_half: null pointer");
+  if (head_dim % 2) return fail(ORATOR_ERR_UNSUPPORTED, "rope_half: head_dim must be even");
+  const long total = static_cast<long>(n_tokens) * n_heads * (head_dim / 2);
+  hipLaunchKernelGGL(rope_kernel<true>, dim3(blocks_for(total)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), x, positions, n_tokens, n_heads, head_dim,
+                     theta_base);
+  return check_launch("rope_half");
+}
+
+int orator_swiglu(const float* gate, const float* up, float* out, int n, void* stream) {
+  if (n <= 0) return ORATOR_OK;
+  if (!gate || !up || !out) return fail(ORATOR_ERR_INVALID, "swiglu: null pointer");
+  hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(n)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), gate, up, out, n);
+  return check_launch("swiglu");
+}
+
+int orator_f32_to_bf16(const float* in, uint16_t* out, long n, void* stream) {
+  if (n <= 0) return ORATOR_OK;
+  if (!in || !out) return fail(ORATOR_ERR_INVALID, "f32_to_bf16: null pointer");
+  if (!aligned16(in) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(ORATOR_ERR_INVALID, "f32_to_bf16: in must be 16-byte and out 8-byte aligned");
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(blocks_for((n + 3) / 4)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), in, out, n);
+  return check_launch("f32_to_bf16");
+}
+
+int orator_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream) {
+  if (n <= 0) return ORATOR_OK;
+  if (!in || !out) return fail(ORATOR_ERR_INVALID, "bf16_to_f32: null pointer");
+  if ((reinterpret_cast<uintptr_t>(in) & 7u) || !aligned16(out))
+    return fail(ORATOR_ERR_INVALID, "bf16_to_f32: in must be 8-byte and out 16-byte aligned");
+  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(blocks_for((n + 3) / 4)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), in, out, n);
+  return check_launch("bf16_to_f32");
+}
+
+int orator_argmax_banned(const float* logits, int n, int ban0, int ban1, int* out_idx,
+                         void* stream) {
+  if (n <= 0) return ORATOR_OK;
+  if (!logits || !out_idx) return fail(ORATOR_ERR_INVALID, "argmax_banned: null pointer");
+  hipLaunchKernelGGL(argmax_banned_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     logits, n, ban0, ban1, out_idx);
+  return check_launch("argmax_banned");
+}
+
+int orator_kv_write(const float* k, const float* v, uint16_t* kc, uint16_t* vc, int Tq, int Hkv,
+                    int Dh, const int* d_pos0, int capacity, void* stream) {
+  if (Tq <= 0 || Hkv <= 0 || Dh <= 0) return ORATOR_OK;
+  if (!k || !v || !kc || !vc || !d_pos0) return fail(ORATOR_ERR_INVALID, "kv_write: null pointer");
+  if (Dh % 4) return fail(ORATOR_ERR_UNSUPPORTED, "kv_write: Dh must be a multiple of 4");
+  if (!aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(kc) & 7u) ||
+      (reinterpret_cast<uintptr_t>(vc) & 7u))
+    return fail(ORATOR_ERR_INVALID, "kv_write: k/v must be 16-byte and caches 8-byte aligned");
+  const long total = static_cast<long>(Tq) * Hkv * (Dh / 4);
+  hipLaunchKernelGGL(kv_write_kernel, dim3(blocks_for(total)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), k, v, kc, vc, Tq, Hkv, Dh, d_pos0, capacity,
+                     nullptr, 0, 0, 0, 1);
+  return check_launch("kv_write");
+}
+
+int orator_kv_write_paged(const float* k, const float* v, uint16_t* kpool, uint16_t* vpool,
+                          const int* page_table, int max_pages, int page_size, int n_pages, int B,
+                          int Tq, int Hkv, int Dh, const int* d_pos0, void* stream) {
+  if (B <= 0 || Tq <= 0 || Hkv <= 0 || Dh <= 0) return ORATOR_OK;
+  if (!k || !v || !kpool || !vpool || !page_table || !d_pos0)
+    return fail(ORATOR_ERR_INVALID, "kv_write_paged: null pointer");
+  if (Dh % 4) return fail(ORATOR_ERR_UNSUPPORTED, "kv_write_paged: Dh must be a multiple of 4");
+  if (!aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(kpool) & 7u) ||
+      (reinterpret_cast<uintptr_t>(vpool) & 7u))
+    return fail(ORATOR_ERR_INVALID, "kv_write_paged: k/v must be 16-byte and pools 8-byte aligned");
+  const int shift = ilog2_exact(page_size);
+  if (shift < 0 || max_pages <= 0 || n_pages <= 0)
+    return fail(ORATOR_ERR_INVALID, "kv_write_paged: page_size must be a power of two");
+  const long total = static_cast<long>(B) * Tq * Hkv * (Dh / 4);
+  hipLaunchKernelGGL(kv_write_kernel, dim3(blocks_for(total)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), k, v, kpool, vpool, Tq, Hkv, Dh, d_pos0, 0,
+                     page_table, max_pages, shift, n_pages, B);
+  return check_launch("kv_write_paged");
+}
+
+}  // extern "C"

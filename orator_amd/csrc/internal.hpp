@@ -1,0 +1,54 @@
+// Host-side internals shared by the launchers and the C ABI: status codes, the
+// per-thread error message, and the per-(device, stream) workspace used by the
+// split-K decode combine.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/orator_attn.h"
+
+namespace orator_hip {
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const std::string& msg);
+// Maps a HIP error to ORATOR_ERR_HIP (recording where it came from), or ORATOR_OK.
+int check_hip(hipError_t e, const char* what);
+// Checks hipGetLastError() after a launch.
+int check_launch(const char* what);
+
+// Device scratch owned by the library, one block per (device, stream), grown on
+// demand.  The first `counter_bytes` are zeroed when the block is (re)allocated and
+// every kernel that uses them leaves them zero again.  Returns nullptr on failure
+// (the error is recorded).
+void* workspace(hipStream_t stream, size_t bytes, size_t counter_bytes);
+constexpr size_t kCounterBytes = 1u << 18;  // 64 Ki uint32 counters
+
+inline int ilog2_exact(int v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return s;
+}
+
+// ---- launchers (defined in the .hip files) ----
+struct DecodeProblem {
+  const float* q;
+  const uint16_t* kpool;
+  const uint16_t* vpool;
+  const int* page_table;  // nullptr => contiguous caches
+  int max_pages;          // page-table row length (paged)
+  int page_size;          // paged only (power of two >= 16)
+  long stream_stride;     // elements between streams' contiguous caches
+  const int* pos;         // [B] device: stream b attends pos[b]+1 keys
+  float* out;
+  int B, Hq, Hkv, Dh;
+  int capacity;           // max keys any stream can attend (grid sizing)
+  float scale;
+};
+int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
+
+}  // namespace orator_hip

@@ -1,0 +1,174 @@
+// Library runtime: error reporting, the per-(device, stream) workspace and the small
+// device-plumbing surface of the C ABI (allocation, copies, streams, events).
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "internal.hpp"
+
+namespace orator_hip {
+
+namespace {
+thread_local std::string g_last_error;
+
+struct Block {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Block> g_ws;
+}  // namespace
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ORATOR_OK;
+  return fail(ORATOR_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int check_launch(const char* what) { return check_hip(hipGetLastError(), what); }
+
+void* workspace(hipStream_t stream, size_t bytes, size_t counter_bytes) {
+  int dev = 0;
+  if (check_hip(hipGetDevice(&dev), "hipGetDevice") != ORATOR_OK) return nullptr;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  Block& blk = g_ws[{dev, stream}];
+  if (blk.bytes >= bytes) return blk.ptr;
+  if (blk.ptr) {
+    // The old block may still be read by queued work on this stream.
+    if (check_hip(hipStreamSynchronize(stream), "workspace sync") != ORATOR_OK) return nullptr;
+    if (check_hip(hipFree(blk.ptr), "workspace free") != ORATOR_OK) return nullptr;
+    blk = Block{};
+  }
+  void* p = nullptr;
+  if (check_hip(hipMalloc(&p, bytes), "workspace hipMalloc") != ORATOR_OK) return nullptr;
+  if (counter_bytes &&
+      check_hip(hipMemsetAsync(p, 0, counter_bytes, stream), "workspace zero") != ORATOR_OK) {
+    (void)hipFree(p);
+    return nullptr;
+  }
+  blk.ptr = p;
+  blk.bytes = bytes;
+  return p;
+}
+
+}  // namespace orator_hip
+
+using orator_hip::check_hip;
+using orator_hip::fail;
+
+extern "C" {
+
+const char* orator_last_error(void) { return orator_hip::g_last_error.c_str(); }
+
+int orator_version(void) { return 1; }
+
+int orator_device_count(int* count) {
+  if (!count) return fail(ORATOR_ERR_INVALID, "device_count: null");
+  return check_hip(hipGetDeviceCount(count), "hipGetDeviceCount");
+}
+
+int orator_set_device(int device) { return check_hip(hipSetDevice(device), "hipSetDevice"); }
+
+int orator_device_name(char* buf, int len) {
+  if (!buf || len <= 0) return fail(ORATOR_ERR_INVALID, "device_name: bad buffer");
+  int dev = 0;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc) return rc;
+  hipDeviceProp_t prop;
+  rc = check_hip(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+  if (rc) return rc;
+  std::string name = std::string(prop.name) + " (" + prop.gcnArchName + ", " +
+                     std::to_string(prop.multiProcessorCount) + " CUs)";
+  snprintf(buf, static_cast<size_t>(len), "%s", name.c_str());
+  return ORATOR_OK;
+}
+
+int orator_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(ORATOR_ERR_INVALID, "malloc: null");
+  return check_hip(hipMalloc(ptr, bytes ? bytes : 1), "hipMalloc");
+}
+
+int orator_free(void* ptr) { return check_hip(hipFree(ptr), "hipFree"); }
+
+int orator_memcpy_htod(void* dst, const void* src, size_t bytes) {
+  return check_hip(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+}
+
+int orator_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+  return check_hip(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+}
+
+int orator_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream) {
+  return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
+                                  static_cast<hipStream_t>(stream)),
+                   "hipMemcpyAsync D2D");
+}
+
+int orator_memset(void* ptr, int value, size_t bytes, void* stream) {
+  return check_hip(hipMemsetAsync(ptr, value, bytes, static_cast<hipStream_t>(stream)),
+                   "hipMemsetAsync");
+}
+
+int orator_stream_create(void** stream) {
+  if (!stream) return fail(ORATOR_ERR_INVALID, "stream_create: null");
+  hipStream_t s = nullptr;
+  const int rc = check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+  *stream = s;
+  return rc;
+}
+
+int orator_stream_destroy(void* stream) {
+  return check_hip(hipStreamDestroy(static_cast<hipStream_t>(stream)), "hipStreamDestroy");
+}
+
+int orator_stream_synchronize(void* stream) {
+  return check_hip(hipStreamSynchronize(static_cast<hipStream_t>(stream)),
+                   "hipStreamSynchronize");
+}
+
+int orator_device_synchronize(void) {
+  return check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
+}
+
+int orator_event_create(void** event) {
+  if (!event) return fail(ORATOR_ERR_INVALID, "event_create: null");
+  hipEvent_t e = nullptr;
+  const int rc = check_hip(hipEventCreate(&e), "hipEventCreate");
+  *event = e;
+  return rc;
+}
+
+int orator_event_destroy(void* event) {
+  return check_hip(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+}
+
+int orator_event_record(void* event, void* stream) {
+  return check_hip(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)),
+                   "hipEventRecord");
+}
+
+int orator_event_elapsed_ms(float* ms, void* start, void* stop) {
+  if (!ms) return fail(ORATOR_ERR_INVALID, "event_elapsed: null");
+  const int rc = check_hip(hipEventSynchronize(static_cast<hipEvent_t>(stop)), "hipEventSynchronize");
+  if (rc) return rc;
+  return check_hip(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                                       static_cast<hipEvent_t>(stop)),
+                   "hipEventElapsedTime");
+}
+
+int orator_workspace_reserve(size_t bytes, void* stream) {
+  const size_t total = bytes + orator_hip::kCounterBytes;
+  return orator_hip::workspace(static_cast<hipStream_t>(stream), total,
+                               orator_hip::kCounterBytes)
+             ? ORATOR_OK
+             : ORATOR_ERR_HIP;
+}
+
+}  // extern "C"

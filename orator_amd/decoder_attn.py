@@ -1,0 +1,42 @@
+"""The text decoder's KV-cache write and attention launchers over the HIP library.
+
+The reference keeps these kernels file-static inside src/model/asr_text_decoder.cu
+(WriteKvCacheKernel :62-77, GqaCacheAttnKernel :88-142, GqaDecodeAttnKernel :149-213);
+the functions here take the same arguments as those kernels' launches (:412-418,
+:534-541), plus the cache capacity the host already knows (AsrTextConfig.max_seq_len).
+Paged variants add a page table; with contiguous in-order pages they address exactly the
+reference layout [max_seq_len, Hkv, Dh].
+"""
+from __future__ import annotations
+
+from ._lib import call
+from .runtime import _sh, ptr
+
+
+def WriteKvCache(k, v, kc, vc, Tq: int, Hkv: int, Dh: int, d_pos0, capacity: int,
+                 stream=None) -> None:
+    """cache[pos0 + t] = bf16_rne(k/v[t]); pos0 = *d_pos0 on the device."""
+    call("orator_kv_write", ptr(k), ptr(v), ptr(kc), ptr(vc), Tq, Hkv, Dh, ptr(d_pos0), capacity,
+         _sh(stream))
+
+
+def WriteKvCachePaged(k, v, kpool, vpool, page_table, max_pages: int, page_size: int,
+                      n_pages: int, B: int, Tq: int, Hkv: int, Dh: int, d_pos0,
+                      stream=None) -> None:
+    call("orator_kv_write_paged", ptr(k), ptr(v), ptr(kpool), ptr(vpool), ptr(page_table),
+         max_pages, page_size, n_pages, B, Tq, Hkv, Dh, ptr(d_pos0), _sh(stream))
+
+
+def GqaDecodeAttn(q, kc, vc, out, Hq: int, Hkv: int, Dh: int, d_pos, capacity: int,
+                  scale: float, stream=None) -> None:
+    """q [Hq, Dh] attends the S = *d_pos + 1 cached keys."""
+    call("orator_gqa_decode", ptr(q), ptr(kc), ptr(vc), ptr(out), Hq, Hkv, Dh, ptr(d_pos),
+         capacity, scale, _sh(stream))
+
+
+def GqaDecodeAttnPaged(q, kpool, vpool, page_table, max_pages: int, page_size: int, d_pos,
+                       out, B: int, Hq: int, Hkv: int, Dh: int, scale: float,
+                       stream=None) -> None:
+    """Stream b's q [Hq, Dh] attends d_pos[b] + 1 keys through page-table row b."""
+    call("orator_gqa_decode_paged", ptr(q), ptr(kpool), ptr(vpool), ptr(page_table), max_pages,
+         page_size, ptr(d_pos), ptr(out), B, Hq, Hkv, Dh, scale, _sh(stream))

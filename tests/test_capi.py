@@ -1,0 +1,81 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point declared in
+include/orator_attn.h, and rejects bad arguments before any launch."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from orator_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_symbols() -> list[str]:
+    names = []
+    for h in (ROOT / "include").glob("*.h"):
+        text = h.read_text()
+        names += re.findall(r"^(?:int|const char\*)\s+(orator_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_symbols()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_signatures_cover_header():
+    names = set(declared_symbols()) - {"orator_last_error"}
+    assert names == set(_lib.SIGNATURES), names ^ set(_lib.SIGNATURES)
+
+
+def test_version():
+    assert _lib.lib().orator_version() >= 1
+
+
+# Validation runs before any HIP call, so these work without a device.
+FAKE = 0x1000  # never dereferenced: every call below is rejected first
+
+
+def test_nonpositive_sizes_are_noops():
+    lib = _lib.lib()
+    assert lib.orator_rms_norm(None, None, None, 0, 128, 1e-6, None) == _lib.ORATOR_OK
+    assert lib.orator_swiglu(None, None, None, 0, None) == _lib.ORATOR_OK
+    assert lib.orator_rope_half(None, None, 0, 16, 128, 1e6, None) == _lib.ORATOR_OK
+    assert lib.orator_gqa_decode(None, None, None, None, 0, 8, 128, None, 16, 0.1,
+                                 None) == _lib.ORATOR_OK
+    assert lib.orator_kv_write(None, None, None, None, 0, 8, 128, None, 16,
+                               None) == _lib.ORATOR_OK
+
+
+def test_null_pointers_rejected():
+    lib = _lib.lib()
+    rc = lib.orator_rms_norm(None, FAKE, FAKE, 4, 128, 1e-6, None)
+    assert rc == _lib.ORATOR_ERR_INVALID
+    assert b"null" in lib.orator_last_error()
+
+
+def test_unsupported_decode_shapes_rejected():
+    lib = _lib.lib()
+    args = (FAKE, FAKE, FAKE, FAKE)
+    # Dh = 96 is not built
+    assert lib.orator_gqa_decode(*args, 16, 8, 96, FAKE, 64, 0.1, None) == _lib.ORATOR_ERR_UNSUPPORTED
+    # Hq not a multiple of Hkv
+    assert lib.orator_gqa_decode(*args, 12, 8, 128, FAKE, 64, 0.1, None) == _lib.ORATOR_ERR_INVALID
+    # group size 8 is not built
+    assert lib.orator_gqa_decode(*args, 64, 8, 128, FAKE, 64, 0.1, None) == _lib.ORATOR_ERR_UNSUPPORTED
+    # paged: page size must be a power of two >= 16
+    assert lib.orator_gqa_decode_paged(FAKE, FAKE, FAKE, FAKE, 8, 24, FAKE, FAKE, 1, 16, 8, 128,
+                                       0.1, None) == _lib.ORATOR_ERR_INVALID
+
+
+def test_python_wrapper_raises_gpu_error():
+    from orator_amd import asr_ops
+    with pytest.raises(_lib.GpuError) as e:
+        asr_ops.RmsNorm(None, FAKE, FAKE, 4, 128, 1e-6)
+    assert e.value.code == _lib.ORATOR_ERR_INVALID

@@ -1,0 +1,163 @@
+"""GPU parity: split-K decode attention (contiguous and paged) and the KV write against the
+oracle.  Bar: fp32 q / bf16 KV / fp32 accumulate, so the fp32-mode tolerance applies:
+max |g - r| / max(|r|, 0.05) <= 1e-4 (0.05 = 5% of the unit-scale V), and bit-exact bf16
+for the KV write."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from gpu_helpers import down, empty, say, up
+from helpers import SplitMix64, rel_err
+from orator_amd import decoder_attn as da
+
+pytestmark = pytest.mark.gpu
+
+FLOOR = 0.05
+TOL = 1e-4
+
+
+def _contig_case(seed, S, cap, Hq=16, Hkv=8, Dh=128):
+    r = SplitMix64(seed)
+    k, v = r.normal((S, Hkv, Dh)), r.normal((S, Hkv, Dh))
+    kc = np.zeros((cap, Hkv, Dh), np.uint16)
+    vc = np.zeros_like(kc)
+    orc.kv_write(k, v, kc, vc, 0)
+    q = r.normal((Hq, Dh))
+    return q, kc, vc
+
+
+@pytest.mark.parametrize("S,cap", [(1, 64), (2, 64), (64, 64), (65, 128), (257, 512),
+                                   (513, 2048), (2048, 2048), (3001, 4096), (4097, 4224)])
+def test_decode_contiguous_matches_oracle(S, cap):
+    Hq, Hkv, Dh = 16, 8, 128
+    q, kc, vc = _contig_case(100 + S, S, cap)
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_decode(q, kc, vc, S - 1, scale)
+    dq, dk, dv = up(q), up(kc), up(vc)
+    dpos = up(np.array([S - 1], np.int32))
+    dout = empty((Hq, Dh), np.float32)
+    say("decode contiguous", S, cap)
+    da.GqaDecodeAttn(dq, dk, dv, dout, Hq, Hkv, Dh, dpos, cap, scale)
+    got = down(dout, (Hq, Dh))
+    assert rel_err(got, ref, FLOOR) <= TOL
+    if S == 1:  # a single key: the output is v0 of the group's kv head
+        np.testing.assert_allclose(got, np.repeat(orc.from_bf16(vc[0]), 2, axis=0), atol=1e-7)
+
+
+@pytest.mark.parametrize("Hq,Hkv,Dh", [(8, 8, 128), (16, 4, 128), (8, 4, 64), (4, 4, 64)])
+def test_decode_group_and_headdim_variants(Hq, Hkv, Dh):
+    S, cap = 777, 1024
+    q, kc, vc = _contig_case(7, S, cap, Hq, Hkv, Dh)
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_decode(q, kc, vc, S - 1, scale)
+    dout = empty((Hq, Dh), np.float32)
+    say("decode variant", Hq, Hkv, Dh)
+    da.GqaDecodeAttn(up(q), up(kc), up(vc), dout, Hq, Hkv, Dh, up(np.array([S - 1], np.int32)),
+                     cap, scale)
+    assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL
+
+
+def test_decode_back_to_back_calls_reuse_combine_state():
+    """The split combine's counters must be left at zero: run several positions in a row
+    on the same cache and check every result."""
+    Hq, Hkv, Dh, cap = 16, 8, 128, 2048
+    q, kc, vc = _contig_case(9, cap, cap)
+    dq, dk, dv = up(q), up(kc), up(vc)
+    dout = empty((Hq, Dh), np.float32)
+    for pos in (2047, 100, 1500, 63, 2047):
+        say("decode repeat", pos)
+        da.GqaDecodeAttn(dq, dk, dv, dout, Hq, Hkv, Dh, up(np.array([pos], np.int32)), cap,
+                         0.08838834764831845)
+        ref = orc.gqa_decode(q, kc, vc, pos, 0.08838834764831845)
+        assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL, pos
+
+
+def test_decode_position_past_capacity_is_clamped():
+    Hq, Hkv, Dh, cap = 16, 8, 128, 256
+    q, kc, vc = _contig_case(10, cap, cap)
+    dout = empty((Hq, Dh), np.float32)
+    say("decode clamp")
+    da.GqaDecodeAttn(up(q), up(kc), up(vc), dout, Hq, Hkv, Dh, up(np.array([5000], np.int32)), cap,
+                     0.1)
+    ref = orc.gqa_decode(q, kc, vc, cap - 1, 0.1)
+    assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL
+
+
+def _paged_case(seed, lens, Hq=16, Hkv=8, Dh=128, ps=16, spare_pages=3):
+    r = SplitMix64(seed)
+    B = len(lens)
+    max_pages = max((n + ps - 1) // ps for n in lens)
+    n_pages = B * max_pages + spare_pages
+    kp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    vp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    perm = np.array(r.uniform(n_pages).argsort(), np.int32)
+    table = perm[:B * max_pages].reshape(B, max_pages).copy()
+    q = r.normal((B, Hq, Dh))
+    pos = np.array(lens, np.int32) - 1
+    return q, kp, vp, table, pos
+
+
+@pytest.mark.parametrize("lens", [[1], [4097], [1025, 2049, 17, 4097, 640, 1, 3333, 2000],
+                                  [4096 + 1] * 16])
+def test_decode_paged_ragged_streams(lens):
+    Hq, Hkv, Dh, ps = 16, 8, 128, 16
+    q, kp, vp, table, pos = _paged_case(sum(lens), lens)
+    B, max_pages = table.shape
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_decode_paged(q, kp, vp, table, ps, pos, scale, threads=8)
+    dout = empty((B, Hq, Dh), np.float32)
+    say("decode paged", lens[:4], len(lens))
+    da.GqaDecodeAttnPaged(up(q), up(kp), up(vp), up(table), max_pages, ps, up(pos), dout, B, Hq,
+                          Hkv, Dh, scale)
+    assert rel_err(down(dout, (B, Hq, Dh)), ref, FLOOR) <= TOL
+
+
+def test_decode_paged_equals_contiguous_for_identity_table():
+    Hq, Hkv, Dh, ps, S = 16, 8, 128, 16, 1000
+    q, kc, vc = _contig_case(12, S, 1024)
+    table = np.arange(1024 // ps, dtype=np.int32)[None, :]
+    dpos = up(np.array([S - 1], np.int32))
+    o1, o2 = empty((Hq, Dh), np.float32), empty((Hq, Dh), np.float32)
+    dq, dk, dv = up(q), up(kc), up(vc)
+    say("decode paged identity")
+    da.GqaDecodeAttn(dq, dk, dv, o1, Hq, Hkv, Dh, dpos, 1024, 0.1)
+    da.GqaDecodeAttnPaged(dq, dk, dv, up(table), table.shape[1], ps, dpos, o2, 1, Hq, Hkv, Dh, 0.1)
+    np.testing.assert_array_equal(down(o1, (Hq, Dh)), down(o2, (Hq, Dh)))
+
+
+def test_kv_write_bit_exact():
+    r = SplitMix64(13)
+    Tq, Hkv, Dh, cap, pos0 = 7, 8, 128, 32, 20
+    k, v = r.normal((Tq, Hkv, Dh)), r.normal((Tq, Hkv, Dh))
+    kc = np.zeros((cap, Hkv, Dh), np.uint16)
+    vc = np.zeros_like(kc)
+    orc.kv_write(k[:cap - pos0], v[:cap - pos0], kc, vc, pos0)  # rows past capacity dropped
+    dkc, dvc = up(np.zeros_like(kc)), up(np.zeros_like(vc))
+    say("kv_write")
+    da.WriteKvCache(up(k), up(v), dkc, dvc, Tq, Hkv, Dh, up(np.array([pos0], np.int32)), cap)
+    np.testing.assert_array_equal(down(dkc, kc.shape, np.uint16), kc)
+    np.testing.assert_array_equal(down(dvc, vc.shape, np.uint16), vc)
+
+
+def test_kv_write_paged_bit_exact():
+    r = SplitMix64(14)
+    B, Tq, Hkv, Dh, ps, max_pages = 3, 5, 8, 128, 16, 4
+    n_pages = B * max_pages
+    table = np.array(r.uniform(n_pages).argsort(), np.int32).reshape(B, max_pages)
+    pos0 = np.array([0, 14, 59], np.int32)
+    k, v = r.normal((B, Tq, Hkv, Dh)), r.normal((B, Tq, Hkv, Dh))
+    kp = np.zeros((n_pages, ps, Hkv, Dh), np.uint16)
+    vp = np.zeros_like(kp)
+    for b in range(B):
+        n = min(Tq, max_pages * ps - int(pos0[b]))
+        orc.kv_write_paged(k[b, :n], v[b, :n], kp, vp, table[b], ps, int(pos0[b]))
+    dkp, dvp = up(np.zeros_like(kp)), up(np.zeros_like(vp))
+    say("kv_write_paged")
+    da.WriteKvCachePaged(up(k), up(v), dkp, dvp, up(table), max_pages, ps, n_pages, B, Tq, Hkv, Dh,
+                         up(pos0))
+    np.testing.assert_array_equal(down(dkp, kp.shape, np.uint16), kp)
+    np.testing.assert_array_equal(down(dvp, vp.shape, np.uint16), vp)

@@ -1,0 +1,100 @@
+"""GPU parity for the asr_ops family: the reference's own fixtures (tests/golden, with the
+reference test's tolerances) and the oracle on seeded inputs."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from gpu_helpers import down, empty, say, up
+from helpers import SplitMix64, rel_err
+from orator_amd import asr_ops
+
+pytestmark = pytest.mark.gpu
+
+
+def test_rmsnorm_fixture_and_oracle(golden):
+    x, w = golden["rmsnorm_x"], golden["rmsnorm_w"]
+    rows, dim = x.shape
+    dout = empty(x.shape, np.float32)
+    say("rmsnorm fixture")
+    asr_ops.RmsNorm(up(x), up(w), dout, rows, dim, 1e-6)
+    got = down(dout, x.shape)
+    assert np.max(np.abs(got - golden["rmsnorm_out"])) < 1e-4  # test_asr_ops.cc:93
+    assert rel_err(got, orc.rms_norm(x, w, 1e-6), 1e-3) < 1e-5
+
+
+@pytest.mark.parametrize("rows,dim", [(16 * 503, 128), (8, 128), (3, 2048), (5, 130)])
+def test_rmsnorm_qk_shapes_in_place(rows, dim):
+    r = SplitMix64(rows + dim)
+    x, w = r.normal((rows, dim)), r.normal((dim,))
+    dx = up(x)
+    say("rmsnorm", rows, dim)
+    asr_ops.RmsNorm(dx, up(w), dx, rows, dim, 1e-6)  # in place, as the decoder calls it
+    assert rel_err(down(dx, x.shape), orc.rms_norm(x, w, 1e-6), 1e-3) < 1e-5
+
+
+def test_rope_interleaved_fixture(golden):
+    x, pos = golden["rope_x"], golden["rope_pos"]
+    T, H, Dh = x.shape
+    dx = up(x)
+    say("rope interleaved fixture")
+    asr_ops.RopeInterleaved(dx, up(pos), T, H, Dh, 1e6)
+    got = down(dx, x.shape)
+    assert np.max(np.abs(got - golden["rope_out"])) < 1e-4  # test_asr_ops.cc:118
+    assert np.max(np.abs(got - orc.rope_interleaved(x, pos, 1e6))) < 1e-6
+
+
+@pytest.mark.parametrize("p0,T,H", [(0, 503, 16), (4096, 3, 8), (100000, 2, 8)])
+def test_rope_half_vs_oracle(p0, T, H):
+    r = SplitMix64(p0 + T)
+    Dh = 128
+    x = r.normal((T, H, Dh))
+    pos = np.arange(p0, p0 + T, dtype=np.int32)
+    dx = up(x)
+    say("rope half", p0, T, H)
+    asr_ops.RopeHalf(dx, up(pos), T, H, Dh, 1e6)
+    got = down(dx, x.shape)
+    # same fp32 angle, sin/cos rounded once from fp64: equal up to rare double roundings
+    assert np.max(np.abs(got - orc.rope_half(x, pos, 1e6))) < 1e-6
+
+
+def test_swiglu_fixture(golden):
+    g, u = golden["swiglu_gate"], golden["swiglu_up"]
+    dout = empty(g.shape, np.float32)
+    say("swiglu")
+    asr_ops.SwiGLU(up(g), up(u), dout, g.size)
+    assert np.max(np.abs(down(dout, g.shape) - golden["swiglu_out"])) < 1e-5  # :141
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 1001, 1 << 20])
+def test_bf16_casts_bit_exact(n):
+    r = SplitMix64(n)
+    x = r.normal((n,), 3.0)
+    db = empty((n,), np.uint16)
+    say("f32_to_bf16", n)
+    asr_ops.F32ToBf16(up(x), db, n)
+    bits = down(db, (n,), np.uint16)
+    np.testing.assert_array_equal(bits, orc.to_bf16(x))
+    df = empty((n,), np.float32)
+    asr_ops.Bf16ToF32(db, df, n)
+    np.testing.assert_array_equal(down(df, (n,)), orc.from_bf16(bits))
+
+
+def _argmax_gpu(x, b0=-1, b1=-1):
+    di = empty((1,), np.int32)
+    asr_ops.ArgmaxBanned(up(x), x.size, b0, b1, di)
+    return int(down(di, (1,), np.int32)[0])
+
+
+def test_argmax_banned_random_and_ties():
+    r = SplitMix64(77)
+    x = r.normal((151936,))
+    top = np.argsort(-x)
+    say("argmax")
+    assert _argmax_gpu(x) == orc.argmax_banned(x) == int(top[0])
+    assert _argmax_gpu(x, int(top[0]), int(top[1])) == int(top[2])
+    for idx in ([2, 258], [1, 2], [1, 3], [130, 2], [5, 5 + 256 * 7, 99]):
+        y = np.zeros(1000, np.float32)
+        y[idx] = 5.0
+        assert _argmax_gpu(y) == orc.argmax_banned(y), idx

@@ -1,0 +1,424 @@
+"""Pins the CPU oracle (oracle/orator_oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something that does not restate its own code:
+the reference's fixture recipe replayed with torch (tests/golden), torch library
+routines (SDPA, bf16 casts), fp64 closed forms, and invariants a wrong sign / index /
+transposition would break.  CPU only.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle_lib as orc
+from helpers import SplitMix64, rel_err
+
+# ------------------------------------------------------------------------ bf16 ----
+
+
+def test_bf16_known_answers():
+    cases = {
+        1.0: 0x3F80,
+        -2.0: 0xC000,
+        # halfway cases round to even
+        float(np.frombuffer(np.uint32(0x3F808000).tobytes(), np.float32)[0]): 0x3F80,
+        float(np.frombuffer(np.uint32(0x3F818000).tobytes(), np.float32)[0]): 0x3F82,
+        # just above halfway rounds up
+        float(np.frombuffer(np.uint32(0x3F808001).tobytes(), np.float32)[0]): 0x3F81,
+        0.0: 0x0000,
+        float("inf"): 0x7F80,
+    }
+    for x, bits in cases.items():
+        assert orc.lib().orc_f32_to_bf16(x) == bits, (x, hex(bits))
+    assert orc.lib().orc_bf16_to_f32(0x3F80) == 1.0
+
+
+def test_bf16_matches_torch_rne():
+    r = SplitMix64(11)
+    x = np.concatenate([
+        r.normal((4096,)),
+        r.normal((1024,), 1e-30),   # subnormal range of fp32 -> bf16
+        r.normal((1024,), 1e30),
+        np.array([65504.0, -3.3895314e38, 1e-45], np.float32),
+    ]).astype(np.float32)
+    ours = orc.to_bf16(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(ours, ref)
+    back = orc.from_bf16(ours)
+    np.testing.assert_array_equal(back, torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+
+
+# --------------------------------------------------------------------- RMSNorm ----
+
+
+def test_rmsnorm_reference_fixture(golden):
+    out = orc.rms_norm(golden["rmsnorm_x"], golden["rmsnorm_w"], 1e-6)
+    assert np.max(np.abs(out - golden["rmsnorm_out"])) < 1e-4  # test_asr_ops.cc:93
+    assert np.max(np.abs(out - golden["rmsnorm_out"])) < 2e-6
+
+
+def test_rmsnorm_invariants():
+    r = SplitMix64(12)
+    x = r.normal((16, 128))
+    w = r.normal((128,))
+    y = orc.rms_norm(x, w, 1e-6)
+    # closed form in fp64
+    ref = x.astype(np.float64) / np.sqrt((x.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6)
+    assert rel_err(y, ref * w, 0.05) < 5e-5
+    # scale invariance (eps negligible)
+    np.testing.assert_allclose(orc.rms_norm(8.0 * x, w, 1e-12), orc.rms_norm(x, w, 1e-12),
+                               rtol=2e-6, atol=1e-7)
+    # constant row c: y = w * sign(c) / sqrt(1 + eps / c^2)
+    c = np.full((2, 128), [[0.5], [-3.0]], np.float32)
+    yc = orc.rms_norm(c, w, 1e-6)
+    expect = w[None, :] * np.sign(c) / np.sqrt(1.0 + 1e-6 / c.astype(np.float64) ** 2)
+    np.testing.assert_allclose(yc, expect, rtol=2e-7, atol=0)
+
+
+# ------------------------------------------------------------------------ RoPE ----
+
+
+def test_rope_interleaved_reference_fixture(golden):
+    out = orc.rope_interleaved(golden["rope_x"], golden["rope_pos"], 1e6)
+    assert np.max(np.abs(out - golden["rope_out"])) < 1e-4  # test_asr_ops.cc:118
+    assert np.max(np.abs(out - golden["rope_out"])) < 2e-6
+
+
+def _hf_rotate_half(x, pos, base, Dh):
+    """HF Qwen3 rotary: x*cos + rotate_half(x)*sin, angle formed as fp32 pos*inv_freq
+    (the reference's fp32 angle), cos/sin and the rest in fp64."""
+    i = torch.arange(Dh // 2, dtype=torch.float64)
+    inv = torch.pow(torch.tensor(base, dtype=torch.float64), -2.0 * i / Dh).float()
+    ang = (torch.from_numpy(pos).float()[:, None] * inv[None, :]).double()
+    emb = torch.cat([ang, ang], dim=-1)[:, None, :]
+    xt = torch.from_numpy(x).double()
+    x1, x2 = xt[..., : Dh // 2], xt[..., Dh // 2:]
+    rot = torch.cat([-x2, x1], dim=-1)
+    return (xt * emb.cos() + rot * emb.sin()).numpy()
+
+
+@pytest.mark.parametrize("p0", [0, 500, 4090])
+def test_rope_half_matches_hf_formula(p0):
+    r = SplitMix64(13 + p0)
+    T, H, Dh = 6, 3, 128
+    x = r.normal((T, H, Dh))
+    pos = np.arange(p0, p0 + T, dtype=np.int32)
+    ours = orc.rope_half(x, pos, 1e6)
+    ref = _hf_rotate_half(x, pos, 1e6, Dh)
+    assert np.max(np.abs(ours - ref)) < 3e-6
+
+
+def test_rope_half_invariants():
+    r = SplitMix64(14)
+    T, H, Dh = 8, 2, 128
+    x = r.normal((T, H, Dh))
+    # position 0 is the identity
+    np.testing.assert_array_equal(orc.rope_half(x, np.zeros(T, np.int32), 1e6), x)
+    pos = np.arange(T, dtype=np.int32) * 37
+    y = orc.rope_half(x, pos, 1e6).astype(np.float64)
+    xd = x.astype(np.float64)
+    # each (j, j+64) pair keeps its norm
+    n_in = xd[..., :64] ** 2 + xd[..., 64:] ** 2
+    n_out = y[..., :64] ** 2 + y[..., 64:] ** 2
+    np.testing.assert_allclose(n_out, n_in, rtol=1e-5, atol=1e-6)
+    # q.k depends on the position difference only
+    q, k = r.normal((1, 1, Dh)), r.normal((1, 1, Dh))
+    d1 = float((orc.rope_half(q, np.array([10], np.int32), 1e6) *
+                orc.rope_half(k, np.array([7], np.int32), 1e6)).sum())
+    d2 = float((orc.rope_half(q, np.array([110], np.int32), 1e6) *
+                orc.rope_half(k, np.array([107], np.int32), 1e6)).sum())
+    assert abs(d1 - d2) < 1e-4 * max(1.0, abs(d1))
+
+
+# ---------------------------------------------------------------------- SwiGLU ----
+
+
+def test_swiglu_reference_fixture(golden):
+    out = orc.swiglu(golden["swiglu_gate"], golden["swiglu_up"])
+    assert np.max(np.abs(out - golden["swiglu_out"])) < 1e-5  # test_asr_ops.cc:141
+
+
+# ----------------------------------------------------------------- GQA (fp32) ----
+
+
+def test_gqa_attention_reference_fixture(golden):
+    T, Dh = 24, 128
+    out = orc.gqa_attention(golden["gqa_q"], golden["gqa_k"], golden["gqa_v"],
+                            1.0 / math.sqrt(Dh), True)
+    assert np.max(np.abs(out - golden["gqa_out"])) < 5e-4  # test_asr_ops.cc:167
+    assert np.max(np.abs(out - golden["gqa_out"])) < 2e-6
+    truth = orc.attention_f64(golden["gqa_q"], golden["gqa_k"], golden["gqa_v"],
+                              1.0 / math.sqrt(Dh), True)
+    assert rel_err(out, truth, 0.05) < 5e-5
+
+
+def test_gqa_attention_noncausal_vs_sdpa():
+    r = SplitMix64(15)
+    T, Hq, Hkv, Dh = 19, 4, 2, 64
+    q, k, v = r.normal((T, Hq, Dh)), r.normal((T, Hkv, Dh)), r.normal((T, Hkv, Dh))
+    out = orc.gqa_attention(q, k, v, 0.125, False)
+    qt = torch.from_numpy(q).double().permute(1, 0, 2)
+    kt = torch.from_numpy(k).double().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)
+    vt = torch.from_numpy(v).double().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)
+    ref = F.scaled_dot_product_attention(qt, kt, vt, scale=0.125).permute(1, 0, 2).numpy()
+    assert rel_err(out, ref, 0.05) < 5e-5
+
+
+# ----------------------------------------------------------- KV cache + a5/a6 ----
+
+
+def _cache(r, S, Hkv, Dh, cap=None):
+    cap = cap or S
+    k, v = r.normal((S, Hkv, Dh)), r.normal((S, Hkv, Dh))
+    kc = np.zeros((cap, Hkv, Dh), np.uint16)
+    vc = np.zeros((cap, Hkv, Dh), np.uint16)
+    orc.kv_write(k, v, kc, vc, 0)
+    return k, v, kc, vc
+
+
+def test_kv_write_bit_exact_and_offset():
+    r = SplitMix64(16)
+    k, v = r.normal((5, 8, 128)), r.normal((5, 8, 128))
+    kc = np.zeros((20, 8, 128), np.uint16)
+    vc = np.zeros((20, 8, 128), np.uint16)
+    orc.kv_write(k, v, kc, vc, 7)
+    tk = torch.from_numpy(k).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    tv = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(kc[7:12], tk)
+    np.testing.assert_array_equal(vc[7:12], tv)
+    assert not kc[:7].any() and not kc[12:].any()
+
+
+def test_kv_write_paged_identity_and_permuted():
+    r = SplitMix64(17)
+    S, Hkv, Dh, ps = 64, 2, 64, 16
+    k, v = r.normal((S, Hkv, Dh)), r.normal((S, Hkv, Dh))
+    kc = np.zeros((S, Hkv, Dh), np.uint16)
+    vc = np.zeros_like(kc)
+    orc.kv_write(k, v, kc, vc, 0)
+    kp = np.zeros((S // ps, ps, Hkv, Dh), np.uint16)
+    vp = np.zeros_like(kp)
+    orc.kv_write_paged(k, v, kp, vp, np.arange(S // ps), ps, 0)
+    np.testing.assert_array_equal(kp.reshape(S, Hkv, Dh), kc)
+    perm = np.array([2, 0, 3, 1], np.int32)
+    kp2 = np.zeros_like(kp)
+    vp2 = np.zeros_like(vp)
+    orc.kv_write_paged(k, v, kp2, vp2, perm, ps, 0)
+    for i, p in enumerate(perm):
+        np.testing.assert_array_equal(kp2[p], kc[i * ps:(i + 1) * ps])
+        np.testing.assert_array_equal(vp2[p], vc[i * ps:(i + 1) * ps])
+
+
+def _sdpa_cache(q, kc, vc, pos0, scale):
+    """torch SDPA (fp64) over the bf16-decoded cache; query row t sees keys [0, pos0+t]."""
+    Tq, Hq, Dh = q.shape
+    Hkv = kc.shape[1]
+    S = pos0 + Tq
+    kf = torch.from_numpy(orc.from_bf16(kc[:S])).double().permute(1, 0, 2)
+    vf = torch.from_numpy(orc.from_bf16(vc[:S])).double().permute(1, 0, 2)
+    kf = kf.repeat_interleave(Hq // Hkv, 0)
+    vf = vf.repeat_interleave(Hq // Hkv, 0)
+    qt = torch.from_numpy(q).double().permute(1, 0, 2)
+    mask = torch.arange(S)[None, :] <= (pos0 + torch.arange(Tq))[:, None]
+    out = F.scaled_dot_product_attention(qt, kf, vf, attn_mask=mask, scale=scale)
+    return out.permute(1, 0, 2).numpy()
+
+
+@pytest.mark.parametrize("pos0,Tq", [(0, 37), (29, 11)])
+def test_prefill_vs_sdpa(pos0, Tq):
+    r = SplitMix64(18 + pos0)
+    Hq, Hkv, Dh = 16, 8, 128
+    _, _, kc, vc = _cache(r, pos0 + Tq, Hkv, Dh)
+    q = r.normal((Tq, Hq, Dh))
+    scale = 1.0 / math.sqrt(Dh)
+    out = orc.gqa_prefill(q, kc, vc, pos0, scale)
+    assert rel_err(out, _sdpa_cache(q, kc, vc, pos0, scale), 0.05) < 5e-5
+
+
+def test_prefill_special_cases():
+    r = SplitMix64(19)
+    Hq, Hkv, Dh = 4, 2, 64
+    # S = 1: the output is v0 exactly
+    _, _, kc, vc = _cache(r, 1, Hkv, Dh)
+    q = r.normal((1, Hq, Dh))
+    out = orc.gqa_prefill(q, kc, vc, 0, 0.125)
+    expect = np.repeat(orc.from_bf16(vc[0]), Hq // Hkv, axis=0)
+    np.testing.assert_array_equal(out[0], expect)
+    # identical keys: uniform weights, output = mean(V) over the attended rows
+    S = 9
+    kc = np.repeat(kc[:1], S, axis=0)
+    vc = orc.to_bf16(r.normal((S, Hkv, Dh)))
+    q = r.normal((1, Hq, Dh))
+    out = orc.gqa_prefill(q, kc, vc, S - 1, 0.125)
+    mean = orc.from_bf16(vc).astype(np.float64).mean(0)
+    np.testing.assert_allclose(out[0], np.repeat(mean, Hq // Hkv, axis=0), rtol=0, atol=2e-6)
+
+
+def test_split_prefill_equivalence():
+    r = SplitMix64(20)
+    T, split, Hq, Hkv, Dh = 40, 13, 16, 8, 128
+    _, _, kc, vc = _cache(r, T, Hkv, Dh)
+    q = r.normal((T, Hq, Dh))
+    full = orc.gqa_prefill(q, kc, vc, 0, 0.088)
+    a = orc.gqa_prefill(q[:split], kc, vc, 0, 0.088)
+    b = orc.gqa_prefill(q[split:], kc, vc, split, 0.088)
+    np.testing.assert_array_equal(np.concatenate([a, b]), full)
+    mt = orc.gqa_prefill(q, kc, vc, 0, 0.088, threads=3)
+    np.testing.assert_array_equal(mt, full)
+
+
+def test_decode_is_last_prefill_row_and_fp64():
+    r = SplitMix64(21)
+    S, Hq, Hkv, Dh = 513, 16, 8, 128
+    _, _, kc, vc = _cache(r, S, Hkv, Dh)
+    q = r.normal((Hq, Dh))
+    scale = 1.0 / math.sqrt(Dh)
+    dec = orc.gqa_decode(q, kc, vc, S - 1, scale)
+    pre = orc.gqa_prefill(q[None], kc, vc, S - 1, scale)[0]
+    assert rel_err(dec, pre, 0.05) < 5e-5
+    truth = orc.attention_f64(q[None], orc.from_bf16(kc), orc.from_bf16(vc), scale, True,
+                              kv_off=S - 1)[0]
+    assert rel_err(dec, truth, 0.05) < 5e-5
+
+
+def test_decode_paged_permutation_invariance():
+    r = SplitMix64(22)
+    B, Hq, Hkv, Dh, ps, npages = 2, 8, 4, 64, 16, 12
+    pos = np.array([150, 77], np.int32)
+    kp = orc.to_bf16(r.normal((npages * B, ps, Hkv, Dh)))
+    vp = orc.to_bf16(r.normal((npages * B, ps, Hkv, Dh)))
+    table = np.arange(B * npages, dtype=np.int32).reshape(B, npages)
+    q = r.normal((B, Hq, Dh))
+    base = orc.gqa_decode_paged(q, kp, vp, table, ps, pos, 0.125)
+    # contiguous view of stream 0 = pages 0..npages-1 in order
+    c0 = orc.gqa_decode(q[0], kp[:npages].reshape(-1, Hkv, Dh), vp[:npages].reshape(-1, Hkv, Dh),
+                        int(pos[0]), 0.125)
+    np.testing.assert_array_equal(base[0], c0)
+    # move the pages of both streams somewhere else and permute the table alike
+    perm = np.array(SplitMix64(5).uniform(B * npages).argsort(), np.int32)
+    kp2, vp2 = np.empty_like(kp), np.empty_like(vp)
+    kp2[perm] = kp
+    vp2[perm] = vp
+    out = orc.gqa_decode_paged(q, kp2, vp2, perm[table], ps, pos, 0.125)
+    np.testing.assert_array_equal(out, base)
+    mt = orc.gqa_decode_paged(q, kp2, vp2, perm[table], ps, pos, 0.125, threads=4)
+    np.testing.assert_array_equal(mt, base)
+
+
+# ---------------------------------------------------------------- Conformer ----
+
+
+def test_relshift_closed_form():
+    for T in (1, 2, 3, 7, 717):
+        idx = range(T) if T < 100 else range(0, T, 37)
+        for i in idx:
+            for j in idx:
+                row, m = orc.relshift_column(T, i, j)
+                assert (row, m) == (i, T - 1 - i + j), (T, i, j)
+
+
+def test_pos_emb_closed_form():
+    T, D = 23, 512
+    pe = orc.build_pos_emb(T, D).astype(np.float64)
+    pos = (T - 1 - np.arange(2 * T - 1))[:, None].astype(np.float64)
+    div = np.exp(-math.log(10000.0) * np.arange(0, D, 2) / D)[None, :]
+    np.testing.assert_allclose(pe[:, 0::2], np.sin(pos * div), atol=2e-5)
+    np.testing.assert_allclose(pe[:, 1::2], np.cos(pos * div), atol=2e-5)
+
+
+def _relpos_inputs(r, T, H, Dk):
+    return (r.normal((T, H, Dk)), r.normal((T, H, Dk)), r.normal((T, H, Dk)),
+            r.normal((2 * T - 1, H, Dk)), r.normal((H, Dk), 0.3), r.normal((H, Dk), 0.3))
+
+
+@pytest.mark.parametrize("T,valid", [(31, 31), (40, 29)])
+def test_relpos_vs_closed_form_fp64(T, valid):
+    r = SplitMix64(23 + T)
+    H, Dk = 4, 64
+    q, k, v, p, u, vb = _relpos_inputs(r, T, H, Dk)
+    out = orc.relpos_attention(q, k, v, p, u, vb, valid, 0.125)
+    truth = orc.relpos_attention_f64(q, k, v, p, u, vb, valid, 0.125)
+    assert rel_err(out, truth, 0.05) < 5e-5
+
+
+def test_relpos_reduces_to_mha_and_masks_keys():
+    r = SplitMix64(24)
+    T, H, Dk = 33, 2, 64
+    q, k, v, p, u, vb = _relpos_inputs(r, T, H, Dk)
+    z = np.zeros_like
+    out = orc.relpos_attention(q, k, v, z(p), z(u), z(vb), T, 0.125)
+    qt, kt, vt = (torch.from_numpy(a).double().permute(1, 0, 2) for a in (q, k, v))
+    ref = F.scaled_dot_product_attention(qt, kt, vt, scale=0.125).permute(1, 0, 2).numpy()
+    assert rel_err(out, ref, 0.05) < 5e-5
+    valid = 20
+    a = orc.relpos_attention(q, k, v, p, u, vb, valid, 0.125)
+    k2, v2 = k.copy(), v.copy()
+    k2[valid:] = r.normal(k2[valid:].shape)
+    v2[valid:] = r.normal(v2[valid:].shape)
+    b = orc.relpos_attention(q, k2, v2, p, u, vb, valid, 0.125)
+    np.testing.assert_array_equal(a, b)
+
+
+# ------------------------------------------------------------------ SGEMM ----
+
+
+@pytest.mark.parametrize("rows,inner,cols,batch", [(13, 64, 13, 8), (14, 64, 14, 8)])
+def test_sgemm_batched_reference_pattern(rows, inner, cols, batch):
+    # test/unit/model/test_gemm_batched.cu:12-61: index%17/17 and index%13/13 inputs
+    a = (np.arange(batch * rows * inner) % 17 / 17.0).astype(np.float32).reshape(batch, rows, inner)
+    w = (np.arange(batch * cols * inner) % 13 / 13.0).astype(np.float32).reshape(batch, cols, inner)
+    out = orc.sgemm_batched(a, w)
+    ref = np.einsum("bmk,bnk->bmn", a.astype(np.float64), w.astype(np.float64))
+    assert np.max(np.abs(out - ref)) < 1e-4
+
+
+def test_sgemm_bias_act():
+    r = SplitMix64(25)
+    a, w, bias = r.normal((7, 48)), r.normal((9, 48)), r.normal((9,))
+    pre = a.astype(np.float64) @ w.astype(np.float64).T + bias
+    acts = {0: pre, 1: pre / (1 + np.exp(-pre)), 2: np.maximum(pre, 0), 3: 1 / (1 + np.exp(-pre))}
+    for act, ref in acts.items():
+        assert rel_err(orc.sgemm(a, w, bias, act), ref, 0.05) < 5e-5, act
+
+
+# ----------------------------------------------------------------- argmax ----
+
+
+def test_argmax_banned_matches_numpy():
+    r = SplitMix64(26)
+    x = r.normal((151936,))
+    top = np.argsort(-x)
+    assert orc.argmax_banned(x) == int(top[0])
+    assert orc.argmax_banned(x, int(top[0])) == int(top[1])
+    assert orc.argmax_banned(x, int(top[1]), int(top[0])) == int(top[2])
+
+
+def test_argmax_tie_rule():
+    """Hand-worked cases of the 256-slot scan + halving tree (src/model/asr_ops.cu:306-322):
+    at level s slot t takes slot t+s only when strictly greater."""
+    n = 1000
+    x = np.zeros(n, np.float32)
+    # tie inside one slot (2 and 258 are both slot 2): the strict '>' scan keeps 2
+    x[[2, 258]] = 5.0
+    assert orc.argmax_banned(x) == 2
+    # tie between slot 1 (index 1) and slot 2 (index 2): at s=2 slot 0 takes slot 2
+    # (5 > 0); at s=1 slot 1 (5) is not > slot 0 (5) -> 2, although index 1 is lower
+    x[:] = 0
+    x[[1, 2]] = 5.0
+    assert orc.argmax_banned(x) == 2
+    assert int(np.argmax(x)) == 1  # what a first-index argmax would say
+    # tie between slot 1 (index 1) and slot 3 (index 3): at s=2 slot 1 keeps 1 against
+    # slot 3; at s=1 slot 0 (value 0) takes slot 1 -> 1
+    x[:] = 0
+    x[[1, 3]] = 5.0
+    assert orc.argmax_banned(x) == 1
+    # slot 130 meets slot 2 at level 128 and loses the tie -> 2
+    x[:] = 0
+    x[[130, 2]] = 5.0
+    assert orc.argmax_banned(x) == 2
+    # everything -inf: no slot ever updates, the reference returns index 0
+    assert orc.argmax_banned(np.full(4, -np.inf, np.float32)) == 0
