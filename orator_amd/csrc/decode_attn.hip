@@ -3,24 +3,29 @@
 // Replaces GqaDecodeAttnKernel (src/model/asr_text_decoder.cu:149-213): one fp32 query
 // per q-head attends S = pos+1 cached keys.  Semantics kept: fp32 q, bf16 K/V widened
 // exactly, fp32 accumulation, scores scaled after the dot, softmax normalised by
-// multiplying with 1/sum.  The exponent is taken base 2 on scores pre-multiplied by
+// multiplying with 1/sum.  Exponents are taken base 2 on scores pre-multiplied by
 // log2(e) (same value up to fp32 rounding).
 //
-// Design (memory-bound, ~2 flop/byte):
-//  * one workgroup = (split of SPLIT keys, kv head, stream); 4 wave64s, each owning a
-//    contiguous quarter of the split.  Both (all G) q heads of the GQA group consume
-//    every K/V row the workgroup loads, so K/V are read from HBM exactly once.
-//  * QK phase, "quad" layout: 4 lanes per key, each lane 4 x 16-byte loads covering 32
-//    of the 128 dims; a quad's 4 loads of one instruction are one contiguous 64-byte
-//    segment of the row.  The 4-lane dot reduction is two DPP quad_perm adds.
-//  * scores stay in registers; workgroup max and sum go through LDS; probabilities are
-//    written to LDS for the PV phase.
-//  * PV phase, "row" layout: Dh/8 lanes per key, one 16-byte load each, so every load
-//    instruction reads whole contiguous K/V rows; per-lane accumulators hold 8 dims x G
-//    heads, reduced across rows with lane shuffles and across waves through LDS.
-//  * split combine: each workgroup stores (acc, max, sum); the last one to finish for
-//    its (stream, kv head) -- found with a device-scope counter that it resets -- merges
-//    the splits in the same launch.
+// Design (HBM-bound, ~2 flop/byte):
+//  * one workgroup = (split of SPLIT keys, kv head, stream), 4 wave64s; each wave streams
+//    a contiguous quarter of the split in 32-key chunks.  All G q heads of the GQA group
+//    consume every K/V row the wave loads, so K/V leave HBM exactly once.
+//  * software pipeline: the K and V loads of chunk c+1 are issued before chunk c is
+//    computed, so every wave keeps 16 KB in flight while it does arithmetic.
+//  * QK, "octet" layout: 8 lanes per key, each lane 2 x 16-byte loads (one contiguous
+//    128-byte half row per instruction and octet); dot reduced with 3 DPP steps.
+//  * online softmax per wave (running max / sum, accumulator rescale once per chunk);
+//    probabilities move to the PV layout with one lane shuffle per key row.
+//  * PV, "row" layout: Dh/8 lanes per key, one 16-byte load each (whole contiguous rows
+//    per instruction); per-lane accumulators hold 8 dims x G heads.
+//  * waves merge in LDS at the end; splits are merged by a second small kernel.  (A
+//    last-workgroup merge in the same launch needs a device-scope release fence per
+//    workgroup -- an L2 write-back on gfx950 -- and measured 7-10x slower.)
+//  * paged KV: the split's page rows are resolved once into LDS, so no K/V load waits
+//    on a page-table load.
+#include <stdlib.h>
+#include <string.h>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -36,7 +41,6 @@ struct DecodeArgs {
   float* out;
   float* part_o;       // [B*Hq][max_splits][DH]
   float* part_ml;      // [B*Hq][max_splits][2]
-  unsigned* counters;  // [B*Hkv], zero between launches
   long stream_stride;
   int max_pages;
   int page_shift;
@@ -46,21 +50,144 @@ struct DecodeArgs {
   float scale_log2e;
 };
 
-template <int DH, int G, int SPLIT>
-__global__ __launch_bounds__(256) void gqa_decode_kernel(DecodeArgs a) {
-  constexpr int NW = 4;
-  constexpr int TPW = SPLIT / NW;   // keys per wave
-  constexpr int C = DH / 32;        // 32-dim chunks in the quad layout
-  constexpr int NI = TPW / 16;      // QK iterations, 16 keys each
-  constexpr int LPT = DH / 8;       // lanes per key in the row layout
-  constexpr int TPI = kWave / LPT;  // keys per PV iteration
-  constexpr int NI2 = TPW / TPI;
-  static_assert(TPW % 16 == 0 && TPW % TPI == 0, "split must cover whole iterations");
+template <int DH>
+struct Chunk {
+  static constexpr int CH = 32;             // keys per chunk
+  static constexpr int NCQ = DH / 64;       // 16-byte loads per lane per key (octet layout)
+  static constexpr int NIQ = CH / 8;        // octet iterations per chunk
+  static constexpr int LPT = DH / 8;        // lanes per key, row layout
+  static constexpr int TPI = kWave / LPT;   // keys per row-layout instruction
+  static constexpr int NIV = CH / TPI;      // row-layout instructions per chunk
+  uint4 k[NIQ][NCQ];
+  uint4 v[NIV];
+};
 
-  __shared__ float p_lds[G][SPLIT];
+// Loads one 32-key chunk starting at absolute key c (rows resolved through row_lds).
+template <int DH>
+__device__ __forceinline__ void load_chunk(Chunk<DH>& ch, const uint16_t* kbase,
+                                           const uint16_t* vbase, const int* row_lds, long rs,
+                                           int c, int t0, int end, int lane) {
+  using CK = Chunk<DH>;
+  const int g0 = (c - t0) >> 4;
+  const long rb0 = row_lds[g0];
+  const long rb1 = row_lds[g0 + 1];
+  const int o = lane & 7;
+#pragma unroll
+  for (int i = 0; i < CK::NIQ; ++i) {
+    const int kk = 8 * i + (lane >> 3);  // key within the chunk
+    const long row = (kk < 16 ? rb0 : rb1) + (kk & 15);
+    const uint16_t* src = kbase + row * rs + 8 * o;
+    if (c + kk < end) {
+#pragma unroll
+      for (int cc = 0; cc < CK::NCQ; ++cc) ch.k[i][cc] = load_nt(src + 64 * cc);
+    } else {
+#pragma unroll
+      for (int cc = 0; cc < CK::NCQ; ++cc) ch.k[i][cc] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  const int dg = lane % CK::LPT;
+  const int r = lane / CK::LPT;
+#pragma unroll
+  for (int i = 0; i < CK::NIV; ++i) {
+    const int kk = CK::TPI * i + r;
+    const long row = (kk < 16 ? rb0 : rb1) + (kk & 15);
+    ch.v[i] = c + kk < end ? load_nt(vbase + row * rs + 8 * dg) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Scores, online-softmax update and PV accumulation for one resident chunk at key c.
+template <int DH, int G>
+__device__ __forceinline__ void process_chunk(const Chunk<DH>& cur,
+                                              const float (&qr)[G][Chunk<DH>::NCQ][8],
+                                              float (&m)[G], float (&lpart)[G],
+                                              float (&acc)[G][8], int c, int end, int lane,
+                                              float scale_log2e) {
+  using CK = Chunk<DH>;
+  // scores, octet layout
+  float s[CK::NIQ][G];
+#pragma unroll
+  for (int i = 0; i < CK::NIQ; ++i) {
+    float d[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) d[g] = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < CK::NCQ; ++cc) {
+      const uint32_t w[4] = {cur.k[i][cc].x, cur.k[i][cc].y, cur.k[i][cc].z, cur.k[i][cc].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float klo = bf16_lo(w[e]);
+        const float khi = bf16_hi(w[e]);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          d[g] = fmaf(qr[g][cc][2 * e], klo, d[g]);
+          d[g] = fmaf(qr[g][cc][2 * e + 1], khi, d[g]);
+        }
+      }
+    }
+    const bool valid = c + 8 * i + (lane >> 3) < end;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float dot = d[g];
+      dot += dpp<0xB1>(dot);
+      dot += dpp<0x4E>(dot);
+      dot += dpp<0x141>(dot);
+      s[i][g] = valid ? dot * scale_log2e : -INFINITY;
+    }
+  }
+  // online softmax update (one rescale per chunk)
+  float pk[CK::NIQ][G];
+  const int o = lane & 7;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float cm = s[0][g];
+#pragma unroll
+    for (int i = 1; i < CK::NIQ; ++i) cm = fmaxf(cm, s[i][g]);
+    cm = fmaxf(cm, __shfl_xor(cm, 8));
+    cm = fmaxf(cm, __shfl_xor(cm, 16));
+    cm = fmaxf(cm, __shfl_xor(cm, 32));
+    const float mn = fmaxf(m[g], cm);
+    const float corr = fast_exp2(m[g] - mn);
+    m[g] = mn;
+    float ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CK::NIQ; ++i) {
+      pk[i][g] = fast_exp2(s[i][g] - mn);
+      ps += pk[i][g];
+    }
+    lpart[g] = lpart[g] * corr + (o == 0 ? ps : 0.0f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] *= corr;
+  }
+  // PV, row layout: the probability of key row r comes from its octet by a lane shuffle
+  const int r = lane / CK::LPT;
+#pragma unroll
+  for (int i = 0; i < CK::NIV; ++i) {
+    const int src = 8 * ((CK::TPI * i + r) & 7);
+    const uint32_t w[4] = {cur.v[i].x, cur.v[i].y, cur.v[i].z, cur.v[i].w};
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float p = __shfl(pk[(CK::TPI * i) >> 3][g], src);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[g][2 * e] = fmaf(p, bf16_lo(w[e]), acc[g][2 * e]);
+        acc[g][2 * e + 1] = fmaf(p, bf16_hi(w[e]), acc[g][2 * e + 1]);
+      }
+    }
+  }
+}
+
+template <int DH, int G, int SPLIT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gqa_decode_kernel(
+    DecodeArgs a) {
+  using CK = Chunk<DH>;
+  constexpr int NW = 4;
+  constexpr int TPW = SPLIT / NW;  // keys per wave
+  constexpr int NG = SPLIT / 16;   // 16-key groups per split
+  static_assert(TPW % CK::CH == 0, "a wave covers whole chunks");
+
   __shared__ float red_o[NW][G][DH];
-  __shared__ float red_ml[NW][G];
-  __shared__ int s_last;
+  __shared__ float red_ml[NW][G][2];
+  __shared__ int row_lds[NG];
 
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
@@ -81,154 +208,86 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(DecodeArgs a) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int Hq = a.Hkv * G;
-  const KvMap map{a.page_table ? a.page_table + static_cast<long>(b) * a.max_pages : nullptr,
-                  a.page_shift, a.page_table ? 0 : static_cast<long>(b) * a.stream_stride};
 
-  // ---- q of the G heads, quad layout: lane owns dims 32c + 8*k4 + e ----
-  const int k4 = lane & 3;
-  float qr[G][C][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float* qh = a.q + (static_cast<long>(b) * Hq + kvh * G + g) * DH + 8 * k4;
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const float4 x0 = *reinterpret_cast<const float4*>(qh + 32 * c);
-      const float4 x1 = *reinterpret_cast<const float4*>(qh + 32 * c + 4);
-      qr[g][c][0] = x0.x; qr[g][c][1] = x0.y; qr[g][c][2] = x0.z; qr[g][c][3] = x0.w;
-      qr[g][c][4] = x1.x; qr[g][c][5] = x1.y; qr[g][c][6] = x1.z; qr[g][c][7] = x1.w;
+  // ---- first pool row of every 16-key group of the split (pages hold >= 16 aligned keys) ----
+  if (tid < NG) {
+    const int j0 = t0 + 16 * tid;
+    int row = j0;
+    if (a.page_table && j0 < S) {
+      const int page = a.page_table[static_cast<long>(b) * a.max_pages + (j0 >> a.page_shift)];
+      row = (page << a.page_shift) | (j0 & ((1 << a.page_shift) - 1));
     }
+    row_lds[tid] = row;
   }
 
-  // ---- phase 1: scores (base-2 scaled) ----
-  const int wbase = wave * TPW;
-  uint4 kreg[NI][C];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int j = t0 + wbase + 16 * i + (lane >> 2);
-    if (j < S) {
-      const uint16_t* row = a.kpool + map.row_offset(j, a.Hkv, kvh, DH) + 8 * k4;
-#pragma unroll
-      for (int c = 0; c < C; ++c) kreg[i][c] = *reinterpret_cast<const uint4*>(row + 32 * c);
-    } else {
-#pragma unroll
-      for (int c = 0; c < C; ++c) kreg[i][c] = make_uint4(0, 0, 0, 0);
-    }
-  }
-  float s[NI][G];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    float d[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) d[g] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const uint32_t w[4] = {kreg[i][c].x, kreg[i][c].y, kreg[i][c].z, kreg[i][c].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float klo = bf16_lo(w[e]);
-        const float khi = bf16_hi(w[e]);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          d[g] = fmaf(qr[g][c][2 * e], klo, d[g]);
-          d[g] = fmaf(qr[g][c][2 * e + 1], khi, d[g]);
-        }
-      }
-    }
-    const bool valid = t0 + wbase + 16 * i + (lane >> 2) < S;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float dot = quad_sum(d[g]);
-      s[i][g] = valid ? dot * a.scale_log2e : -INFINITY;
-    }
-  }
-
-  // ---- workgroup max ----
-  float M[G];
+  // ---- q of the G heads, octet layout: lane owns dims 64*cc + 8*o + e ----
+  const int o = lane & 7;
+  float qr[G][CK::NCQ][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float m = s[0][g];
+    const float* qh = a.q + (static_cast<long>(b) * Hq + kvh * G + g) * DH + 8 * o;
 #pragma unroll
-    for (int i = 1; i < NI; ++i) m = fmaxf(m, s[i][g]);
-    m = wave_max(m);
-    if (lane == 0) red_ml[wave][g] = m;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = red_ml[0][g];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) m = fmaxf(m, red_ml[w][g]);
-    M[g] = m;
+    for (int cc = 0; cc < CK::NCQ; ++cc) {
+      const float4 x0 = *reinterpret_cast<const float4*>(qh + 64 * cc);
+      const float4 x1 = *reinterpret_cast<const float4*>(qh + 64 * cc + 4);
+      qr[g][cc][0] = x0.x; qr[g][cc][1] = x0.y; qr[g][cc][2] = x0.z; qr[g][cc][3] = x0.w;
+      qr[g][cc][4] = x1.x; qr[g][cc][5] = x1.y; qr[g][cc][6] = x1.z; qr[g][cc][7] = x1.w;
+    }
   }
   __syncthreads();
 
-  // ---- probabilities -> LDS, workgroup sum ----
-  float lsum[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) lsum[g] = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float p = fast_exp2(s[i][g] - M[g]);
-      if (k4 == 0) {
-        p_lds[g][wbase + 16 * i + (lane >> 2)] = p;
-        lsum[g] += p;
-      }
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float l = wave_sum(lsum[g]);
-    if (lane == 0) red_ml[wave][g] = l;
-  }
-  __syncthreads();
-  float L[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float l = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) l += red_ml[w][g];
-    L[g] = l;
-  }
+  const long kv_base = (a.page_table ? 0 : static_cast<long>(b) * a.stream_stride) +
+                       static_cast<long>(kvh) * DH;
+  const uint16_t* kbase = a.kpool + kv_base;
+  const uint16_t* vbase = a.vpool + kv_base;
+  const long rs = static_cast<long>(a.Hkv) * DH;  // elements per pool row
+  const int w0 = t0 + wave * TPW;
+  const int w1 = min(w0 + TPW, S);
 
-  // ---- phase 2: PV, row layout ----
-  const int dg = lane % LPT;
-  const int r = lane / LPT;
-  uint4 vreg[NI2];
+  float m[G], lpart[G], acc[G][8];
 #pragma unroll
-  for (int i = 0; i < NI2; ++i) {
-    const int j = t0 + wbase + TPI * i + r;
-    vreg[i] = j < S ? *reinterpret_cast<const uint4*>(a.vpool + map.row_offset(j, a.Hkv, kvh, DH) +
-                                                     8 * dg)
-                    : make_uint4(0, 0, 0, 0);
-  }
-  float acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    lpart[g] = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NI2; ++i) {
-    const int lt = wbase + TPI * i + r;
-    const uint32_t w[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float p = p_lds[g][lt];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[g][2 * e] = fmaf(p, bf16_lo(w[e]), acc[g][2 * e]);
-        acc[g][2 * e + 1] = fmaf(p, bf16_hi(w[e]), acc[g][2 * e + 1]);
-      }
+  }
+  const int r = lane / CK::LPT;
+
+  if (w0 < w1) {
+    // Ping-pong buffers: the loads of one chunk are in flight while the other is computed.
+    CK A, Bb;
+    load_chunk<DH>(A, kbase, vbase, row_lds, rs, w0, t0, w1, lane);
+    int c = w0;
+    while (true) {
+      if (c + CK::CH < w1) load_chunk<DH>(Bb, kbase, vbase, row_lds, rs, c + CK::CH, t0, w1, lane);
+      process_chunk<DH, G>(A, qr, m, lpart, acc, c, w1, lane, a.scale_log2e);
+      c += CK::CH;
+      if (c >= w1) break;
+      if (c + CK::CH < w1) load_chunk<DH>(A, kbase, vbase, row_lds, rs, c + CK::CH, t0, w1, lane);
+      process_chunk<DH, G>(Bb, qr, m, lpart, acc, c, w1, lane, a.scale_log2e);
+      c += CK::CH;
+      if (c >= w1) break;
     }
   }
+
+  // ---- wave partials -> LDS ----
 #pragma unroll
-  for (int off = LPT; off < kWave; off <<= 1)
+  for (int off = CK::LPT; off < kWave; off <<= 1)
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float l = wave_sum(lpart[g]);
+    if (lane == 0) {
+      red_ml[wave][g][0] = m[g];
+      red_ml[wave][g][1] = l;
+    }
+  }
   if (r == 0) {
+    const int dg = lane % CK::LPT;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float4* dst = reinterpret_cast<float4*>(&red_o[wave][g][8 * dg]);
@@ -238,68 +297,112 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(DecodeArgs a) {
   }
   __syncthreads();
 
+  // ---- merge the 4 waves; write the split partial (or the output if it is the only split) ----
   for (int idx = tid; idx < G * DH; idx += 256) {
     const int g = idx / DH;
     const int d = idx % DH;
-    float o = red_o[0][g][d];
+    float mx = red_ml[0][g][0];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) o += red_o[w][g][d];
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, red_ml[w][g][0]);
+    float ov = 0.0f, lv = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = fast_exp2(red_ml[w][g][0] - mx);  // idle waves: 2^-inf = 0
+      ov = fmaf(wt, red_o[w][g][d], ov);
+      lv = fmaf(wt, red_ml[w][g][1], lv);
+    }
     const long bh = static_cast<long>(b) * Hq + kvh * G + g;
     if (n_splits == 1) {
-      a.out[bh * DH + d] = o * (1.0f / L[g]);
+      a.out[bh * DH + d] = ov * (1.0f / lv);
     } else {
       const long ps = bh * a.max_splits + split;
-      a.part_o[ps * DH + d] = o;
+      a.part_o[ps * DH + d] = ov;
       if (d == 0) {
-        a.part_ml[ps * 2] = M[g];
-        a.part_ml[ps * 2 + 1] = L[g];
+        a.part_ml[ps * 2] = mx;
+        a.part_ml[ps * 2 + 1] = lv;
       }
     }
   }
-  if (n_splits == 1) return;
+}
 
-  // ---- split combine by the last workgroup of this (stream, kv head) ----
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned old = atomicAdd(&a.counters[b * a.Hkv + kvh], 1u);
-    s_last = (old == static_cast<unsigned>(n_splits - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  for (int idx = tid; idx < G * DH; idx += 256) {
-    const int g = idx / DH;
-    const int d = idx % DH;
-    const long bh = static_cast<long>(b) * Hq + kvh * G + g;
-    const long base = bh * a.max_splits;
+// Split merge: one workgroup per (stream, q head), after the split kernel.  Wave 0
+// turns the split maxima/sums into normalised weights (one per split, in LDS); then every
+// thread sums its output dims over the splits with independent loads.
+template <int DH>
+__global__ __launch_bounds__(128) void gqa_decode_combine_kernel(DecodeArgs a, int split_len,
+                                                                 int Hq) {
+  __shared__ float wsp[1024];
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  int S = a.pos[b] + 1;
+  if (S > a.capacity) S = a.capacity;
+  const int n_splits = (S + split_len - 1) / split_len;
+  if (n_splits <= 1) return;  // written directly by the split kernel
+  const long bh = static_cast<long>(b) * Hq + h;
+  const long base = bh * a.max_splits;
+  const int tid = threadIdx.x;
+  if (tid < 64) {
     float mx = -INFINITY;
-    for (int sp = 0; sp < n_splits; ++sp) mx = fmaxf(mx, a.part_ml[(base + sp) * 2]);
-    float num = 0.0f, den = 0.0f;
-    for (int sp = 0; sp < n_splits; ++sp) {
+    for (int sp = tid; sp < n_splits; sp += 64) mx = fmaxf(mx, a.part_ml[(base + sp) * 2]);
+    mx = wave_max(mx);
+    float den = 0.0f;
+    for (int sp = tid; sp < n_splits; sp += 64) {
       const float w = fast_exp2(a.part_ml[(base + sp) * 2] - mx);
-      num = fmaf(w, a.part_o[(base + sp) * DH + d], num);
+      wsp[sp] = w;
       den = fmaf(w, a.part_ml[(base + sp) * 2 + 1], den);
     }
-    a.out[bh * DH + d] = num * (1.0f / den);
+    den = wave_sum(den);
+    const float inv = 1.0f / den;
+    for (int sp = tid; sp < n_splits; sp += 64) wsp[sp] *= inv;
   }
-  if (tid == 0) a.counters[b * a.Hkv + kvh] = 0u;
+  __syncthreads();
+  for (int d = tid; d < DH; d += 128) {
+    const float* po = a.part_o + base * DH + d;
+    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+    int sp = 0;
+    for (; sp + 3 < n_splits; sp += 4) {
+      o0 = fmaf(wsp[sp], po[static_cast<long>(sp) * DH], o0);
+      o1 = fmaf(wsp[sp + 1], po[static_cast<long>(sp + 1) * DH], o1);
+      o2 = fmaf(wsp[sp + 2], po[static_cast<long>(sp + 2) * DH], o2);
+      o3 = fmaf(wsp[sp + 3], po[static_cast<long>(sp + 3) * DH], o3);
+    }
+    for (; sp < n_splits; ++sp) o0 = fmaf(wsp[sp], po[static_cast<long>(sp) * DH], o0);
+    a.out[bh * DH + d] = (o0 + o1) + (o2 + o3);
+  }
 }
 
 template <int DH, int G, int SPLIT>
 int launch_split(const DecodeArgs& args, int B, hipStream_t stream) {
   dim3 grid(args.max_splits, args.Hkv, B);
   hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT>), grid, dim3(256), 0, stream, args);
-  return check_launch("gqa_decode_kernel");
+  int rc = check_launch("gqa_decode_kernel");
+  if (rc || args.max_splits <= 1) return rc;
+  hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(128), 0, stream,
+                     args, SPLIT, args.Hkv * G);
+  return check_launch("gqa_decode_combine_kernel");
 }
 
 template <int DH, int G>
 int launch_dh_g(const DecodeArgs& args, int B, int split, hipStream_t stream) {
+  // G = 4 keeps 4 q heads of state per lane: only 256-key splits fit 2 waves/SIMD unspilled.
+  if (G == 4) return launch_split<DH, G, 256>(args, B, stream);
   switch (split) {
-    case 64: return launch_split<DH, G, 64>(args, B, stream);
     case 128: return launch_split<DH, G, 128>(args, B, stream);
-    default: return launch_split<DH, G, 256>(args, B, stream);
+    case 256: return launch_split<DH, G, 256>(args, B, stream);
+    case 512: return launch_split<DH, G, 512>(args, B, stream);
+    default: return launch_split<DH, G, 1024>(args, B, stream);
   }
+}
+
+// Tuning override (read once): ORATOR_DECODE_SPLIT in {128,256,512,1024} fixes the
+// split length instead of the occupancy heuristic.
+int split_override() {
+  static const int v = [] {
+    const char* e = getenv("ORATOR_DECODE_SPLIT");
+    const int x = e ? atoi(e) : 0;
+    return (x == 128 || x == 256 || x == 512 || x == 1024) ? x : 0;
+  }();
+  return v;
 }
 
 }  // namespace
@@ -322,21 +425,21 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
       return fail(ORATOR_ERR_CAPACITY, "gqa_decode: capacity exceeds max_pages*page_size");
   }
   // Largest split that still puts >= 1024 workgroups (4 per CU) on the device.
-  int split = 64;
-  for (int cand : {256, 128}) {
+  int split = 128;
+  for (int cand : {1024, 512, 256}) {
     const long wgs = static_cast<long>(p.B) * p.Hkv * ((p.capacity + cand - 1) / cand);
     if (wgs >= 1024) {
       split = cand;
       break;
     }
   }
+  if (split_override()) split = split_override();
+  if (G == 4) split = 256;
   const int max_splits = (p.capacity + split - 1) / split;
-  const long counters = static_cast<long>(p.B) * p.Hkv;
-  if (counters * 4 > static_cast<long>(kCounterBytes))
-    return fail(ORATOR_ERR_UNSUPPORTED, "gqa_decode: B*Hkv exceeds the combine counter pool");
   const size_t part_o = static_cast<size_t>(p.B) * p.Hq * max_splits * p.Dh * sizeof(float);
   const size_t part_ml = static_cast<size_t>(p.B) * p.Hq * max_splits * 2 * sizeof(float);
-  char* ws = static_cast<char*>(workspace(stream, kCounterBytes + part_o + part_ml, kCounterBytes));
+  if (max_splits > 1024) return fail(ORATOR_ERR_CAPACITY, "gqa_decode: more than 1024 splits");
+  char* ws = static_cast<char*>(workspace(stream, part_o + part_ml, 0));
   if (!ws) return ORATOR_ERR_HIP;
 
   DecodeArgs args;
@@ -346,9 +449,8 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   args.page_table = p.page_table;
   args.pos = p.pos;
   args.out = p.out;
-  args.counters = reinterpret_cast<unsigned*>(ws);
-  args.part_o = reinterpret_cast<float*>(ws + kCounterBytes);
-  args.part_ml = reinterpret_cast<float*>(ws + kCounterBytes + part_o);
+  args.part_o = reinterpret_cast<float*>(ws);
+  args.part_ml = reinterpret_cast<float*>(ws + part_o);
   args.stream_stride = p.stream_stride;
   args.max_pages = p.max_pages;
   args.page_shift = page_shift;

@@ -95,6 +95,6 @@ def test_argmax_banned_random_and_ties():
     assert _argmax_gpu(x) == orc.argmax_banned(x) == int(top[0])
     assert _argmax_gpu(x, int(top[0]), int(top[1])) == int(top[2])
     for idx in ([2, 258], [1, 2], [1, 3], [130, 2], [5, 5 + 256 * 7, 99]):
-        y = np.zeros(1000, np.float32)
+        y = np.zeros(2000, np.float32)
         y[idx] = 5.0
         assert _argmax_gpu(y) == orc.argmax_banned(y), idx

@@ -11,11 +11,17 @@ import math
 
 import numpy as np
 import pytest
-import torch
-import torch.nn.functional as F
 
 import oracle_lib as orc
 from helpers import SplitMix64, rel_err
+
+# torch (CPU) is a library oracle here.  It is imported lazily so that collecting this
+# module in a GPU run never loads torch's own HIP runtime next to the product library.
+
+def _torch():
+    import torch as _t
+    import torch.nn.functional as _F
+    return _t, _F
 
 # ------------------------------------------------------------------------ bf16 ----
 
@@ -38,6 +44,7 @@ def test_bf16_known_answers():
 
 
 def test_bf16_matches_torch_rne():
+    torch, F = _torch()
     r = SplitMix64(11)
     x = np.concatenate([
         r.normal((4096,)),
@@ -91,6 +98,7 @@ def test_rope_interleaved_reference_fixture(golden):
 def _hf_rotate_half(x, pos, base, Dh):
     """HF Qwen3 rotary: x*cos + rotate_half(x)*sin, angle formed as fp32 pos*inv_freq
     (the reference's fp32 angle), cos/sin and the rest in fp64."""
+    torch, F = _torch()
     i = torch.arange(Dh // 2, dtype=torch.float64)
     inv = torch.pow(torch.tensor(base, dtype=torch.float64), -2.0 * i / Dh).float()
     ang = (torch.from_numpy(pos).float()[:, None] * inv[None, :]).double()
@@ -157,6 +165,7 @@ def test_gqa_attention_reference_fixture(golden):
 
 
 def test_gqa_attention_noncausal_vs_sdpa():
+    torch, F = _torch()
     r = SplitMix64(15)
     T, Hq, Hkv, Dh = 19, 4, 2, 64
     q, k, v = r.normal((T, Hq, Dh)), r.normal((T, Hkv, Dh)), r.normal((T, Hkv, Dh))
@@ -181,6 +190,7 @@ def _cache(r, S, Hkv, Dh, cap=None):
 
 
 def test_kv_write_bit_exact_and_offset():
+    torch, F = _torch()
     r = SplitMix64(16)
     k, v = r.normal((5, 8, 128)), r.normal((5, 8, 128))
     kc = np.zeros((20, 8, 128), np.uint16)
@@ -215,6 +225,7 @@ def test_kv_write_paged_identity_and_permuted():
 
 def _sdpa_cache(q, kc, vc, pos0, scale):
     """torch SDPA (fp64) over the bf16-decoded cache; query row t sees keys [0, pos0+t]."""
+    torch, F = _torch()
     Tq, Hq, Dh = q.shape
     Hkv = kc.shape[1]
     S = pos0 + Tq
@@ -346,6 +357,7 @@ def test_relpos_vs_closed_form_fp64(T, valid):
 
 
 def test_relpos_reduces_to_mha_and_masks_keys():
+    torch, F = _torch()
     r = SplitMix64(24)
     T, H, Dk = 33, 2, 64
     q, k, v, p, u, vb = _relpos_inputs(r, T, H, Dk)
