@@ -116,6 +116,26 @@ int orator_gqa_decode_paged(const float* q, const uint16_t* kpool, const uint16_
                             const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
                             float scale, void* stream);
 
+/* Prefill precision modes.
+ * FP32: q enters the MFMA products as three bf16 terms and the softmax weights as two, so
+ *       results track the fp32 reference (GqaCacheAttnKernel) to fp32 rounding level.
+ * BF16: q and the softmax weights rounded to bf16 (one MFMA per product). */
+#define ORATOR_PREFILL_FP32 0
+#define ORATOR_PREFILL_BF16 1
+
+/* GqaCacheAttnKernel (src/model/asr_text_decoder.cu:88-142, launch :537-541): query row t
+ * (absolute position *d_pos0 + t) of q [Tq, Hq, Dh] attends keys [0, pos0 + t] of the bf16
+ * cache.  fp32 mode.  `capacity` = the cache's max_seq_len (keys past it are not read). */
+int orator_gqa_prefill(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int Tq,
+                       int Hq, int Hkv, int Dh, const int* d_pos0, int capacity, float scale,
+                       void* stream);
+/* General form: q as fp32 (`q`) or bf16 bits (`q_bf16`, used when q is NULL); contiguous
+ * cache (page_table NULL) or one stream's page-table row; `mode` ORATOR_PREFILL_*. */
+int orator_gqa_prefill_ex(const float* q, const uint16_t* q_bf16, const uint16_t* kpool,
+                          const uint16_t* vpool, const int* page_table, int max_pages,
+                          int page_size, float* out, int Tq, int Hq, int Hkv, int Dh,
+                          const int* d_pos0, int capacity, float scale, int mode, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,7 +67,12 @@ SIGNATURES: dict[str, list] = {
     "orator_kv_write_paged": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p],
     "orator_gqa_decode": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+    "orator_gqa_prefill": [_p, _p, _p, _p, _i, _i, _i, _i, _p, _i, _f, _p],
+    "orator_gqa_prefill_ex": [_p, _p, _p, _p, _p, _i, _i, _p, _i, _i, _i, _i, _p, _i, _f, _i, _p],
 }
+
+PREFILL_FP32 = 0
+PREFILL_BF16 = 1
 
 _lib = None
 

@@ -9,7 +9,7 @@ reference layout [max_seq_len, Hkv, Dh].
 """
 from __future__ import annotations
 
-from ._lib import call
+from ._lib import PREFILL_BF16, PREFILL_FP32, call  # noqa: F401
 from .runtime import _sh, ptr
 
 
@@ -40,3 +40,20 @@ def GqaDecodeAttnPaged(q, kpool, vpool, page_table, max_pages: int, page_size: i
     """Stream b's q [Hq, Dh] attends d_pos[b] + 1 keys through page-table row b."""
     call("orator_gqa_decode_paged", ptr(q), ptr(kpool), ptr(vpool), ptr(page_table), max_pages,
          page_size, ptr(d_pos), ptr(out), B, Hq, Hkv, Dh, scale, _sh(stream))
+
+
+def GqaCacheAttn(q, kc, vc, out, Tq: int, Hq: int, Hkv: int, Dh: int, d_pos0, capacity: int,
+                 scale: float, stream=None) -> None:
+    """Prefill: row t of q [Tq, Hq, Dh] (absolute position *d_pos0 + t) attends keys
+    [0, pos0 + t]; fp32 mode."""
+    call("orator_gqa_prefill", ptr(q), ptr(kc), ptr(vc), ptr(out), Tq, Hq, Hkv, Dh, ptr(d_pos0),
+         capacity, scale, _sh(stream))
+
+
+def GqaCacheAttnEx(q, q_bf16, kpool, vpool, page_table, max_pages: int, page_size: int, out,
+                   Tq: int, Hq: int, Hkv: int, Dh: int, d_pos0, capacity: int, scale: float,
+                   mode: int = PREFILL_FP32, stream=None) -> None:
+    """Prefill with fp32 or bf16 q, contiguous or paged cache, fp32 or bf16 precision mode."""
+    call("orator_gqa_prefill_ex", ptr(q), ptr(q_bf16), ptr(kpool), ptr(vpool), ptr(page_table),
+         max_pages, page_size, ptr(out), Tq, Hq, Hkv, Dh, ptr(d_pos0), capacity, scale, mode,
+         _sh(stream))

@@ -1,0 +1,144 @@
+"""GPU parity: MFMA prefill attention against the oracle's GqaCacheAttnKernel restatement.
+
+fp32 mode: max |g - r| / max(|r|, 0.05) <= 1e-4.  bf16 mode: max |g - r| <= 2e-2 on
+unit-scale outputs.  Inputs follow BASELINE configs[1]: N(0,1) q/k/v, QK-RMSNorm (unit
+gain, eps 1e-6) and RoPE theta 1e6 at the tokens' absolute positions, K/V rounded to bf16
+by the KV write."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from gpu_helpers import down, empty, say, up
+from helpers import SplitMix64, rel_err
+from orator_amd import decoder_attn as da
+
+pytestmark = pytest.mark.gpu
+
+FLOOR, TOL32, TOL16 = 0.05, 1e-4, 2e-2
+
+
+def _layer_inputs(seed, T, pos0, Hq=16, Hkv=8, Dh=128, cap=None):
+    """q (normed, roped) for positions pos0..pos0+T-1 and a bf16 cache holding positions
+    0..pos0+T-1 (earlier positions = a previous prefill)."""
+    r = SplitMix64(seed)
+    S = pos0 + T
+    cap = cap or S
+    ones = np.ones(Dh, np.float32)
+    k = orc.rms_norm(r.normal((S * Hkv, Dh)), ones, 1e-6).reshape(S, Hkv, Dh)
+    k = orc.rope_half(k, np.arange(S, dtype=np.int32), 1e6)
+    v = r.normal((S, Hkv, Dh))
+    kc = np.zeros((cap, Hkv, Dh), np.uint16)
+    vc = np.zeros_like(kc)
+    orc.kv_write(k, v, kc, vc, 0)
+    q = orc.rms_norm(r.normal((T * Hq, Dh)), ones, 1e-6).reshape(T, Hq, Dh)
+    q = orc.rope_half(q, np.arange(pos0, pos0 + T, dtype=np.int32), 1e6)
+    return q, kc, vc
+
+
+def _run(q, kc, vc, pos0, cap, mode, Hkv, page=None):
+    T, Hq, Dh = q.shape
+    dout = empty(q.shape, np.float32)
+    scale = 1.0 / math.sqrt(Dh)
+    dpos = up(np.array([pos0], np.int32))
+    if page is None:
+        if mode == da.PREFILL_FP32:
+            da.GqaCacheAttn(up(q), up(kc), up(vc), dout, T, Hq, Hkv, Dh, dpos, cap, scale)
+        else:
+            da.GqaCacheAttnEx(up(q), None, up(kc), up(vc), None, 0, 0, dout, T, Hq, Hkv, Dh, dpos,
+                              cap, scale, mode)
+    else:
+        kp, vp, table, ps = page
+        da.GqaCacheAttnEx(up(q), None, up(kp), up(vp), up(table), table.size, ps, dout, T, Hq, Hkv,
+                          Dh, dpos, cap, scale, mode)
+    return down(dout, q.shape)
+
+
+@pytest.mark.parametrize("mode", [da.PREFILL_FP32, da.PREFILL_BF16])
+def test_prefill_config2_shape(mode):
+    """T = 503 (128 prompt + 375 audio), pos0 = 0."""
+    T, Hq, Hkv, Dh = 503, 16, 8, 128
+    q, kc, vc = _layer_inputs(503, T, 0)
+    ref = orc.gqa_prefill(q, kc, vc, 0, 1.0 / math.sqrt(Dh), threads=8)
+    say("prefill config2", mode)
+    got = _run(q, kc, vc, 0, T, mode, Hkv)
+    if mode == da.PREFILL_FP32:
+        assert rel_err(got, ref, FLOOR) <= TOL32
+    else:
+        assert np.max(np.abs(got - ref)) <= TOL16
+
+
+def test_prefill_streaming_split_equals_full():
+    """PrefillAt(0..128) then PrefillAt(128..503) on the same cache gives the full result
+    (test/unit/model/test_asr_decoder.cc:76-127)."""
+    T, split, Hkv, Dh = 503, 128, 8, 128
+    q, kc, vc = _layer_inputs(7, T, 0)
+    say("prefill split")
+    full = _run(q, kc, vc, 0, T, da.PREFILL_FP32, Hkv)
+    a = _run(np.ascontiguousarray(q[:split]), kc, vc, 0, T, da.PREFILL_FP32, Hkv)
+    b = _run(np.ascontiguousarray(q[split:]), kc, vc, split, T, da.PREFILL_FP32, Hkv)
+    # same rows, same keys, same kernel: identical up to the row's tile grouping
+    assert rel_err(np.concatenate([a, b]), full, FLOOR) <= 2e-6
+
+
+@pytest.mark.parametrize("T,pos0,cap", [(1, 0, 64), (1, 700, 1024), (37, 1000, 2048),
+                                        (64, 0, 64), (65, 3, 128), (200, 1800, 2048)])
+def test_prefill_offsets_and_ragged(T, pos0, cap):
+    Hkv, Dh = 8, 128
+    q, kc, vc = _layer_inputs(T + pos0, T, pos0, cap=cap)
+    ref = orc.gqa_prefill(q, kc, vc, pos0, 1.0 / math.sqrt(Dh), threads=8)
+    say("prefill offsets", T, pos0, cap)
+    got = _run(q, kc, vc, pos0, cap, da.PREFILL_FP32, Hkv)
+    assert rel_err(got, ref, FLOOR) <= TOL32
+    if T == 1 and pos0 == 0:  # one key: the output is v0
+        np.testing.assert_allclose(got[0], np.repeat(orc.from_bf16(vc[0]), 2, axis=0), atol=1e-6)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 4)])
+def test_prefill_group_variants(Hq, Hkv):
+    T, pos0, Dh = 150, 20, 128
+    q, kc, vc = _layer_inputs(Hq * 10 + Hkv, T, pos0, Hq=Hq, Hkv=Hkv)
+    ref = orc.gqa_prefill(q, kc, vc, pos0, 1.0 / math.sqrt(Dh), threads=8)
+    say("prefill groups", Hq, Hkv)
+    got = _run(q, kc, vc, pos0, pos0 + T, da.PREFILL_FP32, Hkv)
+    assert rel_err(got, ref, FLOOR) <= TOL32
+
+
+def test_prefill_paged_matches_contiguous():
+    T, pos0, Hkv, Dh, ps = 300, 100, 8, 128, 16
+    q, kc, vc = _layer_inputs(11, T, pos0, cap=400)
+    n_pages = 400 // ps
+    perm = np.array(SplitMix64(3).uniform(n_pages).argsort(), np.int32)
+    kp = np.empty((n_pages, ps, Hkv, Dh), np.uint16)
+    vp = np.empty_like(kp)
+    kp[perm] = kc.reshape(n_pages, ps, Hkv, Dh)
+    vp[perm] = vc.reshape(n_pages, ps, Hkv, Dh)
+    say("prefill paged")
+    a = _run(q, kc, vc, pos0, 400, da.PREFILL_FP32, Hkv)
+    b = _run(q, kc, vc, pos0, 400, da.PREFILL_FP32, Hkv, page=(kp, vp, perm, ps))
+    np.testing.assert_array_equal(a, b)
+
+
+def test_prefill_bf16_q_input():
+    T, Hkv, Dh = 96, 8, 128
+    q, kc, vc = _layer_inputs(13, T, 0)
+    qb = orc.to_bf16(q)
+    ref = orc.gqa_prefill(orc.from_bf16(qb), kc, vc, 0, 1.0 / math.sqrt(Dh), threads=8)
+    dout = empty(q.shape, np.float32)
+    say("prefill bf16 q")
+    da.GqaCacheAttnEx(None, up(qb), up(kc), up(vc), None, 0, 0, dout, T, 16, Hkv, Dh,
+                      up(np.array([0], np.int32)), T, 1.0 / math.sqrt(Dh), da.PREFILL_BF16)
+    assert np.max(np.abs(down(dout, q.shape) - ref)) <= TOL16
+
+
+def test_prefill_2048_bf16():
+    """The prefill throughput shape (2048 tokens), bf16 mode."""
+    T, Hkv, Dh = 2048, 8, 128
+    q, kc, vc = _layer_inputs(2048, T, 0)
+    ref = orc.gqa_prefill(q, kc, vc, 0, 1.0 / math.sqrt(Dh), threads=16)
+    say("prefill 2048 bf16")
+    got = _run(q, kc, vc, 0, T, da.PREFILL_BF16, Hkv)
+    assert np.max(np.abs(got - ref)) <= TOL16
