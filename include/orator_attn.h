@@ -88,6 +88,11 @@ int orator_rope_half(float* x, const int* positions, int n_tokens, int n_heads, 
  * Same tie rule: ties keep the candidate of the lower scan slot. */
 int orator_argmax_banned(const float* logits, int n, int ban0, int ban1, int* out_idx,
                          void* stream);
+/* asr_ops::GqaAttention (include/model/asr_ops.cuh:50-56; src/model/asr_ops.cu:130-195,252-295).
+ * fp32 q [T,Hq,Dh], k/v [T,Hkv,Dh]; row i attends keys [0,i] (causal) or [0,T).  Default
+ * stream.  Dh in {64,128}, Hq/Hkv in {1,2,4} (the reference accepts any power-of-two Dh). */
+int orator_gqa_attention(const float* q, const float* k, const float* v, float* out, int T, int Hq,
+                         int Hkv, int Dh, float scale, int causal);
 /* asr_gemm::F32ToBf16 / Bf16ToF32 (include/model/asr_gemm.h:23-25; src/model/asr_gemm.cu:45-57). */
 int orator_f32_to_bf16(const float* in, uint16_t* out, long n, void* stream);
 int orator_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream);
@@ -102,6 +107,21 @@ int orator_kv_write(const float* k, const float* v, uint16_t* kc, uint16_t* vc, 
 int orator_kv_write_paged(const float* k, const float* v, uint16_t* kpool, uint16_t* vpool,
                           const int* page_table, int max_pages, int page_size, int n_pages,
                           int B, int Tq, int Hkv, int Dh, const int* d_pos0, void* stream);
+
+/* Fused QK-RMSNorm + RoPE + KV write: the decoder's per-layer sequence
+ *   RmsNorm(q, q_norm) ; RmsNorm(k, k_norm) ; RopeHalf(q) ; RopeHalf(k) ; WriteKvCache(k, v)
+ * (src/model/asr_text_decoder.cu:408-413 decode, :530-536 prefill) in one launch.  Token t
+ * of q/k/v (rows q + t*q_stride, k/v + t*kv_stride, heads contiguous, Dh = 128) is
+ * normalised and rotated at positions[t] in place; k and v go to the cache row of
+ * positions[t] as bf16.  Cache: contiguous (page_table NULL, `capacity` rows) or paged
+ * (stream = t / tokens_per_stream selects the page-table row; `capacity` = pages in the
+ * pool).  Rows outside the cache are not written. */
+int orator_qk_norm_rope_kv_write(float* q, float* k, const float* v, long q_stride, long kv_stride,
+                                 const float* q_norm, const float* k_norm, float eps,
+                                 const int* positions, float theta, int n_tokens,
+                                 int tokens_per_stream, int Hq, int Hkv, int Dh, uint16_t* kpool,
+                                 uint16_t* vpool, const int* page_table, int max_pages,
+                                 int page_size, int capacity, void* stream);
 
 /* GqaDecodeAttnKernel (src/model/asr_text_decoder.cu:149-213, launch :416-418):
  * q [Hq, Dh] fp32 attends the S = *d_pos + 1 keys of the bf16 cache kc/vc.

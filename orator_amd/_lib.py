@@ -60,6 +60,7 @@ SIGNATURES: dict[str, list] = {
     "orator_swiglu": [_p, _p, _p, _i, _p],
     "orator_rope_half": [_p, _p, _i, _i, _i, _f, _p],
     "orator_argmax_banned": [_p, _i, _i, _i, _p, _p],
+    "orator_gqa_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _f, _i],
     "orator_f32_to_bf16": [_p, _p, _l, _p],
     "orator_bf16_to_f32": [_p, _p, _l, _p],
     # decoder KV + attention
@@ -67,6 +68,8 @@ SIGNATURES: dict[str, list] = {
     "orator_kv_write_paged": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p],
     "orator_gqa_decode": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+    "orator_qk_norm_rope_kv_write": [_p, _p, _p, _l, _l, _p, _p, _f, _p, _f, _i, _i, _i, _i, _i,
+                                     _p, _p, _p, _i, _i, _i, _p],
     "orator_gqa_prefill": [_p, _p, _p, _p, _i, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_prefill_ex": [_p, _p, _p, _p, _p, _i, _i, _p, _i, _i, _i, _i, _p, _i, _f, _i, _p],
 }

@@ -35,6 +35,13 @@ def RopeHalf(x, positions, n_tokens: int, n_heads: int, head_dim: int, theta_bas
          _sh(stream))
 
 
+def GqaAttention(q, k, v, out, T: int, Hq: int, Hkv: int, Dh: int, scale: float,
+                 causal: bool) -> None:
+    """include/model/asr_ops.cuh:55-56 (fp32 GQA self-attention, default stream)."""
+    call("orator_gqa_attention", ptr(q), ptr(k), ptr(v), ptr(out), T, Hq, Hkv, Dh, scale,
+         int(bool(causal)))
+
+
 def ArgmaxBanned(logits, n: int, ban0: int, ban1: int, out_idx, stream=None) -> None:
     """include/model/asr_ops.cuh:58-62."""
     call("orator_argmax_banned", ptr(logits), n, ban0, ban1, ptr(out_idx), _sh(stream))

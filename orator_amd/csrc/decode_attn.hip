@@ -34,10 +34,11 @@ namespace {
 
 struct DecodeArgs {
   const float* q;
-  const uint16_t* kpool;
-  const uint16_t* vpool;
+  const void* kpool;  // bf16 bits or fp32, per the kernel's KV type
+  const void* vpool;
   const int* page_table;
-  const int* pos;
+  const int* pos;      // [B]: stream b attends pos[b]+1 keys (pos_mode 0)
+  int pos_mode;        // 0: pos[b]+1 keys; 1: b+1 keys (causal self-attn); 2: capacity keys
   float* out;
   float* part_o;       // [B*Hq][max_splits][DH]
   float* part_ml;      // [B*Hq][max_splits][2]
@@ -50,36 +51,61 @@ struct DecodeArgs {
   float scale_log2e;
 };
 
-template <int DH>
+// Number of keys stream b attends, clamped to the capacity.
+__device__ __forceinline__ int stream_keys(const DecodeArgs& a, int b) {
+  const int S = a.pos_mode == 0 ? a.pos[b] + 1 : (a.pos_mode == 1 ? b + 1 : a.capacity);
+  return S > a.capacity ? a.capacity : S;
+}
+
+// Element helpers: K/V rows are bf16 (cache) or fp32 (self-attention over fp32 K/V).
+template <typename KV>
+struct KvElem {
+  static constexpr int EPV = 16 / sizeof(KV);  // elements per 16-byte load
+  // element e of a 16-byte load, widened to fp32
+  static __device__ __forceinline__ float get(const uint4& u, int e) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    if constexpr (sizeof(KV) == 2)
+      return (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
+    else
+      return __uint_as_float(w[e]);
+  }
+};
+
+template <int DH, typename KV>
 struct Chunk {
-  static constexpr int CH = 32;             // keys per chunk
-  static constexpr int NCQ = DH / 64;       // 16-byte loads per lane per key (octet layout)
-  static constexpr int NIQ = CH / 8;        // octet iterations per chunk
-  static constexpr int LPT = DH / 8;        // lanes per key, row layout
-  static constexpr int TPI = kWave / LPT;   // keys per row-layout instruction
-  static constexpr int NIV = CH / TPI;      // row-layout instructions per chunk
+  static constexpr int EPV = KvElem<KV>::EPV;
+  static constexpr int CH = sizeof(KV) == 2 ? 32 : 16;  // keys per chunk (same bytes)
+  static constexpr int NCQ = DH / (8 * EPV);    // 16-byte loads per lane per key (octet layout)
+  static constexpr int QPL = NCQ * EPV;         // dims per lane in the octet layout
+  static constexpr int NIQ = CH / 8;            // octet iterations per chunk
+  static constexpr int LPT = DH / 8;            // lanes per key, row layout (8 dims per lane)
+  static constexpr int NV = 8 / EPV;            // 16-byte loads per lane per key, row layout
+  static constexpr int TPI = kWave / LPT;       // keys per row-layout instruction
+  static constexpr int NIV = CH / TPI;          // row-layout instructions per chunk
   uint4 k[NIQ][NCQ];
-  uint4 v[NIV];
+  uint4 v[NIV][NV];
 };
 
 // Loads one 32-key chunk starting at absolute key c (rows resolved through row_lds).
-template <int DH>
-__device__ __forceinline__ void load_chunk(Chunk<DH>& ch, const uint16_t* kbase,
-                                           const uint16_t* vbase, const int* row_lds, long rs,
-                                           int c, int t0, int end, int lane) {
-  using CK = Chunk<DH>;
+// Octet layout: lane o of a key's 8 lanes reads bytes 128*cc + 16*o of the row.
+template <int DH, typename KV>
+__device__ __forceinline__ void load_chunk(Chunk<DH, KV>& ch, const KV* kbase, const KV* vbase,
+                                           const int* row_lds, long rs, int c, int t0, int end,
+                                           int lane) {
+  using CK = Chunk<DH, KV>;
+  constexpr int EPV = CK::EPV;
   const int g0 = (c - t0) >> 4;
   const long rb0 = row_lds[g0];
-  const long rb1 = row_lds[g0 + 1];
+  const long rb1 = CK::CH > 16 ? row_lds[g0 + 1] : rb0;
   const int o = lane & 7;
 #pragma unroll
   for (int i = 0; i < CK::NIQ; ++i) {
     const int kk = 8 * i + (lane >> 3);  // key within the chunk
     const long row = (kk < 16 ? rb0 : rb1) + (kk & 15);
-    const uint16_t* src = kbase + row * rs + 8 * o;
+    const KV* src = kbase + row * rs + EPV * o;
     if (c + kk < end) {
 #pragma unroll
-      for (int cc = 0; cc < CK::NCQ; ++cc) ch.k[i][cc] = load_nt(src + 64 * cc);
+      for (int cc = 0; cc < CK::NCQ; ++cc) ch.k[i][cc] = load_nt(src + 8 * EPV * cc);
     } else {
 #pragma unroll
       for (int cc = 0; cc < CK::NCQ; ++cc) ch.k[i][cc] = make_uint4(0, 0, 0, 0);
@@ -91,18 +117,22 @@ __device__ __forceinline__ void load_chunk(Chunk<DH>& ch, const uint16_t* kbase,
   for (int i = 0; i < CK::NIV; ++i) {
     const int kk = CK::TPI * i + r;
     const long row = (kk < 16 ? rb0 : rb1) + (kk & 15);
-    ch.v[i] = c + kk < end ? load_nt(vbase + row * rs + 8 * dg) : make_uint4(0, 0, 0, 0);
+    const KV* src = vbase + row * rs + 8 * dg;
+#pragma unroll
+    for (int u = 0; u < CK::NV; ++u)
+      ch.v[i][u] = c + kk < end ? load_nt(src + EPV * u) : make_uint4(0, 0, 0, 0);
   }
 }
 
 // Scores, online-softmax update and PV accumulation for one resident chunk at key c.
-template <int DH, int G>
-__device__ __forceinline__ void process_chunk(const Chunk<DH>& cur,
-                                              const float (&qr)[G][Chunk<DH>::NCQ][8],
+template <int DH, int G, typename KV>
+__device__ __forceinline__ void process_chunk(const Chunk<DH, KV>& cur,
+                                              const float (&qr)[G][Chunk<DH, KV>::QPL],
                                               float (&m)[G], float (&lpart)[G],
                                               float (&acc)[G][8], int c, int end, int lane,
                                               float scale_log2e) {
-  using CK = Chunk<DH>;
+  using CK = Chunk<DH, KV>;
+  using E = KvElem<KV>;
   // scores, octet layout
   float s[CK::NIQ][G];
 #pragma unroll
@@ -112,16 +142,11 @@ __device__ __forceinline__ void process_chunk(const Chunk<DH>& cur,
     for (int g = 0; g < G; ++g) d[g] = 0.0f;
 #pragma unroll
     for (int cc = 0; cc < CK::NCQ; ++cc) {
-      const uint32_t w[4] = {cur.k[i][cc].x, cur.k[i][cc].y, cur.k[i][cc].z, cur.k[i][cc].w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float klo = bf16_lo(w[e]);
-        const float khi = bf16_hi(w[e]);
+      for (int e = 0; e < CK::EPV; ++e) {
+        const float kv = E::get(cur.k[i][cc], e);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          d[g] = fmaf(qr[g][cc][2 * e], klo, d[g]);
-          d[g] = fmaf(qr[g][cc][2 * e + 1], khi, d[g]);
-        }
+        for (int g = 0; g < G; ++g) d[g] = fmaf(qr[g][cc * CK::EPV + e], kv, d[g]);
       }
     }
     const bool valid = c + 8 * i + (lane >> 3) < end;
@@ -163,23 +188,22 @@ __device__ __forceinline__ void process_chunk(const Chunk<DH>& cur,
 #pragma unroll
   for (int i = 0; i < CK::NIV; ++i) {
     const int src = 8 * ((CK::TPI * i + r) & 7);
-    const uint32_t w[4] = {cur.v[i].x, cur.v[i].y, cur.v[i].z, cur.v[i].w};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float p = __shfl(pk[(CK::TPI * i) >> 3][g], src);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[g][2 * e] = fmaf(p, bf16_lo(w[e]), acc[g][2 * e]);
-        acc[g][2 * e + 1] = fmaf(p, bf16_hi(w[e]), acc[g][2 * e + 1]);
-      }
+      for (int u = 0; u < CK::NV; ++u)
+#pragma unroll
+        for (int e = 0; e < CK::EPV; ++e)
+          acc[g][u * CK::EPV + e] = fmaf(p, E::get(cur.v[i][u], e), acc[g][u * CK::EPV + e]);
     }
   }
 }
 
-template <int DH, int G, int SPLIT>
+template <int DH, int G, int SPLIT, typename KV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gqa_decode_kernel(
     DecodeArgs a) {
-  using CK = Chunk<DH>;
+  using CK = Chunk<DH, KV>;
   constexpr int NW = 4;
   constexpr int TPW = SPLIT / NW;  // keys per wave
   constexpr int NG = SPLIT / 16;   // 16-key groups per split
@@ -192,8 +216,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
-  int S = a.pos[b] + 1;
-  if (S > a.capacity) S = a.capacity;
+  int S = stream_keys(a, b);
   if (S <= 0) {  // no keys: the reference's 1/sum guard yields zeros
     if (split == 0)
       for (int idx = threadIdx.x; idx < G * DH; idx += 256)
@@ -220,26 +243,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     row_lds[tid] = row;
   }
 
-  // ---- q of the G heads, octet layout: lane owns dims 64*cc + 8*o + e ----
+  // ---- q of the G heads, octet layout: lane owns dims 8*EPV*cc + EPV*o + e ----
   const int o = lane & 7;
-  float qr[G][CK::NCQ][8];
+  float qr[G][CK::QPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float* qh = a.q + (static_cast<long>(b) * Hq + kvh * G + g) * DH + 8 * o;
+    const float* qh = a.q + (static_cast<long>(b) * Hq + kvh * G + g) * DH + CK::EPV * o;
 #pragma unroll
-    for (int cc = 0; cc < CK::NCQ; ++cc) {
-      const float4 x0 = *reinterpret_cast<const float4*>(qh + 64 * cc);
-      const float4 x1 = *reinterpret_cast<const float4*>(qh + 64 * cc + 4);
-      qr[g][cc][0] = x0.x; qr[g][cc][1] = x0.y; qr[g][cc][2] = x0.z; qr[g][cc][3] = x0.w;
-      qr[g][cc][4] = x1.x; qr[g][cc][5] = x1.y; qr[g][cc][6] = x1.z; qr[g][cc][7] = x1.w;
-    }
+    for (int cc = 0; cc < CK::NCQ; ++cc)
+#pragma unroll
+      for (int e4 = 0; e4 < CK::EPV; e4 += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(qh + 8 * CK::EPV * cc + e4);
+        qr[g][cc * CK::EPV + e4] = x.x;
+        qr[g][cc * CK::EPV + e4 + 1] = x.y;
+        qr[g][cc * CK::EPV + e4 + 2] = x.z;
+        qr[g][cc * CK::EPV + e4 + 3] = x.w;
+      }
   }
   __syncthreads();
 
   const long kv_base = (a.page_table ? 0 : static_cast<long>(b) * a.stream_stride) +
                        static_cast<long>(kvh) * DH;
-  const uint16_t* kbase = a.kpool + kv_base;
-  const uint16_t* vbase = a.vpool + kv_base;
+  const KV* kbase = static_cast<const KV*>(a.kpool) + kv_base;
+  const KV* vbase = static_cast<const KV*>(a.vpool) + kv_base;
   const long rs = static_cast<long>(a.Hkv) * DH;  // elements per pool row
   const int w0 = t0 + wave * TPW;
   const int w1 = min(w0 + TPW, S);
@@ -257,15 +283,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   if (w0 < w1) {
     // Ping-pong buffers: the loads of one chunk are in flight while the other is computed.
     CK A, Bb;
-    load_chunk<DH>(A, kbase, vbase, row_lds, rs, w0, t0, w1, lane);
+    load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, w0, t0, w1, lane);
     int c = w0;
     while (true) {
-      if (c + CK::CH < w1) load_chunk<DH>(Bb, kbase, vbase, row_lds, rs, c + CK::CH, t0, w1, lane);
-      process_chunk<DH, G>(A, qr, m, lpart, acc, c, w1, lane, a.scale_log2e);
+      if (c + CK::CH < w1) load_chunk<DH, KV>(Bb, kbase, vbase, row_lds, rs, c + CK::CH, t0, w1, lane);
+      process_chunk<DH, G, KV>(A, qr, m, lpart, acc, c, w1, lane, a.scale_log2e);
       c += CK::CH;
       if (c >= w1) break;
-      if (c + CK::CH < w1) load_chunk<DH>(A, kbase, vbase, row_lds, rs, c + CK::CH, t0, w1, lane);
-      process_chunk<DH, G>(Bb, qr, m, lpart, acc, c, w1, lane, a.scale_log2e);
+      if (c + CK::CH < w1) load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, c + CK::CH, t0, w1, lane);
+      process_chunk<DH, G, KV>(Bb, qr, m, lpart, acc, c, w1, lane, a.scale_log2e);
       c += CK::CH;
       if (c >= w1) break;
     }
@@ -334,8 +360,7 @@ __global__ __launch_bounds__(128) void gqa_decode_combine_kernel(DecodeArgs a, i
   __shared__ float wsp[1024];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  int S = a.pos[b] + 1;
-  if (S > a.capacity) S = a.capacity;
+  const int S = stream_keys(a, b);
   const int n_splits = (S + split_len - 1) / split_len;
   if (n_splits <= 1) return;  // written directly by the split kernel
   const long bh = static_cast<long>(b) * Hq + h;
@@ -371,10 +396,10 @@ __global__ __launch_bounds__(128) void gqa_decode_combine_kernel(DecodeArgs a, i
   }
 }
 
-template <int DH, int G, int SPLIT>
+template <int DH, int G, int SPLIT, typename KV>
 int launch_split(const DecodeArgs& args, int B, hipStream_t stream) {
   dim3 grid(args.max_splits, args.Hkv, B);
-  hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT>), grid, dim3(256), 0, stream, args);
+  hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV>), grid, dim3(256), 0, stream, args);
   int rc = check_launch("gqa_decode_kernel");
   if (rc || args.max_splits <= 1) return rc;
   hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(128), 0, stream,
@@ -382,16 +407,31 @@ int launch_split(const DecodeArgs& args, int B, hipStream_t stream) {
   return check_launch("gqa_decode_combine_kernel");
 }
 
-template <int DH, int G>
+template <int DH, int G, typename KV>
 int launch_dh_g(const DecodeArgs& args, int B, int split, hipStream_t stream) {
   // G = 4 keeps 4 q heads of state per lane: only 256-key splits fit 2 waves/SIMD unspilled.
-  if (G == 4) return launch_split<DH, G, 256>(args, B, stream);
-  switch (split) {
-    case 128: return launch_split<DH, G, 128>(args, B, stream);
-    case 256: return launch_split<DH, G, 256>(args, B, stream);
-    case 512: return launch_split<DH, G, 512>(args, B, stream);
-    default: return launch_split<DH, G, 1024>(args, B, stream);
+  if constexpr (G == 4) {
+    return launch_split<DH, G, 256, KV>(args, B, stream);
+  } else {
+    switch (split) {
+      case 128: return launch_split<DH, G, 128, KV>(args, B, stream);
+      case 512: return launch_split<DH, G, 512, KV>(args, B, stream);
+      case 1024: return launch_split<DH, G, 1024, KV>(args, B, stream);
+      default: return launch_split<DH, G, 256, KV>(args, B, stream);
+    }
   }
+}
+
+template <typename KV>
+int launch_kv(const DecodeArgs& args, int B, int Dh, int G, int split, hipStream_t stream) {
+  if (Dh == 128) {
+    if (G == 1) return launch_dh_g<128, 1, KV>(args, B, split, stream);
+    if (G == 2) return launch_dh_g<128, 2, KV>(args, B, split, stream);
+    return launch_dh_g<128, 4, KV>(args, B, split, stream);
+  }
+  if (G == 1) return launch_dh_g<64, 1, KV>(args, B, split, stream);
+  if (G == 2) return launch_dh_g<64, 2, KV>(args, B, split, stream);
+  return launch_dh_g<64, 4, KV>(args, B, split, stream);
 }
 
 // Tuning override (read once): ORATOR_DECODE_SPLIT in {128,256,512,1024} fixes the
@@ -409,7 +449,7 @@ int split_override() {
 
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (p.B <= 0 || p.Hq <= 0 || p.Hkv <= 0 || p.Dh <= 0) return ORATOR_OK;  // reference no-op
-  if (!p.q || !p.kpool || !p.vpool || !p.pos || !p.out)
+  if (!p.q || !p.kpool || !p.vpool || (!p.pos && p.pos_mode == 0) || !p.out)
     return fail(ORATOR_ERR_INVALID, "gqa_decode: null pointer");
   if (p.Hq % p.Hkv) return fail(ORATOR_ERR_INVALID, "gqa_decode: Hq must be a multiple of Hkv");
   const int G = p.Hq / p.Hkv;
@@ -424,15 +464,9 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
     if (static_cast<long>(p.max_pages) * p.page_size < p.capacity)
       return fail(ORATOR_ERR_CAPACITY, "gqa_decode: capacity exceeds max_pages*page_size");
   }
-  // Largest split that still puts >= 1024 workgroups (4 per CU) on the device.
-  int split = 128;
-  for (int cand : {1024, 512, 256}) {
-    const long wgs = static_cast<long>(p.B) * p.Hkv * ((p.capacity + cand - 1) / cand);
-    if (wgs >= 1024) {
-      split = cand;
-      break;
-    }
-  }
+  // 256-key splits: measured best on MI355X for B = 1 and B = 16 at 4K keys (128 makes the
+  // merge dominate, 512+ leaves too few workgroups and lengthens the tail).
+  int split = 256;
   if (split_override()) split = split_override();
   if (G == 4) split = 256;
   const int max_splits = (p.capacity + split - 1) / split;
@@ -443,6 +477,7 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (!ws) return ORATOR_ERR_HIP;
 
   DecodeArgs args;
+  args.pos_mode = p.pos_mode;
   args.q = p.q;
   args.kpool = p.kpool;
   args.vpool = p.vpool;
@@ -459,14 +494,8 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   args.capacity = p.capacity;
   args.scale_log2e = p.scale * 1.4426950408889634f;
 
-  if (p.Dh == 128) {
-    if (G == 1) return launch_dh_g<128, 1>(args, p.B, split, stream);
-    if (G == 2) return launch_dh_g<128, 2>(args, p.B, split, stream);
-    return launch_dh_g<128, 4>(args, p.B, split, stream);
-  }
-  if (G == 1) return launch_dh_g<64, 1>(args, p.B, split, stream);
-  if (G == 2) return launch_dh_g<64, 2>(args, p.B, split, stream);
-  return launch_dh_g<64, 4>(args, p.B, split, stream);
+  if (p.kv_f32) return launch_kv<float>(args, p.B, p.Dh, G, split, stream);
+  return launch_kv<uint16_t>(args, p.B, p.Dh, G, split, stream);
 }
 
 }  // namespace orator_hip
@@ -515,6 +544,27 @@ int orator_gqa_decode_paged(const float* q, const uint16_t* kpool, const uint16_
   p.capacity = max_pages * page_size;
   p.scale = scale;
   return launch_gqa_decode(p, static_cast<hipStream_t>(stream));
+}
+
+// asr_ops::GqaAttention (include/model/asr_ops.cuh:50-56; src/model/asr_ops.cu:252-295):
+// fp32 self-attention = decode of T query rows over one shared fp32 K/V, row i attending
+// keys [0, i] (causal) or [0, T).  Default stream, as the reference.
+int orator_gqa_attention(const float* q, const float* k, const float* v, float* out, int T, int Hq,
+                         int Hkv, int Dh, float scale, int causal) {
+  DecodeProblem p{};
+  p.q = q;
+  p.kpool = k;
+  p.vpool = v;
+  p.kv_f32 = true;
+  p.pos_mode = causal ? 1 : 2;
+  p.out = out;
+  p.B = T;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.Dh = Dh;
+  p.capacity = T;
+  p.scale = scale;
+  return launch_gqa_decode(p, nullptr);
 }
 
 }  // extern "C"

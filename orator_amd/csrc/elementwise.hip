@@ -203,6 +203,78 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const float* __restrict__
   *reinterpret_cast<uint2*>(vc + dst) = make_uint2(pack_bf16x2(vv.x, vv.y), pack_bf16x2(vv.z, vv.w));
 }
 
+// -------------------------------------------- fused QK-norm + RoPE + KV write ----
+// One wave64 per (token, head) row of Dh = 128: lane j owns the rotate-half pair
+// (j, j + 64).  q rows: RMSNorm(q_norm) then RoPE, written back in place.  k rows:
+// RMSNorm(k_norm), RoPE, written back in place and as bf16 into the cache row of the
+// token's position, together with the bf16 of the matching v row.  Same arithmetic as
+// RmsNorm + RopeHalf + WriteKvCache run back to back (src/model/asr_text_decoder.cu:408-413,
+// 530-536); only the order of the sum of squares differs.
+struct QkvArgs {
+  float* q;
+  float* k;
+  const float* v;
+  long q_stride;   // elements between consecutive tokens of q
+  long kv_stride;  // ... of k and v
+  const float* q_norm;
+  const float* k_norm;
+  float eps;
+  const int* positions;  // [n_tokens]
+  float theta;
+  int n_tokens, tokens_per_stream, Hq, Hkv;
+  uint16_t* kpool;
+  uint16_t* vpool;
+  const int* page_table;  // nullptr => contiguous cache of `capacity` rows
+  int max_pages, page_shift, capacity;  // paged: capacity = number of pages in the pool
+};
+
+__global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(QkvArgs a) {
+#pragma clang fp contract(off)
+  constexpr int Dh = 128, half = 64;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int per_token = a.Hq + a.Hkv;
+  if (row >= a.n_tokens * per_token) return;
+  const int t = row / per_token;
+  const int hh = row % per_token;
+  const bool is_q = hh < a.Hq;
+  const int h = is_q ? hh : hh - a.Hq;
+  float* x = is_q ? a.q + t * a.q_stride + static_cast<long>(h) * Dh
+                  : a.k + t * a.kv_stride + static_cast<long>(h) * Dh;
+  const float* w = is_q ? a.q_norm : a.k_norm;
+  const float x0 = x[lane], x1 = x[lane + half];
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss / Dh + a.eps)));
+  const float n0 = x0 * inv * w[lane], n1 = x1 * inv * w[lane + half];
+  const int pos = a.positions[t];
+  float c, s;
+  rope_cs(static_cast<float>(pos), a.theta, lane, Dh, &c, &s);
+  const float r0 = n0 * c - n1 * s;
+  const float r1 = n1 * c + n0 * s;
+  x[lane] = r0;
+  x[lane + half] = r1;
+  if (is_q) return;
+  // cache row of this token's position
+  long crow;
+  if (a.page_table) {
+    const int b = t / a.tokens_per_stream;
+    const int pi = pos >> a.page_shift;
+    if (pos < 0 || pi >= a.max_pages) return;
+    const int page = a.page_table[static_cast<long>(b) * a.max_pages + pi];
+    if (page < 0 || page >= a.capacity) return;
+    crow = (static_cast<long>(page) << a.page_shift) | (pos & ((1 << a.page_shift) - 1));
+  } else {
+    if (pos < 0 || pos >= a.capacity) return;
+    crow = pos;
+  }
+  const long dst = (crow * a.Hkv + h) * Dh;
+  const float* vr = a.v + t * a.kv_stride + static_cast<long>(h) * Dh;
+  a.kpool[dst + lane] = f32_to_bf16(r0);
+  a.kpool[dst + lane + half] = f32_to_bf16(r1);
+  a.vpool[dst + lane] = f32_to_bf16(vr[lane]);
+  a.vpool[dst + lane + half] = f32_to_bf16(vr[lane + half]);
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -320,6 +392,48 @@ int orator_kv_write_paged(const float* k, const float* v, uint16_t* kpool, uint1
                      static_cast<hipStream_t>(stream), k, v, kpool, vpool, Tq, Hkv, Dh, d_pos0, 0,
                      page_table, max_pages, shift, n_pages, B);
   return check_launch("kv_write_paged");
+}
+
+int orator_qk_norm_rope_kv_write(float* q, float* k, const float* v, long q_stride, long kv_stride,
+                                 const float* q_norm, const float* k_norm, float eps,
+                                 const int* positions, float theta, int n_tokens,
+                                 int tokens_per_stream, int Hq, int Hkv, int Dh, uint16_t* kpool,
+                                 uint16_t* vpool, const int* page_table, int max_pages,
+                                 int page_size, int capacity, void* stream) {
+  if (n_tokens <= 0 || Hq <= 0 || Hkv <= 0 || Dh <= 0) return ORATOR_OK;
+  if (!q || !k || !v || !q_norm || !k_norm || !positions || !kpool || !vpool)
+    return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: null pointer");
+  if (Dh != 128) return fail(ORATOR_ERR_UNSUPPORTED, "qk_norm_rope_kv_write: Dh must be 128");
+  if (capacity <= 0) return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: capacity must be > 0");
+  QkvArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.q_stride = q_stride;
+  a.kv_stride = kv_stride;
+  a.q_norm = q_norm;
+  a.k_norm = k_norm;
+  a.eps = eps;
+  a.positions = positions;
+  a.theta = theta;
+  a.n_tokens = n_tokens;
+  a.tokens_per_stream = tokens_per_stream > 0 ? tokens_per_stream : n_tokens;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.kpool = kpool;
+  a.vpool = vpool;
+  a.page_table = page_table;
+  a.capacity = capacity;
+  if (page_table) {
+    a.page_shift = ilog2_exact(page_size);
+    if (a.page_shift < 0 || max_pages <= 0)
+      return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: page_size must be a power of two");
+    a.max_pages = max_pages;
+  }
+  const long rows = static_cast<long>(n_tokens) * (Hq + Hkv);
+  hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("qk_norm_rope_kv_write");
 }
 
 }  // extern "C"

@@ -37,8 +37,10 @@ inline int ilog2_exact(int v) {
 // ---- launchers (defined in the .hip files) ----
 struct DecodeProblem {
   const float* q;
-  const uint16_t* kpool;
-  const uint16_t* vpool;
+  const void* kpool;      // bf16 bits, or fp32 when kv_f32
+  const void* vpool;
+  bool kv_f32;
+  int pos_mode;           // 0: stream b attends pos[b]+1 keys; 1: b+1 keys; 2: capacity keys
   const int* page_table;  // nullptr => contiguous caches
   int max_pages;          // page-table row length (paged)
   int page_size;          // paged only (power of two >= 16)

@@ -57,3 +57,13 @@ def GqaCacheAttnEx(q, q_bf16, kpool, vpool, page_table, max_pages: int, page_siz
     call("orator_gqa_prefill_ex", ptr(q), ptr(q_bf16), ptr(kpool), ptr(vpool), ptr(page_table),
          max_pages, page_size, ptr(out), Tq, Hq, Hkv, Dh, ptr(d_pos0), capacity, scale, mode,
          _sh(stream))
+
+
+def QkNormRopeKvWrite(q, k, v, q_stride: int, kv_stride: int, q_norm, k_norm, eps: float,
+                      positions, theta: float, n_tokens: int, tokens_per_stream: int, Hq: int,
+                      Hkv: int, Dh: int, kpool, vpool, page_table=None, max_pages: int = 0,
+                      page_size: int = 0, capacity: int = 0, stream=None) -> None:
+    """RmsNorm(q), RmsNorm(k), RopeHalf(q, k) in place and the bf16 KV write, fused."""
+    call("orator_qk_norm_rope_kv_write", ptr(q), ptr(k), ptr(v), q_stride, kv_stride, ptr(q_norm),
+         ptr(k_norm), eps, ptr(positions), theta, n_tokens, tokens_per_stream, Hq, Hkv, Dh,
+         ptr(kpool), ptr(vpool), ptr(page_table), max_pages, page_size, capacity, _sh(stream))

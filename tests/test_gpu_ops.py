@@ -98,3 +98,31 @@ def test_argmax_banned_random_and_ties():
         y = np.zeros(2000, np.float32)
         y[idx] = 5.0
         assert _argmax_gpu(y) == orc.argmax_banned(y), idx
+
+
+def test_gqa_attention_fixture(golden):
+    """The reference's own GQA check: T=24, 16/8 heads, causal, max-abs 5e-4 against torch
+    SDPA (test/unit/model/test_asr_ops.cc:145-169)."""
+    q, k, v = golden["gqa_q"], golden["gqa_k"], golden["gqa_v"]
+    T, Hq, Dh = q.shape
+    Hkv = k.shape[1]
+    dout = empty(q.shape, np.float32)
+    say("gqa_attention fixture")
+    asr_ops.GqaAttention(up(q), up(k), up(v), dout, T, Hq, Hkv, Dh, 1.0 / np.sqrt(Dh), True)
+    got = down(dout, q.shape)
+    assert np.max(np.abs(got - golden["gqa_out"])) < 5e-4
+    assert rel_err(got, orc.gqa_attention(q, k, v, 1.0 / np.sqrt(Dh), True), 0.05) <= 1e-4
+
+
+@pytest.mark.parametrize("T,Hq,Hkv,Dh,causal", [(1, 16, 8, 128, True), (256, 16, 8, 128, True),
+                                               (100, 8, 8, 64, False), (300, 16, 4, 64, True),
+                                               (129, 16, 8, 128, False)])
+def test_gqa_attention_vs_oracle(T, Hq, Hkv, Dh, causal):
+    r = SplitMix64(T * 7 + Hkv)
+    q, k, v = r.normal((T, Hq, Dh), 0.3), r.normal((T, Hkv, Dh), 0.3), r.normal((T, Hkv, Dh))
+    scale = 1.0 / np.sqrt(Dh)
+    dout = empty(q.shape, np.float32)
+    say("gqa_attention", T, Hq, Hkv, Dh, causal)
+    asr_ops.GqaAttention(up(q), up(k), up(v), dout, T, Hq, Hkv, Dh, scale, causal)
+    ref = orc.gqa_attention(q, k, v, scale, causal)
+    assert rel_err(down(dout, q.shape), ref, 0.05) <= 1e-4
