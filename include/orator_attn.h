@@ -136,6 +136,37 @@ int orator_gqa_decode_paged(const float* q, const uint16_t* kpool, const uint16_
                             const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
                             float scale, void* stream);
 
+/* ----------------------------------------------------------------- GEMM ---- */
+/* gemm::LaunchSgemm (include/model/gemm.cuh:160-174): out[M,N] = act(in[M,K] W[N,K]^T + bias),
+ * act 0 none, 1 SiLU, 2 ReLU, 3 sigmoid (gemm.cuh:38-45); bias may be NULL. */
+int orator_sgemm(const float* in, const float* W, const float* bias, float* out, int M, int K,
+                 int N, int act, void* stream);
+/* gemm::LaunchSgemmBatched (include/model/gemm.cuh:251-268): per batch b,
+ * out+b*stride_out = act(in+b*stride_in . (W+b*stride_w)^T); any M, N, K, alignment. */
+int orator_sgemm_batched(const float* in, const float* W, float* out, int M, int K, int N, int act,
+                         int batch, long stride_in, long stride_w, long stride_out, void* stream);
+
+/* ----------------------------------------------------- Conformer rel-pos ---- */
+/* Attention core of ConformerLayer::Forward (src/model/conformer_layer.cu:405-444): q/k/v
+ * [T,H,Dk] (linear_q/k/v outputs), p [2T-1,H,Dk] (linear_pos of BuildPosEmb), u/v biases
+ * [H,Dk]; out [T,H,Dk] = softmax((AC + rel_shift(BD)) * scale, keys >= valid_len masked) . v,
+ * the context fed to linear_out.  fp32, reference decomposition (batched SGEMMs). */
+int orator_relpos_attention(const float* q, const float* k, const float* v, const float* p,
+                            const float* pos_bias_u, const float* pos_bias_v, float* out, int T,
+                            int H, int Dk, int valid_len, float scale, void* stream);
+
+/* Same attention core, fused on fp16 MFMA (one launch, no [H,T,2T-1] BD matrix): inputs
+ * fp16 bits (in_f16 = 1) or fp32 rounded to fp16 on load (in_f16 = 0); biases and output
+ * fp32; Dk = 64.  Max abs error ~1e-3 on unit-scale outputs (fp16 operands, fp32 accumulate). */
+int orator_relpos_attention_fast(const void* q, const void* k, const void* v, const void* p,
+                                 const float* pos_bias_u, const float* pos_bias_v, float* out,
+                                 int T, int H, int Dk, int valid_len, float scale, int in_f16,
+                                 void* stream);
+
+/* ConformerLayer::BuildPosEmb (src/model/conformer_layer.cu:314-329): HOST function filling
+ * pe [2T-1, d_model] (host memory) with the relative positional encoding. */
+int orator_build_pos_emb(float* pe, int T, int d_model);
+
 /* Prefill precision modes.
  * FP32: q enters the MFMA products as three bf16 terms and the softmax weights as two, so
  *       results track the fp32 reference (GqaCacheAttnKernel) to fp32 rounding level.

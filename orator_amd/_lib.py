@@ -70,6 +70,11 @@ SIGNATURES: dict[str, list] = {
     "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
     "orator_qk_norm_rope_kv_write": [_p, _p, _p, _l, _l, _p, _p, _f, _p, _f, _i, _i, _i, _i, _i,
                                      _p, _p, _p, _i, _i, _i, _p],
+    "orator_sgemm": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "orator_sgemm_batched": [_p, _p, _p, _i, _i, _i, _i, _i, _l, _l, _l, _p],
+    "orator_build_pos_emb": [_p, _i, _i],
+    "orator_relpos_attention_fast": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i, _p],
+    "orator_relpos_attention": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _p],
     "orator_gqa_prefill": [_p, _p, _p, _p, _i, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_prefill_ex": [_p, _p, _p, _p, _p, _i, _i, _p, _i, _i, _i, _i, _p, _i, _f, _i, _p],
 }

@@ -1,0 +1,38 @@
+"""The FastConformer layer's relative-position attention core (the block of
+ConformerLayer::Forward between linear_q/k/v/pos and linear_out,
+src/model/conformer_layer.cu:405-444) and BuildPosEmb (:314-329) over the HIP library."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from ._lib import call
+from .runtime import _sh, ptr
+
+
+def RelPosAttention(q, k, v, p, pos_bias_u, pos_bias_v, out, T: int, H: int, Dk: int,
+                    valid_len: int, scale: float | None = None, stream=None) -> None:
+    """out [T,H,Dk] = softmax((AC + rel_shift(BD)) * scale, keys >= valid masked) . v."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(Dk)
+    call("orator_relpos_attention", ptr(q), ptr(k), ptr(v), ptr(p), ptr(pos_bias_u),
+         ptr(pos_bias_v), ptr(out), T, H, Dk, valid_len, scale, _sh(stream))
+
+
+def RelPosAttentionFast(q, k, v, p, pos_bias_u, pos_bias_v, out, T: int, H: int, Dk: int,
+                        valid_len: int, scale: float | None = None, in_f16: bool = True,
+                        stream=None) -> None:
+    """Fused fp16-MFMA form of RelPosAttention (inputs fp16 bits, or fp32 if in_f16=False)."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(Dk)
+    call("orator_relpos_attention_fast", ptr(q), ptr(k), ptr(v), ptr(p), ptr(pos_bias_u),
+         ptr(pos_bias_v), ptr(out), T, H, Dk, valid_len, scale, int(bool(in_f16)), _sh(stream))
+
+
+def BuildPosEmb(T: int, d_model: int) -> np.ndarray:
+    """RelPositionalEncoding pos_emb [2T-1, d_model] for positions T-1 .. -(T-1), built on the
+    host by the library with the reference's float math (conformer_layer.cu:314-329)."""
+    pe = np.empty((max(2 * T - 1, 0), d_model), np.float32)
+    call("orator_build_pos_emb", pe.ctypes.data, T, d_model)
+    return pe

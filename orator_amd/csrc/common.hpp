@@ -75,6 +75,15 @@ __device__ __forceinline__ uint4 load_nt(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Orders LDS traffic between the lanes of ONE wave (wave-private LDS regions): the fences
+// make the compiler wait for this wave's LDS writes and keep later LDS reads after them.
+// Waves may run different trip counts, so a workgroup barrier would not be safe there.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
 // Raw v_exp_f32 (2^x); 2^-inf = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -53,4 +53,8 @@ struct DecodeProblem {
 };
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
 
+int launch_sgemm(const float* in, const float* W, const float* bias, float* out, int M, int K,
+                 int N, int act, int batch, long stride_in, long stride_w, long stride_out,
+                 hipStream_t stream);
+
 }  // namespace orator_hip

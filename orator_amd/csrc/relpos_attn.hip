@@ -1,0 +1,420 @@
+// FastConformer relative-position MHSA core (Transformer-XL u/v biases), gfx950.
+//
+// Replaces the attention block of ConformerLayer::Forward (src/model/conformer_layer.cu:405-444):
+//   AC[h,i,j] = (q_i + u_h) . k_j,   BD[h,i,m] = (q_i + v_h) . p_m  (m over 2T-1 rel. positions)
+//   score[h,i,j] = (AC[h,i,j] + BD[h,i,T-1-i+j]) * scale   for j < valid, else -1e30
+//   out[i,h,:] = softmax_j(score[h,i,:]) . v
+// q, k, v [T,H,Dk], p [2T-1,H,Dk] (linear_pos output), u, v_bias [H,Dk]; out [T,H,Dk]
+// (the context before linear_out).  BD[h,i,T-1-i+j] is the closed form of the reference's
+// rel_shift index arithmetic (RelShiftScoresKernel, :130-155).
+//
+// fp32 mode keeps the reference's decomposition -- head-major gathers, batched fp32 GEMMs
+// for AC, BD and the context -- so its arithmetic is the reference's up to summation
+// order; the rel-shift, mask, scale and row softmax are fused into one row kernel.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace orator_hip {
+namespace {
+
+// qu[h,t,d] = q[t,h,d] + u[h,d]; qv likewise with v_bias; kh[h,t,d] = k[t,h,d];
+// ph[h,m,d] = p[m,h,d]; vt[h,d,t] = v[t,h,d].
+__global__ __launch_bounds__(256) void relpos_gather_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ p, const float* __restrict__ u, const float* __restrict__ vb,
+    float* __restrict__ qu, float* __restrict__ qv, float* __restrict__ kh,
+    float* __restrict__ ph, float* __restrict__ vt, int T, int H, int Dk) {
+  const long n = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int P = 2 * T - 1;
+  const long ntd = static_cast<long>(H) * T * Dk;
+  const long npd = static_cast<long>(H) * P * Dk;
+  if (n < ntd) {
+    const int d = static_cast<int>(n % Dk);
+    const int t = static_cast<int>((n / Dk) % T);
+    const int h = static_cast<int>(n / (static_cast<long>(Dk) * T));
+    const long src = (static_cast<long>(t) * H + h) * Dk + d;
+    const float qq = q[src];
+    qu[n] = qq + u[h * Dk + d];
+    qv[n] = qq + vb[h * Dk + d];
+    kh[n] = k[src];
+    vt[(static_cast<long>(h) * Dk + d) * T + t] = v[src];
+  }
+  if (n < npd) {
+    const int d = static_cast<int>(n % Dk);
+    const int m = static_cast<int>((n / Dk) % P);
+    const int h = static_cast<int>(n / (static_cast<long>(Dk) * P));
+    ph[n] = p[(static_cast<long>(m) * H + h) * Dk + d];
+  }
+}
+
+// One workgroup per (h, i) row: score = (AC + BD[T-1-i+j]) * scale (j < valid), softmax in
+// place over the row, AttnSoftmaxKernel's max / exp / 1/sum order (:158-192).
+__global__ __launch_bounds__(256) void relpos_softmax_kernel(float* __restrict__ ac,
+                                                             const float* __restrict__ bd, int T,
+                                                             int valid, float scale) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;  // h*T + i
+  const int i = row % T;
+  const int P = 2 * T - 1;
+  float* s = ac + static_cast<long>(row) * T;
+  const float* bdr = bd + static_cast<long>(row) * P + (T - 1 - i);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float mx = -1e30f;
+  for (int j = tid; j < T; j += 256) {
+    const float x = j < valid ? (s[j] + bdr[j]) * scale : -1e30f;
+    s[j] = x;
+    mx = fmaxf(mx, x);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sum = 0.0f;
+  for (int j = tid; j < T; j += 256) {
+    const float e = expf(s[j] - mx);
+    s[j] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  const float inv = 1.0f / (red[0] + red[1] + red[2] + red[3]);
+  for (int j = tid; j < T; j += 256) s[j] *= inv;
+}
+
+// out[t,h,d] = ctx[h,t,d]
+__global__ __launch_bounds__(256) void relpos_scatter_kernel(const float* __restrict__ ctx,
+                                                             float* __restrict__ out, int T, int H,
+                                                             int Dk) {
+  const long n = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (n >= static_cast<long>(H) * T * Dk) return;
+  const int d = static_cast<int>(n % Dk);
+  const int t = static_cast<int>((n / Dk) % T);
+  const int h = static_cast<int>(n / (static_cast<long>(Dk) * T));
+  out[(static_cast<long>(t) * H + h) * Dk + d] = ctx[n];
+}
+
+inline int blocks(long n) { return static_cast<int>((n + 255) / 256); }
+
+int relpos_fp32(const float* q, const float* k, const float* v, const float* p, const float* u,
+                const float* vb, float* out, int T, int H, int Dk, int valid, float scale,
+                hipStream_t stream) {
+  const int P = 2 * T - 1;
+  const size_t td = static_cast<size_t>(H) * T * Dk, pd = static_cast<size_t>(H) * P * Dk;
+  const size_t tt = static_cast<size_t>(H) * T * T, tp = static_cast<size_t>(H) * T * P;
+  const size_t floats = 4 * td + pd + td /*vt*/ + tt + tp;
+  float* ws = static_cast<float*>(workspace(stream, floats * sizeof(float), 0));
+  if (!ws) return ORATOR_ERR_HIP;
+  float* qu = ws;
+  float* qv = qu + td;
+  float* kh = qv + td;
+  float* ctx = kh + td;
+  float* vt = ctx + td;
+  float* ph = vt + td;
+  float* ac = ph + pd;
+  float* bd = ac + tt;
+  hipLaunchKernelGGL(relpos_gather_kernel, dim3(blocks(static_cast<long>(pd > td ? pd : td))),
+                     dim3(256), 0, stream, q, k, v, p, u, vb, qu, qv, kh, ph, vt, T, H, Dk);
+  int rc = check_launch("relpos_gather");
+  if (rc) return rc;
+  rc = launch_sgemm(qu, kh, nullptr, ac, T, Dk, T, 0, H, static_cast<long>(T) * Dk,
+                    static_cast<long>(T) * Dk, static_cast<long>(T) * T, stream);
+  if (rc) return rc;
+  rc = launch_sgemm(qv, ph, nullptr, bd, T, Dk, P, 0, H, static_cast<long>(T) * Dk,
+                    static_cast<long>(P) * Dk, static_cast<long>(T) * P, stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(relpos_softmax_kernel, dim3(H * T), dim3(256), 0, stream, ac, bd, T, valid,
+                     scale);
+  rc = check_launch("relpos_softmax");
+  if (rc) return rc;
+  rc = launch_sgemm(ac, vt, nullptr, ctx, T, T, Dk, 0, H, static_cast<long>(T) * T,
+                    static_cast<long>(Dk) * T, static_cast<long>(T) * Dk, stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(relpos_scatter_kernel, dim3(blocks(static_cast<long>(td))), dim3(256), 0,
+                     stream, ctx, out, T, H, Dk);
+  return check_launch("relpos_scatter");
+}
+
+}  // namespace
+}  // namespace orator_hip
+
+using namespace orator_hip;
+
+extern "C" {
+
+int orator_relpos_attention(const float* q, const float* k, const float* v, const float* p,
+                            const float* pos_bias_u, const float* pos_bias_v, float* out, int T,
+                            int H, int Dk, int valid_len, float scale, void* stream) {
+  if (T <= 0 || H <= 0 || Dk <= 0) return ORATOR_OK;
+  if (!q || !k || !v || !p || !pos_bias_u || !pos_bias_v || !out)
+    return fail(ORATOR_ERR_INVALID, "relpos_attention: null pointer");
+  if (valid_len > T) valid_len = T;
+  return relpos_fp32(q, k, v, p, pos_bias_u, pos_bias_v, out, T, H, Dk, valid_len, scale,
+                     static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+// ===================================================================== fused fp16 path
+//
+// One workgroup = one (head, 32-query tile); its 4 wave64s split the key range (tiles of 32
+// keys, wave w takes tiles w, w+4, ...) and merge (max, sum, acc) through LDS at the end.
+// Per key tile and wave, on v_mfma_f32_32x32x16_f16 (S^T orientation, so the softmax
+// state is per lane = per query column):
+//   AC^T[j][i] = K[j] . (q_i + u)                  4 MFMAs
+//   R[r][i]    = P[base + r] . (q_i + v), r < 64   8 MFMAs, base = T-1-(i0+31)+j0
+//   BD^T[j][i] = R[j - i + 31][i]                  (the rel shift: R goes through LDS)
+//   O^T[d][i] += V^T[d][j] P^T[j][i]               4 MFMAs, V^T staged through LDS
+// so the BD band costs 2x the MFMA work of AC instead of a [H,T,2T-1] GEMM through HBM.
+// Inputs fp16 (or fp32 converted on load), u/v biases fp32, output fp32.
+namespace orator_hip {
+namespace {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kRpDk = 64;
+constexpr int kRpWaves = 4;
+constexpr int kVtRow = 32 + 8;   // V^T tile row (halves): 80 bytes
+constexpr int kRtRow = 64 + 1;   // R^T row (floats)
+
+__device__ __forceinline__ f16x8_t as_f16x8(uint4 u) { return __builtin_bit_cast(f16x8_t, u); }
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  const _Float16 ha = static_cast<_Float16>(a), hb = static_cast<_Float16>(b);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
+}
+
+// 8 consecutive elements as fp16 bits (converting fp32 input).
+template <typename IN>
+__device__ __forceinline__ uint4 load8_h(const IN* p) {
+  if constexpr (sizeof(IN) == 2) {
+    return *reinterpret_cast<const uint4*>(p);
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    return make_uint4(pack_h2(a.x, a.y), pack_h2(a.z, a.w), pack_h2(b.x, b.y), pack_h2(b.z, b.w));
+  }
+}
+
+template <typename IN>
+__device__ __forceinline__ void load8_f(const IN* p, float (&x)[8]) {
+  if constexpr (sizeof(IN) == 2) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[e] & 0xffffu)));
+      x[2 * e + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[e] >> 16)));
+    }
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  }
+}
+
+struct RelPosArgs {
+  const void *q, *k, *v, *p;
+  const float *u, *vb;
+  float* out;
+  int T, H, valid;
+  float scale_log2e;
+};
+
+template <typename IN>
+__global__ __launch_bounds__(256) void relpos_fused_kernel(RelPosArgs a) {
+  __shared__ uint16_t vt_lds[kRpWaves][kRpDk][kVtRow];
+  __shared__ float rt_lds[kRpWaves][32][kRtRow];
+  __shared__ float mo_lds[kRpWaves][2][32];
+  __shared__ float o_lds[kRpWaves][kRpDk][33];
+
+  const int h = blockIdx.x % a.H;
+  const int i0 = (blockIdx.x / a.H) * 32;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 31, h2 = lane >> 5;
+  const int T = a.T, H = a.H;
+  const long rs = static_cast<long>(H) * kRpDk;  // elements per token row
+  const IN* qp = static_cast<const IN*>(a.q);
+  const IN* kp = static_cast<const IN*>(a.k);
+  const IN* vp = static_cast<const IN*>(a.v);
+  const IN* pp = static_cast<const IN*>(a.p);
+
+  // (q_i + u) and (q_i + v) of this lane's query column, B operand per 16-dim k-step
+  const int qi = i0 + col;
+  const bool q_ok = qi < T;
+  uint4 qu[4], qv[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int d0 = 16 * ks + 8 * h2;
+    if (!q_ok) {
+      qu[ks] = qv[ks] = make_uint4(0, 0, 0, 0);
+      continue;
+    }
+    float x[8];
+    load8_f(qp + qi * rs + h * kRpDk + d0, x);
+    const float* ub = a.u + h * kRpDk + d0;
+    const float* vb = a.vb + h * kRpDk + d0;
+    qu[ks] = make_uint4(pack_h2(x[0] + ub[0], x[1] + ub[1]), pack_h2(x[2] + ub[2], x[3] + ub[3]),
+                        pack_h2(x[4] + ub[4], x[5] + ub[5]), pack_h2(x[6] + ub[6], x[7] + ub[7]));
+    qv[ks] = make_uint4(pack_h2(x[0] + vb[0], x[1] + vb[1]), pack_h2(x[2] + vb[2], x[3] + vb[3]),
+                        pack_h2(x[4] + vb[4], x[5] + vb[5]), pack_h2(x[6] + vb[6], x[7] + vb[7]));
+  }
+
+  f32x16_t o[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
+  float m = -INFINITY, lsum = 0.0f;
+  const int n_tiles = (a.valid + 31) / 32;
+  const int P = 2 * T - 1;
+
+  for (int n = wave; n < n_tiles; n += kRpWaves) {
+    const int j0 = 32 * n;
+    wave_lds_sync();  // the previous tile's LDS reads precede this tile's writes
+    // V^T tile -> wave-private LDS (8 b16 stores per 16-byte row piece)
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int key = 8 * it + (lane >> 3), dc = lane & 7;
+      const int j = j0 + key;
+      const uint4 w = j < T ? load8_h(vp + j * rs + h * kRpDk + 8 * dc) : make_uint4(0, 0, 0, 0);
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt_lds[wave][8 * dc + 2 * e][key] = static_cast<uint16_t>(ws[e] & 0xffffu);
+        vt_lds[wave][8 * dc + 2 * e + 1][key] = static_cast<uint16_t>(ws[e] >> 16);
+      }
+    }
+    // AC^T and R = P_window (q + v)^T
+    f32x16_t s, r0, r1;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = r0[e] = r1[e] = 0.0f;
+    const int jk = j0 + col;
+    const int base = T - 1 - (i0 + 31) + j0;
+    const int pr0 = base + col, pr1 = base + 32 + col;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int d0 = 16 * ks + 8 * h2;
+      const uint4 ka = jk < T ? load8_h(kp + jk * rs + h * kRpDk + d0) : make_uint4(0, 0, 0, 0);
+      const uint4 pa0 = (pr0 >= 0 && pr0 < P) ? load8_h(pp + static_cast<long>(pr0) * rs + h * kRpDk + d0)
+                                             : make_uint4(0, 0, 0, 0);
+      const uint4 pa1 = (pr1 >= 0 && pr1 < P) ? load8_h(pp + static_cast<long>(pr1) * rs + h * kRpDk + d0)
+                                             : make_uint4(0, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(ka), as_f16x8(qu[ks]), s, 0, 0, 0);
+      r0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(pa0), as_f16x8(qv[ks]), r0, 0, 0, 0);
+      r1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(pa1), as_f16x8(qv[ks]), r1, 0, 0, 0);
+    }
+    // R^T -> LDS; the lane's accumulator rows are 8i + 4*h2 + j (+32 for r1), column = col
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int rr = 8 * (e >> 2) + 4 * h2 + (e & 3);
+      rt_lds[wave][col][rr] = r0[e];
+      rt_lds[wave][col][32 + rr] = r1[e];
+    }
+    wave_lds_sync();  // R^T and V^T written by all lanes before any lane reads them
+    // scores: (AC + BD) * scale, key mask j >= valid, padding query columns masked
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
+      const float bd = rt_lds[wave][col][jl - col + 31];
+      const float x = (q_ok && j0 + jl < a.valid) ? (s[e] + bd) * a.scale_log2e : -INFINITY;
+      s[e] = x;
+      tmax = fmaxf(tmax, x);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mn = fmaxf(m, tmax);
+    const float mref = mn == -INFINITY ? 0.0f : mn;
+    const float corr = fast_exp2(m - mref);
+    m = mn;
+    float psum = 0.0f;
+    uint4 pk[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = fast_exp2(s[8 * st + e] - mref);
+        psum += pv[e];
+      }
+      pk[st] = make_uint4(pack_h2(pv[0], pv[1]), pack_h2(pv[2], pv[3]), pack_h2(pv[4], pv[5]),
+                          pack_h2(pv[6], pv[7]));
+    }
+    lsum = lsum * corr + psum;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const uint16_t* vr = &vt_lds[wave][32 * dt + col][16 * st + 4 * h2];
+        const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
+        const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(make_uint4(v0.x, v0.y, v1.x, v1.y)),
+                                                       as_f16x8(pk[st]), o[dt], 0, 0, 0);
+      }
+  }
+
+  // ---- merge the waves' partial softmax states ----
+  lsum += __shfl_xor(lsum, 32);
+  if (h2 == 0) {
+    mo_lds[wave][0][col] = m;
+    mo_lds[wave][1][col] = lsum;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      o_lds[wave][32 * dt + 8 * (e >> 2) + 4 * h2 + (e & 3)][col] = o[dt][e];
+  __syncthreads();
+  for (int idx = tid; idx < 32 * kRpDk; idx += 256) {
+    const int c = idx / kRpDk, d = idx % kRpDk;
+    const int i = i0 + c;
+    if (i >= T) continue;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kRpWaves; ++w) mx = fmaxf(mx, mo_lds[w][0][c]);
+    const float mr = mx == -INFINITY ? 0.0f : mx;
+    float ov = 0.0f, lv = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kRpWaves; ++w) {
+      const float wt = fast_exp2(mo_lds[w][0][c] - mr);
+      ov = fmaf(wt, o_lds[w][d][c], ov);
+      lv = fmaf(wt, mo_lds[w][1][c], lv);
+    }
+    a.out[(static_cast<long>(i) * H + h) * kRpDk + d] = lv > 0.0f ? ov / lv : 0.0f;
+  }
+}
+
+}  // namespace
+}  // namespace orator_hip
+
+extern "C" {
+
+int orator_relpos_attention_fast(const void* q, const void* k, const void* v, const void* p,
+                                 const float* pos_bias_u, const float* pos_bias_v, float* out,
+                                 int T, int H, int Dk, int valid_len, float scale, int in_f16,
+                                 void* stream) {
+  using namespace orator_hip;
+  if (T <= 0 || H <= 0 || Dk <= 0) return ORATOR_OK;
+  if (!q || !k || !v || !p || !pos_bias_u || !pos_bias_v || !out)
+    return fail(ORATOR_ERR_INVALID, "relpos_attention_fast: null pointer");
+  if (Dk != kRpDk) return fail(ORATOR_ERR_UNSUPPORTED, "relpos_attention_fast: Dk must be 64");
+  RelPosArgs args{q, k, v, p, pos_bias_u, pos_bias_v, out, T, H, valid_len > T ? T : valid_len,
+                  scale * 1.4426950408889634f};
+  const dim3 grid(((T + 31) / 32) * H);
+  if (in_f16)
+    hipLaunchKernelGGL(relpos_fused_kernel<_Float16>, grid, dim3(256), 0,
+                       static_cast<hipStream_t>(stream), args);
+  else
+    hipLaunchKernelGGL(relpos_fused_kernel<float>, grid, dim3(256), 0,
+                       static_cast<hipStream_t>(stream), args);
+  return check_launch("relpos_fused_kernel");
+}
+
+}  // extern "C"

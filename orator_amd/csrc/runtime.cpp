@@ -2,6 +2,7 @@
 // device-plumbing surface of the C ABI (allocation, copies, streams, events).
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <map>
 #include <mutex>
 #include <string>
@@ -161,6 +162,24 @@ int orator_event_elapsed_ms(float* ms, void* start, void* stop) {
   return check_hip(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
                                        static_cast<hipEvent_t>(stop)),
                    "hipEventElapsedTime");
+}
+
+// ConformerLayer::BuildPosEmb (src/model/conformer_layer.cu:314-329): host-side relative
+// positional encoding [2T-1, d_model] for positions T-1 .. -(T-1), evaluated with the float
+// overloads of std::exp / log / sin / cos as the reference does.
+int orator_build_pos_emb(float* pe, int T, int d_model) {
+  if (T <= 0 || d_model <= 0) return ORATOR_OK;
+  if (!pe) return fail(ORATOR_ERR_INVALID, "build_pos_emb: null pointer");
+  const int P = 2 * T - 1;
+  for (int idx = 0; idx < P; ++idx) {
+    const float pos = static_cast<float>(T - 1 - idx);
+    for (int i = 0; i < d_model; i += 2) {
+      const float div = std::exp(-(std::log(10000.0f)) * static_cast<float>(i) / d_model);
+      pe[static_cast<size_t>(idx) * d_model + i] = std::sin(pos * div);
+      if (i + 1 < d_model) pe[static_cast<size_t>(idx) * d_model + i + 1] = std::cos(pos * div);
+    }
+  }
+  return ORATOR_OK;
 }
 
 int orator_workspace_reserve(size_t bytes, void* stream) {

@@ -1,0 +1,91 @@
+"""GPU parity: batched SGEMM (gemm.cuh) and the Conformer rel-pos attention core against the
+oracle.  fp32 paths: max |g - r| / max(|r|, floor) <= 1e-4."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from gpu_helpers import down, empty, say, up
+from helpers import SplitMix64, rel_err
+from orator_amd import conformer_attn as ca
+from orator_amd import gemm
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,inner,cols,batch", [(13, 64, 13, 8), (14, 64, 14, 8)])
+def test_sgemm_batched_reference_test(rows, inner, cols, batch):
+    """test/unit/model/test_gemm_batched.cu:12-61: index%17/17 and index%13/13 inputs, f64
+    brute force, max-abs 1e-4."""
+    a = (np.arange(batch * rows * inner) % 17 / 17.0).astype(np.float32).reshape(batch, rows, inner)
+    w = (np.arange(batch * cols * inner) % 13 / 13.0).astype(np.float32).reshape(batch, cols, inner)
+    dout = empty((batch, rows, cols), np.float32)
+    say("sgemm_batched ref", rows, cols)
+    gemm.LaunchSgemmBatched(up(a), up(w), dout, rows, inner, cols, 0, batch, rows * inner,
+                            cols * inner, rows * cols)
+    ref = np.einsum("bmk,bnk->bmn", a.astype(np.float64), w.astype(np.float64))
+    assert np.max(np.abs(down(dout, (batch, rows, cols)) - ref)) < 1e-4
+
+
+@pytest.mark.parametrize("M,K,N,act", [(7, 13, 9, 0), (717, 512, 512, 0), (65, 64, 130, 1),
+                                       (100, 33, 70, 2), (5, 2048, 3, 3), (1433, 512, 512, 0)])
+def test_sgemm_bias_act_vs_oracle(M, K, N, act):
+    r = SplitMix64(M * 3 + K + N)
+    a, w, bias = r.normal((M, K)), r.normal((N, K), 1.0 / math.sqrt(K)), r.normal((N,))
+    dout = empty((M, N), np.float32)
+    say("sgemm", M, K, N, act)
+    gemm.LaunchSgemm(up(a), up(w), up(bias), dout, M, K, N, act)
+    got = down(dout, (M, N))
+    pre = a.astype(np.float64) @ w.astype(np.float64).T + bias
+    truth = {0: pre, 1: pre / (1 + np.exp(-pre)), 2: np.maximum(pre, 0), 3: 1 / (1 + np.exp(-pre))}[act]
+    assert np.max(np.abs(got - truth)) < 1e-4  # the reference's SGEMM gate
+    assert rel_err(got, orc.sgemm(a, w, bias, act), 1.0) <= 1e-5  # unit-scale outputs
+
+
+def _relpos_inputs(r, T, H, Dk):
+    return (r.normal((T, H, Dk)), r.normal((T, H, Dk)), r.normal((T, H, Dk)),
+            r.normal((2 * T - 1, H, Dk)), r.normal((H, Dk), 0.3), r.normal((H, Dk), 0.3))
+
+
+@pytest.mark.parametrize("T,valid", [(1, 1), (2, 2), (3, 2), (126, 125), (717, 717), (400, 333)])
+def test_relpos_fp32_vs_oracle(T, valid):
+    """Config-4 shape (T = 717: 340 chunk + 1 right context + 188 FIFO + 188 speaker cache),
+    the NeMo verification shape (T = 126, valid = 125, tools/verify/cc/verify_conformer.cc),
+    and tiny T where the rel-shift wraps."""
+    H, Dk = 8, 64
+    r = SplitMix64(T * 11 + valid)
+    q, k, v, p, u, vb = _relpos_inputs(r, T, H, Dk)
+    scale = 1.0 / math.sqrt(Dk)
+    ref = orc.relpos_attention(q, k, v, p, u, vb, valid, scale)
+    dout = empty(q.shape, np.float32)
+    say("relpos fp32", T, valid)
+    ca.RelPosAttention(up(q), up(k), up(v), up(p), up(u), up(vb), dout, T, H, Dk, valid, scale)
+    assert rel_err(down(dout, q.shape), ref, 0.05) <= 1e-4
+
+
+def _to_f16_bits(x):
+    return np.ascontiguousarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("T,valid,in_f16", [(717, 717, True), (717, 700, False), (126, 125, True),
+                                             (1, 1, True), (33, 20, True), (300, 300, False)])
+def test_relpos_fused_vs_oracle(T, valid, in_f16):
+    """Fused fp16-MFMA rel-pos attention (fp16 inputs N(0,1)).  fp16
+    operands with fp32 accumulation: max abs error <= 2e-2 on unit-scale outputs, judged
+    against the oracle run on the fp16-rounded inputs."""
+    H, Dk = 8, 64
+    r = SplitMix64(T * 13 + valid)
+    q, k, v, p, u, vb = _relpos_inputs(r, T, H, Dk)
+    q, k, v, p = (x.astype(np.float16).astype(np.float32) for x in (q, k, v, p))
+    scale = 1.0 / math.sqrt(Dk)
+    ref = orc.relpos_attention(q, k, v, p, u, vb, valid, scale)
+    dout = empty(q.shape, np.float32)
+    say("relpos fused", T, valid, in_f16)
+    ins = [up(_to_f16_bits(x)) if in_f16 else up(x) for x in (q, k, v, p)]
+    ca.RelPosAttentionFast(*ins, up(u), up(vb), dout, T, H, Dk, valid, scale, in_f16=in_f16)
+    got = down(dout, q.shape)
+    assert np.max(np.abs(got - ref)) <= 2e-2
+    assert np.max(np.abs(got - ref)) <= 5e-3  # observed class of fp16 rounding of q+u, q+v, P

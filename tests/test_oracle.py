@@ -434,3 +434,10 @@ def test_argmax_tie_rule():
     assert orc.argmax_banned(x) == 2
     # everything -inf: no slot ever updates, the reference returns index 0
     assert orc.argmax_banned(np.full(4, -np.inf, np.float32)) == 0
+
+
+def test_host_build_pos_emb_matches_oracle():
+    """orator_amd.conformer_attn.BuildPosEmb (host, like the reference's) vs the oracle."""
+    from orator_amd.conformer_attn import BuildPosEmb
+    for T, D in ((1, 512), (23, 512), (717, 512), (5, 7)):
+        np.testing.assert_array_equal(BuildPosEmb(T, D), orc.build_pos_emb(T, D))
