@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["decode", "prefill", "conformer", "sweep"], default=None,
+                    help="run one part (for profiling); prints that part's numbers only")
     return ap.parse_args()
 
 
@@ -57,6 +59,7 @@ def log(*a):
 
 def run_decode(steps: int, warmup: int):
     from orator_amd import decoder_attn as da
+    from orator_amd._lib import call
     from orator_amd.runtime import DeviceBuffer, Event, Stream, synchronize
 
     total_tok = L_BASE + warmup + steps + 1
@@ -78,7 +81,6 @@ def run_decode(steps: int, warmup: int):
         off = 0
         while off < buf.nbytes:
             n = min(dblock.nbytes, buf.nbytes - off)
-            from orator_amd._lib import call
             call("orator_memcpy_dtod", buf.ptr + off, dblock.ptr, n, stream.handle)
             off += n
         return buf
@@ -110,8 +112,9 @@ def run_decode(steps: int, warmup: int):
         for l in range(LAYERS):
             da.WriteKvCachePaged(ks[v], vs[v], kpools[l], vpools[l], tables[l], max_pages, PAGE,
                                  n_pages, B, 1, HKV, DH, pos_ptr, stream)
-            if evs is not None:
+            if evs is not None:  # the decode operation: split-K kernel + split merge kernel
                 evs[l][0].record(stream)
+                call("orator_time_next_decode", evs[l][2].handle, evs[l][3].handle)
             da.GqaDecodeAttnPaged(qs[v], kpools[l], vpools[l], tables[l], max_pages, PAGE, pos_ptr,
                                   outs, B, HQ, HKV, DH, scale, stream)
             if evs is not None:
@@ -140,8 +143,8 @@ def run_decode(steps: int, warmup: int):
 
     # ---- decode kernel launch durations (events on the launch stream) ----
     n_kstep = min(steps, 16)
-    evs = [(Event(), Event()) for _ in range(LAYERS)]
-    durs, kbytes = [], []
+    evs = [(Event(), Event(), Event(), Event()) for _ in range(LAYERS)]
+    durs, sdurs, kbytes = [], [], []
     for i in range(n_kstep):
         t = warmup + steps - n_kstep + i
         step(t, evs)
@@ -149,6 +152,7 @@ def run_decode(steps: int, warmup: int):
         S = L_BASE + t + 1
         for l in range(LAYERS):
             durs.append(evs[l][0].elapsed_ms(evs[l][1]))
+            sdurs.append(evs[l][2].elapsed_ms(evs[l][3]))
             kbytes.append(B * decode_bytes(S, (S + PAGE - 1) // PAGE))
     avg_ms = float(np.mean(durs))
     achieved = float(np.mean(kbytes)) / (avg_ms / 1e3) / 1e9
@@ -159,9 +163,149 @@ def run_decode(steps: int, warmup: int):
     return {
         "gpu_ms": gpu_ms, "wall_s": wall_s, "ms_per_step": elapsed_s * 1e3 / steps,
         "value_gbs": value_gbs, "kernel_avg_us": avg_ms * 1e3,
+        "split_kernel_avg_us": float(np.mean(sdurs)) * 1e3,
         "kernel_bytes": float(np.mean(kbytes)), "achieved_gbs": achieved,
         "max_pages": max_pages, "parity": parity,
     }
+
+
+def run_prefill(T: int, mode: int, iters: int = 20):
+    """Prefill attention over one layer's bf16 cache at pos0 = 0 (BASELINE configs[1] shape
+    for T = 503; T = 2048 is the throughput target), rotating over 4 layers' caches.
+    Returns the kernel's average time and algorithmic causal TFLOP/s, 4*Hq*Dh*T(T+1)/2."""
+    from orator_amd import decoder_attn as da
+    from orator_amd.runtime import DeviceBuffer, Event, Stream
+
+    rng = np.random.default_rng(T)
+    st = Stream()
+    nl = 4
+    bits = lambda shape: DeviceBuffer.from_array(
+        (rng.standard_normal(shape).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+    kc = [bits((T, HKV, DH)) for _ in range(nl)]
+    vc = [bits((T, HKV, DH)) for _ in range(nl)]
+    q = DeviceBuffer.from_array(rng.standard_normal((T, HQ, DH)).astype(np.float32))
+    qb = bits((T, HQ, DH))
+    out = DeviceBuffer(T * HQ * DH * 4)
+    pos = DeviceBuffer.from_array(np.zeros(1, np.int32))
+    scale = 1.0 / math.sqrt(DH)
+
+    def run(l):
+        if mode == da.PREFILL_BF16:
+            da.GqaCacheAttnEx(None, qb, kc[l], vc[l], None, 0, 0, out, T, HQ, HKV, DH, pos, T,
+                              scale, mode, st)
+        else:
+            da.GqaCacheAttnEx(q, None, kc[l], vc[l], None, 0, 0, out, T, HQ, HKV, DH, pos, T,
+                              scale, mode, st)
+
+    for l in range(nl):
+        run(l)
+    st.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(st)
+    for i in range(iters):
+        run(i % nl)
+    e1.record(st)
+    st.synchronize()
+    us = e0.elapsed_ms(e1) * 1e3 / iters
+    flops = 4.0 * HQ * DH * T * (T + 1) / 2
+    tf = flops / (us * 1e-6) / 1e12
+    return {"T": T, "mode": "bf16" if mode == da.PREFILL_BF16 else "fp32", "us": round(us, 2),
+            "tflops": round(tf, 2), "frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
+
+
+def run_conformer(T: int = 717, layers: int = 17, H: int = 8, Dk: int = 64):
+    """17 back-to-back rel-pos MHSA cores, T = 717, fp16 inputs N(0,1),
+    non-causal.  Algorithmic flops 6*H*T^2*Dk per layer (AC, the used BD band, PV)."""
+    from orator_amd import conformer_attn as ca
+    from orator_amd.runtime import DeviceBuffer, Event, Stream
+
+    rng = np.random.default_rng(4)
+    st = Stream()
+    f16 = lambda shape: DeviceBuffer.from_array(
+        rng.standard_normal(shape).astype(np.float16).view(np.uint16))
+    f32 = lambda shape: DeviceBuffer.from_array(rng.standard_normal(shape).astype(np.float32))
+    P = 2 * T - 1
+    ins = [(f16((T, H, Dk)), f16((T, H, Dk)), f16((T, H, Dk)), f16((P, H, Dk))) for _ in range(layers)]
+    ins32 = [f32((T, H, Dk)), f32((T, H, Dk)), f32((T, H, Dk)), f32((P, H, Dk))]
+    u, vb = f32((H, Dk)), f32((H, Dk))
+    out = DeviceBuffer(T * H * Dk * 4)
+    scale = 1.0 / math.sqrt(Dk)
+    for l in range(layers):
+        ca.RelPosAttentionFast(*ins[l], u, vb, out, T, H, Dk, T, scale, True, st)
+    ca.RelPosAttention(*ins32, u, vb, out, T, H, Dk, T, scale, st)
+    st.synchronize()
+    e0, e1, e2 = Event(), Event(), Event()
+    reps = 5
+    e0.record(st)
+    for _ in range(reps):
+        for l in range(layers):
+            ca.RelPosAttentionFast(*ins[l], u, vb, out, T, H, Dk, T, scale, True, st)
+    e1.record(st)
+    for _ in range(reps):
+        ca.RelPosAttention(*ins32, u, vb, out, T, H, Dk, T, scale, st)
+    e2.record(st)
+    st.synchronize()
+    us_f16 = e0.elapsed_ms(e1) * 1e3 / (reps * layers)
+    us_f32 = e1.elapsed_ms(e2) * 1e3 / reps
+    flops = 6.0 * H * T * T * Dk
+    tf = flops / (us_f16 * 1e-6) / 1e12
+    return {"T": T, "layers": layers, "fused_f16_us_per_layer": round(us_f16, 2),
+            "fused_f16_tflops": round(tf, 2), "frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+            "stack_ms": round(us_f16 * layers / 1e3, 4),
+            "fp32_reference_order_us_per_layer": round(us_f32, 2)}
+
+
+def run_decode_sweep():
+    """BASELINE configs[2] sweep: decode kernel GB/s at L in {1024, 2048, 4096}, B in {1, 16}
+    (one launch per layer over 28 layers' paged caches)."""
+    from orator_amd import decoder_attn as da
+    from orator_amd._lib import call
+    from orator_amd.runtime import DeviceBuffer, Event, Stream
+
+    st = Stream()
+    rng = np.random.default_rng(9)
+    block = (rng.standard_normal(1 << 22).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    dblock = DeviceBuffer.from_array(block)
+    res = []
+    for B_ in (1, 16):
+        for L in (1024, 2048, 4096):
+            S = L + 1
+            mp = (S + PAGE - 1) // PAGE
+            npg = B_ * mp
+            elems = npg * PAGE * HKV * DH
+            nl = 28
+            pools = []
+            for _ in range(2 * nl):
+                buf = DeviceBuffer(elems * 2)
+                off = 0
+                while off < buf.nbytes:
+                    n = min(dblock.nbytes, buf.nbytes - off)
+                    call("orator_memcpy_dtod", buf.ptr + off, dblock.ptr, n, st.handle)
+                    off += n
+                pools.append(buf)
+            tab = DeviceBuffer.from_array(rng.permutation(npg).astype(np.int32).reshape(B_, mp))
+            q = DeviceBuffer.from_array(rng.standard_normal((B_, HQ, DH)).astype(np.float32))
+            out = DeviceBuffer(B_ * HQ * DH * 4)
+            pos = DeviceBuffer.from_array(np.full(B_, S - 1, np.int32))
+            run = lambda l: da.GqaDecodeAttnPaged(q, pools[2 * l], pools[2 * l + 1], tab, mp, PAGE,
+                                                  pos, out, B_, HQ, HKV, DH, 0.0884, st)
+            for l in range(nl):
+                run(l)
+            st.synchronize()
+            e0, e1 = Event(), Event()
+            e0.record(st)
+            for r in range(3):
+                for l in range(nl):
+                    run(l)
+            e1.record(st)
+            st.synchronize()
+            us = e0.elapsed_ms(e1) * 1e3 / (3 * nl)
+            gbs = B_ * decode_bytes(S, mp) / (us * 1e-6) / 1e9
+            res.append({"B": B_, "L": L, "us_per_layer": round(us, 2), "GBs": round(gbs, 1),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "footprint_MB": round(nl * B_ * decode_bytes(S, mp) / 1e6, 1)})
+            del pools
+    return res
 
 
 def spot_check(kpool, vpool, table, max_pages, qs, outs, last_pos, var, scale):
@@ -241,9 +385,25 @@ def main():
         sys.exit(2)
     from orator_amd.runtime import device_name
     log("device:", device_name())
+    if args.only:
+        from orator_amd import decoder_attn as da
+        part = {"decode": lambda: run_decode(args.steps, args.warmup),
+                "prefill": lambda: [run_prefill(503, da.PREFILL_BF16),
+                                    run_prefill(2048, da.PREFILL_BF16)],
+                "conformer": run_conformer, "sweep": run_decode_sweep}[args.only]()
+        print(json.dumps({"only": args.only, "result": part}, default=float))
+        return
     dec = run_decode(args.steps, args.warmup)
     log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value_gbs']:.1f} GB/s; kernel "
         f"{dec['kernel_avg_us']:.1f} us avg -> {dec['achieved_gbs']:.1f} GB/s; parity {dec['parity']}")
+    from orator_amd import decoder_attn as da
+    pre = [run_prefill(503, da.PREFILL_BF16), run_prefill(503, da.PREFILL_FP32),
+           run_prefill(2048, da.PREFILL_BF16), run_prefill(2048, da.PREFILL_FP32)]
+    log("prefill:", pre)
+    conf = run_conformer()
+    log("conformer:", conf)
+    sweep = run_decode_sweep()
+    log("decode sweep:", sweep)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": "GQA decode-attn HBM GB/s (% peak); prefill-attn TFLOP/s (% MFMA peak)",
@@ -265,10 +425,15 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gqa_decode_kernel", "kernel_avg_us": round(dec["kernel_avg_us"], 2),
+                     "kernel": "gqa_decode = gqa_decode_kernel (split-K) + gqa_decode_combine_kernel",
+                     "kernel_avg_us": round(dec["kernel_avg_us"], 2),
+                     "split_kernel_avg_us": round(dec["split_kernel_avg_us"], 2),
                      "bytes_per_launch": int(dec["kernel_bytes"])},
         "cpu_baseline": cpu,
         "parity": dec["parity"],
+        "prefill": pre,
+        "conformer_relpos": conf,
+        "decode_sweep": sweep,
     }
     print(json.dumps(line))
 

@@ -65,9 +65,12 @@ int orator_event_create(void** event);
 int orator_event_destroy(void* event);
 int orator_event_record(void* event, void* stream);
 int orator_event_elapsed_ms(float* ms, void* start, void* stop);
-/* Pre-sizes the library workspace of `stream` (used by the split-K decode combine)
- * so that later calls do not allocate, e.g. before hipGraph capture. */
+/* Pre-sizes the library workspace of `stream` (split-K decode partials, rel-pos fp32
+ * intermediates) so that later calls do not allocate, e.g. before hipGraph capture. */
 int orator_workspace_reserve(size_t bytes, void* stream);
+/* Measurement hook (this thread): the next decode call records `start` before and `stop`
+ * after its split kernel on the launch stream, so that kernel alone can be timed. */
+int orator_time_next_decode(void* start, void* stop);
 
 /* ------------------------------------------------------- asr_ops family ---- */
 /* asr_ops::RmsNorm (include/model/asr_ops.cuh:21-25; src/model/asr_ops.cu:21-51,199-204).

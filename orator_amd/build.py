@@ -72,6 +72,22 @@ def build_hip(jobs: int | None = None) -> Path:
     return LIB
 
 
+CPP_TEST_SRC = ROOT / "tests" / "cpp" / "test_asr_ops.cc"
+CPP_TEST_BIN = ROOT / "tests" / "cpp" / "test_asr_ops"
+
+
+def build_cpp_tests() -> Path:
+    """The C++ drop-in header exercised by a host program (g++, links the library)."""
+    cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__",
+           "-I", str(ROOT / "include"), "-I", "/opt/rocm/include", str(CPP_TEST_SRC),
+           "-o", str(CPP_TEST_BIN), f"-L{PKG}", "-lorator_attn", "-Wl,-rpath,$ORIGIN/../../orator_amd",
+           f"-L{ROCM_LIB}", "-lamdhip64", f"-Wl,-rpath,{ROCM_LIB}"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"C++ test build failed:\n{proc.stdout}{proc.stderr}")
+    return CPP_TEST_BIN
+
+
 def build_oracle() -> Path:
     make = shutil.which("make")
     if make is None:
@@ -85,6 +101,7 @@ def build_oracle() -> Path:
 def build_all() -> None:
     build_oracle()
     build_hip()
+    build_cpp_tests()
 
 
 if __name__ == "__main__":

@@ -399,8 +399,12 @@ __global__ __launch_bounds__(128) void gqa_decode_combine_kernel(DecodeArgs a, i
 template <int DH, int G, int SPLIT, typename KV>
 int launch_split(const DecodeArgs& args, int B, hipStream_t stream) {
   dim3 grid(args.max_splits, args.Hkv, B);
+  hipEvent_t ev0, ev1;
+  take_timing_events(&ev0, &ev1);
+  if (ev0) (void)hipEventRecord(ev0, stream);
   hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV>), grid, dim3(256), 0, stream, args);
   int rc = check_launch("gqa_decode_kernel");
+  if (ev1) (void)hipEventRecord(ev1, stream);
   if (rc || args.max_splits <= 1) return rc;
   hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(128), 0, stream,
                      args, SPLIT, args.Hkv * G);

@@ -25,7 +25,6 @@ int check_launch(const char* what);
 // every kernel that uses them leaves them zero again.  Returns nullptr on failure
 // (the error is recorded).
 void* workspace(hipStream_t stream, size_t bytes, size_t counter_bytes);
-constexpr size_t kCounterBytes = 1u << 18;  // 64 Ki uint32 counters
 
 inline int ilog2_exact(int v) {
   if (v <= 0 || (v & (v - 1))) return -1;
@@ -33,6 +32,10 @@ inline int ilog2_exact(int v) {
   while ((1 << s) < v) ++s;
   return s;
 }
+
+// Optional measurement hook: when set, the next decode launch records `start` right before
+// and `stop` right after its split kernel (on the launch stream), then clears the hook.
+void take_timing_events(hipEvent_t* start, hipEvent_t* stop);
 
 // ---- launchers (defined in the .hip files) ----
 struct DecodeProblem {

@@ -21,7 +21,14 @@ struct Block {
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Block> g_ws;
+thread_local hipEvent_t g_ev_start = nullptr, g_ev_stop = nullptr;
 }  // namespace
+
+void take_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+  *start = g_ev_start;
+  *stop = g_ev_stop;
+  g_ev_start = g_ev_stop = nullptr;
+}
 
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
@@ -182,12 +189,15 @@ int orator_build_pos_emb(float* pe, int T, int d_model) {
   return ORATOR_OK;
 }
 
+int orator_time_next_decode(void* start, void* stop) {
+  orator_hip::g_ev_start = static_cast<hipEvent_t>(start);
+  orator_hip::g_ev_stop = static_cast<hipEvent_t>(stop);
+  return ORATOR_OK;
+}
+
 int orator_workspace_reserve(size_t bytes, void* stream) {
-  const size_t total = bytes + orator_hip::kCounterBytes;
-  return orator_hip::workspace(static_cast<hipStream_t>(stream), total,
-                               orator_hip::kCounterBytes)
-             ? ORATOR_OK
-             : ORATOR_ERR_HIP;
+  return orator_hip::workspace(static_cast<hipStream_t>(stream), bytes, 0) ? ORATOR_OK
+                                                                           : ORATOR_ERR_HIP;
 }
 
 }  // extern "C"
