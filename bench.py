@@ -35,6 +35,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
 
 LAYERS, B, HQ, HKV, DH, L_BASE, PAGE = 28, 16, 16, 8, 128, 4096, 16
+HBM_TRAFFIC_PER_OP = 274.0e6  # bytes, measured with rocprofv3 --pmc (profiles/decode_b16_l4096_hbm_traffic.md)
 
 
 def parse():
@@ -424,7 +425,11 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4),
+                     # rocprofv3 FETCH_SIZE x 1.993 + WRITE_SIZE x 1.0 KiB per decode op
+                     # (split + merge kernels) at this workload, S = 4102.
+                     "traffic": HBM_TRAFFIC_PER_OP,
+                     "traffic_over_algorithmic": round(HBM_TRAFFIC_PER_OP / dec["kernel_bytes"], 3),
                      "kernel": "gqa_decode = gqa_decode_kernel (split-K) + gqa_decode_combine_kernel",
                      "kernel_avg_us": round(dec["kernel_avg_us"], 2),
                      "split_kernel_avg_us": round(dec["split_kernel_avg_us"], 2),

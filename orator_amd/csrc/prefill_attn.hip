@@ -11,17 +11,28 @@
 //    the softmax weights as two (hi + lo, ~2^-17 relative); K/V are exact in bf16, so QK is
 //    fp32-exact and PV within ~1e-6 of the fp32 reference, at 2.5x the MFMA work.
 //
-// Tiling (one workgroup = 4 wave64s = 128 query rows = 64 tokens x 2 heads of one GQA
-// group; K/V tiles of 64 keys shared by both heads through LDS):
+// Work split (one workgroup = 8 wave64s = a block of 32 query rows x 2 waves, i.e. 64 query
+// rows = 32 tokens x 2 heads of one GQA group, and 4 key groups):
+//  * key group g of the workgroup takes the 32-key tiles g, g+4, g+8, ... of the block's
+//    causal key range with its own double-buffered LDS tiles; the 4 partial softmax states
+//    are merged through LDS at the end.  Two waves per SIMD (<= 256 VGPRs each) let one
+//    wave's softmax VALU run under the other's MFMAs, and 32-token blocks give ~2x more
+//    workgroups than CUs, so heaviest-first dispatch evens out the causal triangle.
 //  * S^T = K Q^T: K tile rows are the MFMA A operand (ds_read_b128 from a padded,
 //    conflict-free LDS layout), the wave's 32 query columns stay in registers as B.  In the
 //    32x32 accumulator layout every lane owns ONE query column and 16 keys, so the row
-//    max / sum of the online softmax are in-lane plus one lane exchange (xor 32).
+//    max / sum of the online softmax are in-lane plus one exchange between lane halves.
+//  * S^T of the next tile is issued before the softmax of the current one, so the MFMAs of
+//    one overlap the VALU of the other inside a wave too.
+//  * the running max is a stale reference: it is only moved (and O, l rescaled) when a new
+//    score exceeds it by more than 2^8, so weights stay <= 256 and most tiles skip the
+//    64-register rescale.  Softmax is invariant to the reference, so this is exact.
 //  * O^T += V^T P^T: P^T comes straight from the S^T accumulators (no LDS round trip);
-//    V^T is read from an LDS copy of the tile that is transposed while it is stored.
-//  * K/V tiles are re-read by every token block of the head, so they use plain (L2-
-//    cached) loads; the next tile is loaded from HBM into registers while the current one is
-//    multiplied, then stored to the other LDS buffer (double buffering, one barrier/tile).
+//    V stays row-major in LDS and the V^T operand is read with ds_read_b64_tr_b16 (a
+//    transposing LDS read), so no VALU work transposes V; 288-byte rows keep both the
+//    16-byte stores and the transposing reads conflict-free.
+//  * the next tile is loaded from HBM/L2 into registers a full round ahead of its LDS
+//    store (one barrier per round).
 //  * workgroups are ordered heaviest (latest tokens, most keys) first, and the kv head is
 //    the fastest-varying index, so each kv head's workgroups share an XCD (blockIdx % 8).
 #include "common.hpp"
@@ -31,13 +42,21 @@ namespace orator_hip {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kDh = 128;
-constexpr int kBN = 64;              // keys per tile
-constexpr int kKRow = kDh + 8;       // padded K row (bf16 elements): 272 bytes
-constexpr int kVRow = kBN + 8;       // padded V^T row: 144 bytes
-constexpr int kMaxRowGroups = 1024;  // page-row table: up to 16384 keys
+constexpr int kBN = 32;                              // keys per tile
+constexpr int kGroups = 4;                           // key groups per workgroup
+constexpr int kRowWaves = 2;                         // query-row waves per key group
+constexpr int kGroupThreads = 64 * kRowWaves;        // 128
+constexpr int kThreads = kGroupThreads * kGroups;    // 512
+constexpr int kKRow = kDh + 8;                       // padded K row (bf16 elements): 272 B
+constexpr int kVRow = kDh + 16;                      // padded V row (bf16 elements): 288 B
+constexpr int kMaxRowGroups = 1024;                  // page-row table: up to 16384 keys
+constexpr float kStaleMax = 8.0f;                    // log2 slack of the reference max
 
 struct PrefillArgs {
   const float* q;         // [Tq, Hq, Dh] fp32, or
@@ -51,13 +70,57 @@ struct PrefillArgs {
   int Tq, Hq, Hkv;
   int capacity;
   int n_tblocks;
-  float scale_log2e;
+  float scale_log2e;      // > 0
 };
+
+// One key group's LDS: double-buffered K and V rows.
+struct GroupTiles {
+  uint16_t k[2][kBN][kKRow];
+  uint16_t v[2][kBN][kVRow];
+};
+constexpr int kTileBytes = kGroups * static_cast<int>(sizeof(GroupTiles));          // 143360
+constexpr int kMergeBytes = 8 * 64 * 64 * 4 + 8 * 2 * 64 * 4;                        // 135168
+static_assert(kMergeBytes <= kTileBytes, "merge area reuses the tile buffers");
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
 __device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Two fp32 -> two RNE bf16 in one dword (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Sum of the two bf16 halves of w, added to acc (v_dot2_f32_bf16 against (1, 1)).
+__device__ __forceinline__ float add_bf16x2(uint32_t w, float acc) {
+  const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), ones, acc, false);
+}
+
+// Value of the lane 32 apart combined with this lane's: returns (this, partner) halves.
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element (i & 3) of the
+// 8 bytes addressed by lane 4k + (i >> 2), for k = 0..3.  With lane s of the group pointing at
+// row r0 + (s >> 2), columns c0 + 4 (s & 3) .. +3 of a row-major bf16 tile, lane i therefore
+// gets column c0 + i of rows r0 .. r0 + 3: a transposed 4 x 16 block.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+  const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p));
+  return __builtin_bit_cast(uint2, r);
 }
 
 // Splits 8 fp32 into bf16 hi (RNE) and the bf16 of the remainder (x - hi is exact in fp32).
@@ -76,11 +139,10 @@ __device__ __forceinline__ void split8(float (&x)[8], uint4& hi, uint4& lo) {
 }
 
 template <int G, bool PRECISE>
-__global__ __launch_bounds__(256) void gqa_prefill_kernel(PrefillArgs a) {
-  constexpr int TW = 32 / G;   // tokens per wave (32 query columns = TW tokens x G heads)
-  constexpr int BT = 4 * TW;   // tokens per workgroup
-  __shared__ uint16_t k_lds[2][kBN][kKRow];
-  __shared__ uint16_t vt_lds[2][kDh][kVRow];
+__global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
+  constexpr int TW = 32 / G;          // tokens per wave (32 query columns = TW tokens x G heads)
+  constexpr int BT = kRowWaves * TW;  // tokens per workgroup
+  __shared__ __align__(16) unsigned char smem[kTileBytes];
   __shared__ int row_lds[kMaxRowGroups];
 
   const int kvh = blockIdx.x % a.Hkv;
@@ -88,18 +150,26 @@ __global__ __launch_bounds__(256) void gqa_prefill_kernel(PrefillArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int h2 = lane >> 5;     // which half of the 32x32 accumulator rows this lane holds
-  const int col = lane & 31;    // this lane's query column
+  const int grp = __builtin_amdgcn_readfirstlane(wave >> 1);  // key group (wave-uniform)
+  const int rw = wave & 1;                                     // query-row wave of the group
+  const int gt = tid & (kGroupThreads - 1);  // thread index within the group
+  const int h2 = lane >> 5;   // which half of the 32x32 accumulator rows this lane holds
+  const int col = lane & 31;  // this lane's query column
   const int pos0 = *a.pos0p;
+  GroupTiles& tl = reinterpret_cast<GroupTiles*>(smem)[grp];
 
   const int t_blk = tblock * BT;
   const int t_end = min(t_blk + BT, a.Tq);
   const int n_keys = min(pos0 + t_end, a.capacity);  // keys [0, n_keys) are needed
   const int n_tiles = (n_keys + kBN - 1) / kBN;
+  const int n_rounds = (n_tiles + kGroups - 1) / kGroups;
+  const int my_tiles = n_tiles > grp ? (n_tiles - grp + kGroups - 1) / kGroups : 0;
+  // tiles with a key beyond this need the causal / capacity mask
+  const int mask_from = min(pos0 + t_blk, n_keys - 1);
 
   // ---- page rows of the needed keys (16-key groups) ----
-  const int n_groups = (n_keys + 15) >> 4;
-  for (int gi = tid; gi < n_groups; gi += 256) {
+  const int n_rowgroups = (n_keys + 15) >> 4;
+  for (int gi = tid; gi < n_rowgroups; gi += kThreads) {
     int row = gi << 4;
     if (a.page_table) {
       const int j0 = gi << 4;
@@ -110,10 +180,10 @@ __global__ __launch_bounds__(256) void gqa_prefill_kernel(PrefillArgs a) {
   }
 
   // ---- this wave's query columns: token tq, head hq ----
-  const int tq = t_blk + wave * TW + (col % TW);
+  const int tq = t_blk + rw * TW + (col % TW);
   const int hq = kvh * G + col / TW;
   const bool q_valid = tq < a.Tq;
-  const int q_lim = pos0 + tq;  // last key this column may attend
+  const int q_lim = min(pos0 + tq, n_keys - 1);  // last key this column may attend
   // B operand per 16-dim k-step (dims 16ks + 8*h2 + e).  fp32 mode carries q as three bf16
   // terms hi + mid + lo (exact to fp32 rounding); bf16 mode uses hi only.
   uint4 qhi[8], qmid[8], qlo[8];
@@ -137,52 +207,77 @@ __global__ __launch_bounds__(256) void gqa_prefill_kernel(PrefillArgs a) {
   }
   __syncthreads();  // row_lds ready
 
-  // ---- tile loader: K rows as 16-byte chunks, V as key pairs for the transposed store ----
-  const long rs = static_cast<long>(a.Hkv) * kDh;
+  // ---- tile loader (group-local tile j = key tile grp + kGroups*j) ----
+  // K and V rows 8p + ld_row (p = 0..3), one 16-byte chunk (dims 8*ld_chunk..) per thread;
+  // with the padded rows the LDS stores are conflict-free.
+  const long rs = static_cast<long>(a.Hkv) * kDh;  // elements between consecutive rows
   const uint16_t* kbase = a.kpool + static_cast<long>(kvh) * kDh;
   const uint16_t* vbase = a.vpool + static_cast<long>(kvh) * kDh;
-  uint4 kreg[4], vreg[2][2];
-  auto load_tile = [&](int n) {
-    const int k0 = n * kBN;
+  const int ld_row = gt >> 4, ld_chunk = gt & 15;
+  const uint32_t lane_off = static_cast<uint32_t>((ld_row * rs + 8 * ld_chunk) * 2);  // bytes
+  const long rs2 = rs * 2;
+  // Row of `key` (clamped to the last needed key, so every load stays in bounds).
+  auto row_clamped = [&](int key) -> long {
+    key = min(key, n_keys - 1);
+    return static_cast<long>(row_lds[key >> 4] + (key & 15));
+  };
+  auto load_rows = [&](const uint16_t* base, int j, u32x4_t (&r)[4]) {
+    const int k0 = (grp + kGroups * j) * kBN;  // uniform
+    if (k0 + kBN <= n_keys) {
+      // whole tile valid: two 16-row groups with uniform bases
+      const long rg0 = __builtin_amdgcn_readfirstlane(row_lds[k0 >> 4]);
+      const long rg1 = __builtin_amdgcn_readfirstlane(row_lds[(k0 >> 4) + 1]);
+      const char* b0 = reinterpret_cast<const char*>(base + rg0 * rs) + lane_off;
+      const char* b1 = reinterpret_cast<const char*>(base + rg1 * rs) + lane_off;
+      r[0] = *reinterpret_cast<const u32x4_t*>(b0);
+      r[1] = *reinterpret_cast<const u32x4_t*>(b0 + 8 * rs2);
+      r[2] = *reinterpret_cast<const u32x4_t*>(b1);
+      r[3] = *reinterpret_cast<const u32x4_t*>(b1 + 8 * rs2);
+    } else {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {  // 16 keys per pass, 16 lanes per 256-byte row
-      const int key = k0 + 16 * p + (tid >> 4);
-      kreg[p] = key < n_keys ? *reinterpret_cast<const uint4*>(
-                                   kbase + (row_lds[key >> 4] + (key & 15)) * rs + 8 * (tid & 15))
-                             : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {  // key pair kp, 8 dims at 8*dc
-      const int kp = 16 * u + (tid >> 4);
-      const int key = k0 + 2 * kp;
-      const int dc = tid & 15;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        vreg[u][t] = key + t < n_keys
-                         ? *reinterpret_cast<const uint4*>(
-                               vbase + (row_lds[(key + t) >> 4] + ((key + t) & 15)) * rs + 8 * dc)
-                         : make_uint4(0, 0, 0, 0);
+      for (int p = 0; p < 4; ++p)
+        r[p] = *reinterpret_cast<const u32x4_t*>(
+            base + row_clamped(k0 + 8 * p + ld_row) * rs + 8 * ld_chunk);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto load_k = [&](int j, u32x4_t (&r)[4]) { load_rows(kbase, j, r); };
+  auto load_v = [&](int j, u32x4_t (&r)[4]) { load_rows(vbase, j, r); };
+  auto store_k = [&](int buf, const u32x4_t (&r)[4]) {
 #pragma unroll
     for (int p = 0; p < 4; ++p)
-      *reinterpret_cast<uint4*>(&k_lds[buf][16 * p + (tid >> 4)][8 * (tid & 15)]) = kreg[p];
+      *reinterpret_cast<u32x4_t*>(&tl.k[buf][8 * p + ld_row][8 * ld_chunk]) = r[p];
+  };
+  // Keys past the end are stored as zeros in V: their weights are 0, and 0 * inf must not
+  // occur.  (Keys past the end in K need nothing: their scores are replaced by the mask.)
+  auto store_v = [&](int buf, u32x4_t (&r)[4], int j) {
+    const int k0 = (grp + kGroups * j) * kBN;
+    if (k0 + kBN > n_keys) {  // uniform over the group
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int kp = 16 * u + (tid >> 4);
-      const int dc = tid & 15;
-      const uint32_t w0[4] = {vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w};
-      const uint32_t w1[4] = {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // dims 8dc+2e (low halves) and 8dc+2e+1 (high halves) of keys 2kp, 2kp+1
-        const uint32_t lo = (w0[e] & 0xffffu) | (w1[e] << 16);
-        const uint32_t hi = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
-        *reinterpret_cast<uint32_t*>(&vt_lds[buf][8 * dc + 2 * e][2 * kp]) = lo;
-        *reinterpret_cast<uint32_t*>(&vt_lds[buf][8 * dc + 2 * e + 1][2 * kp]) = hi;
-      }
+      for (int p = 0; p < 4; ++p)
+        if (k0 + 8 * p + ld_row >= n_keys) r[p] = u32x4_t{0, 0, 0, 0};
     }
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      *reinterpret_cast<u32x4_t*>(&tl.v[buf][8 * p + ld_row][8 * ld_chunk]) = r[p];
+  };
+
+  // S^T (32 keys x this wave's 32 query columns) of the tile in K buffer `buf`.
+  auto qk = [&](int buf) {
+    f32x16_t s = {};
+    uint4 kf[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      kf[ks] = *reinterpret_cast<const uint4*>(&tl.k[buf][col][16 * ks + 8 * h2]);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8_t ka = as_bf16x8(kf[ks]);
+      if (PRECISE) {  // small terms first
+        s = mfma32(ka, as_bf16x8(qlo[ks]), s);
+        s = mfma32(ka, as_bf16x8(qmid[ks]), s);
+      }
+      s = mfma32(ka, as_bf16x8(qhi[ks]), s);
+    }
+    return s;
   };
 
   f32x16_t o[4];
@@ -190,109 +285,178 @@ __global__ __launch_bounds__(256) void gqa_prefill_kernel(PrefillArgs a) {
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
-  float m = -INFINITY, lsum = 0.0f;
+  float m = -INFINITY;  // reference max (log2 units), shared by the lane pair col, col+32
+  float lsum = 0.0f;    // this lane's 16 keys of each tile
+  const float c = a.scale_log2e;
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int n = 0; n < n_tiles; ++n) {
-    const int buf = n & 1;
-    if (n + 1 < n_tiles) load_tile(n + 1);
-
-    // S^T for keys [64n, 64n+64): two 32-key accumulators
-    f32x16_t s[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s[kt][e] = 0.0f;
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        const bf16x8_t ka = as_bf16x8(
-            *reinterpret_cast<const uint4*>(&k_lds[buf][32 * kt + col][16 * ks + 8 * h2]));
-        if (PRECISE) {  // small terms first
-          s[kt] = mfma32(ka, as_bf16x8(qlo[ks]), s[kt]);
-          s[kt] = mfma32(ka, as_bf16x8(qmid[ks]), s[kt]);
-        }
-        s[kt] = mfma32(ka, as_bf16x8(qhi[ks]), s[kt]);
-      }
-    }
-    // scale, causal mask, online softmax (this lane: one query column, 32 keys of the tile)
-    const int kbase_n = kBN * n + 4 * h2;
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+  // Softmax of tile j (scores s) and O^T += V^T P^T from V buffer `buf`.
+  auto softmax_pv = [&](f32x16_t s, int j, int buf) {
+    const int k0 = (grp + kGroups * j) * kBN;
+    if (k0 + kBN - 1 > mask_from) {  // uniform over the workgroup
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int key = kbase_n + 32 * kt + 8 * (e >> 2) + (e & 3);
-        const float v = (q_valid && key <= q_lim) ? s[kt][e] * a.scale_log2e : -INFINITY;
-        s[kt][e] = v;
-        tmax = fmaxf(tmax, v);
+        const int key = k0 + 8 * (e >> 2) + 4 * h2 + (e & 3);
+        if (key > q_lim) s[e] = -INFINITY;
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float mn = fmaxf(m, tmax);
-    const float mref = mn == -INFINITY ? 0.0f : mn;  // fully masked column (padding token)
-    const float corr = fast_exp2(m - mref);
-    m = mn;
-    float psum = 0.0f;
-    uint4 phi[4], plo[4];  // B operand per 16-key k-step a: keys 16a + 8(e/4) + 4*h2 + e%4
+    }
+    float mx = s[0];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
+    for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[e]);
+    mx = xor32_max(mx) * c;
+    if (__builtin_amdgcn_ballot_w64(mx > m + kStaleMax)) {  // move the reference max
+      const float mn = fmaxf(m, mx);
+      const float corr = m == mn ? 1.0f : fast_exp2(m - mn);
+      m = mn;
+      lsum *= corr;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+    }
+    const float mref = m == -INFINITY ? 0.0f : m;  // nothing attended yet: weights are 0
+    uint4 phi[2], plo[2];  // B operand per 16-key k-step st: keys 16st + 8(e/4) + 4*h2 + e%4
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
       float pv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pv[e] = fast_exp2(s[st >> 1][8 * (st & 1) + e] - mref);
-        psum += pv[e];
-      }
+      for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(fmaf(s[8 * st + e], c, -mref));
+      uint32_t hw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hw[e] = cvt_bf16x2(pv[2 * e], pv[2 * e + 1]);
+      phi[st] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
       if (PRECISE) {
-        split8(pv, phi[st], plo[st]);
+        uint32_t lw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lw[e] = cvt_bf16x2(pv[2 * e] - bf16_lo(hw[e]), pv[2 * e + 1] - bf16_hi(hw[e]));
+          lsum += pv[2 * e] + pv[2 * e + 1];
+        }
+        plo[st] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
       } else {
-        phi[st] = make_uint4(pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]),
-                             pack_bf16x2(pv[4], pv[5]), pack_bf16x2(pv[6], pv[7]));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lsum = add_bf16x2(hw[e], lsum);
       }
     }
-    lsum = lsum * corr + psum;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
     // O^T[dims, queries] += V^T[dims, keys] P^T[keys, queries]
+    // A operand (V^T: row = dim 32dt + col, k = keys 16st + 4*h2 + 8*(e/4) + e%4) by
+    // transposed reads of the row-major V tile: 16-lane group g covers dims 16*(g & 1) ..
+    // of the 32-dim block and keys 4*(g >> 1) .. (+8 for the second half).
+    const int tg = lane >> 4, ts = lane & 15;
+    const uint16_t* vsrc = &tl.v[buf][4 * (tg >> 1) + (ts >> 2)][16 * (tg & 1) + 4 * (ts & 3)];
+    uint4 vf[2][4];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
+    for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const uint16_t* vr = &vt_lds[buf][32 * dt + col][16 * st + 4 * h2];
-        const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
-        const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
-        const bf16x8_t va = as_bf16x8(make_uint4(v0.x, v0.y, v1.x, v1.y));
-        o[dt] = mfma32(va, as_bf16x8(phi[st]), o[dt]);
+        const uint2 v0 = lds_read_tr16(vsrc + (16 * st) * kVRow + 32 * dt);
+        const uint2 v1 = lds_read_tr16(vsrc + (16 * st + 8) * kVRow + 32 * dt);
+        vf[st][dt] = make_uint4(v0.x, v0.y, v1.x, v1.y);
+      }
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const bf16x8_t va = as_bf16x8(vf[st][dt]);
         if (PRECISE) o[dt] = mfma32(va, as_bf16x8(plo[st]), o[dt]);
+        o[dt] = mfma32(va, as_bf16x8(phi[st]), o[dt]);
       }
     }
-    if (n + 1 < n_tiles) store_tile(buf ^ 1);
+  };
+
+  u32x4_t kr[4], vr[4];
+  if constexpr (!PRECISE) {
+    // ---- prologue: K0, V0, K1 into LDS, S(0); K2, V1 in flight ----
+    {
+      u32x4_t k1[4];
+      load_k(0, kr);
+      load_v(0, vr);
+      load_k(1, k1);
+      store_k(0, kr);
+      store_v(0, vr, 0);
+      store_k(1, k1);
+    }
     __syncthreads();
+    f32x16_t s_cur = qk(0);
+    load_k(2, kr);
+    load_v(1, vr);
+    __syncthreads();
+    // ---- round j: store K(j+2), V(j+1); load K(j+3), V(j+2); S(j+1) on the MFMAs while
+    // the softmax of tile j runs on the VALU; PV of tile j; one barrier ----
+    for (int j = 0; j < n_rounds; ++j) {
+      store_k(j & 1, kr);
+      store_v((j + 1) & 1, vr, j + 1);
+      load_k(j + 3, kr);
+      load_v(j + 2, vr);
+      // (S of a tile past the group's range reads stale LDS and is never used)
+      const f32x16_t s_nxt = qk((j + 1) & 1);
+      if (j < my_tiles) softmax_pv(s_cur, j, j & 1);
+      s_cur = s_nxt;
+      __syncthreads();
+    }
+  } else {
+    // fp32 mode holds three q terms, so S is not pipelined (register budget of 2 waves/SIMD):
+    // round j stores tile j+1, loads tile j+2, and computes S, softmax and PV of tile j.
+    load_k(0, kr);
+    load_v(0, vr);
+    store_k(0, kr);
+    store_v(0, vr, 0);
+    load_k(1, kr);
+    load_v(1, vr);
+    __syncthreads();
+    for (int j = 0; j < n_rounds; ++j) {
+      store_k((j + 1) & 1, kr);
+      store_v((j + 1) & 1, vr, j + 1);
+      load_k(j + 2, kr);
+      load_v(j + 2, vr);
+      if (j < my_tiles) softmax_pv(qk(j & 1), j, j & 1);
+      __syncthreads();
+    }
   }
 
-  // ---- normalise and store: lane owns query column `col`, dims 32dt + 8i + 4*h2 + j ----
-  lsum += __shfl_xor(lsum, 32);
-  if (!q_valid) return;
-  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  float* orow = a.out + (static_cast<long>(tq) * a.Hq + hq) * kDh + 4 * h2;
+  // ---- merge the 4 key groups through LDS; wave (grp, rw) finishes dims 32*grp.. of rw ----
+  lsum = xor32_sum(lsum);
+  float* mo = reinterpret_cast<float*>(smem);  // [wave][64 values][64 lanes]
+  float* mml = mo + 8 * 64 * 64;               // [wave][m, l][64 lanes]
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<float4*>(orow + 32 * dt + 8 * i) =
-          make_float4(o[dt][4 * i] * inv, o[dt][4 * i + 1] * inv, o[dt][4 * i + 2] * inv,
-                      o[dt][4 * i + 3] * inv);
+    for (int e = 0; e < 16; ++e) mo[(wave * 64 + 16 * dt + e) * 64 + lane] = o[dt][e];
+  mml[(wave * 2) * 64 + lane] = m;
+  mml[(wave * 2 + 1) * 64 + lane] = lsum;
+  __syncthreads();
+  float mg[kGroups], M = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < kGroups; ++g) {
+    mg[g] = mml[((2 * g + rw) * 2) * 64 + lane];
+    M = fmaxf(M, mg[g]);
+  }
+  float f[16], L = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) f[e] = 0.0f;
+#pragma unroll
+  for (int g = 0; g < kGroups; ++g) {
+    const int wv = 2 * g + rw;
+    const float w = mg[g] == -INFINITY ? 0.0f : fast_exp2(mg[g] - M);
+    L += w * mml[(wv * 2 + 1) * 64 + lane];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) f[e] += w * mo[(wv * 64 + 16 * grp + e) * 64 + lane];
+  }
+  if (!q_valid) return;
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  float* orow = a.out + (static_cast<long>(tq) * a.Hq + hq) * kDh + 32 * grp + 4 * h2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<float4*>(orow + 8 * i) =
+        make_float4(f[4 * i] * inv, f[4 * i + 1] * inv, f[4 * i + 2] * inv, f[4 * i + 3] * inv);
 }
 
 template <int G>
 int launch_g(const PrefillArgs& args, bool precise, hipStream_t stream) {
   const dim3 grid(args.n_tblocks * args.Hkv);
   if (precise)
-    hipLaunchKernelGGL((gqa_prefill_kernel<G, true>), grid, dim3(256), 0, stream, args);
+    hipLaunchKernelGGL((gqa_prefill_kernel<G, true>), grid, dim3(kThreads), 0, stream, args);
   else
-    hipLaunchKernelGGL((gqa_prefill_kernel<G, false>), grid, dim3(256), 0, stream, args);
+    hipLaunchKernelGGL((gqa_prefill_kernel<G, false>), grid, dim3(kThreads), 0, stream, args);
   return check_launch("gqa_prefill_kernel");
 }
 
@@ -310,6 +474,7 @@ int launch_prefill(const float* q, const uint16_t* q_bf16, const uint16_t* kpool
   if (mode != ORATOR_PREFILL_FP32 && mode != ORATOR_PREFILL_BF16)
     return fail(ORATOR_ERR_INVALID, "gqa_prefill: unknown precision mode");
   if (capacity <= 0) return fail(ORATOR_ERR_INVALID, "gqa_prefill: capacity must be > 0");
+  if (!(scale > 0.0f)) return fail(ORATOR_ERR_INVALID, "gqa_prefill: scale must be > 0");
   if (capacity > 16 * kMaxRowGroups)
     return fail(ORATOR_ERR_UNSUPPORTED, "gqa_prefill: more than 16384 cached keys");
   PrefillArgs args{};
@@ -333,7 +498,7 @@ int launch_prefill(const float* q, const uint16_t* q_bf16, const uint16_t* kpool
   args.Hkv = Hkv;
   args.capacity = capacity;
   args.scale_log2e = scale * 1.4426950408889634f;
-  const int BT = 4 * (32 / G);
+  const int BT = kRowWaves * (32 / G);
   args.n_tblocks = (Tq + BT - 1) / BT;
   const bool precise = mode == ORATOR_PREFILL_FP32;
   if (G == 1) return launch_g<1>(args, precise, stream);
