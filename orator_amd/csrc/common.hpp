@@ -84,6 +84,14 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// Workgroup barrier for an LDS hand-off between waves that does NOT wait for outstanding
+// global loads: __syncthreads() also waits for vmcnt(0), which would drain every register
+// prefetch in flight at the barrier.  Only LDS traffic (lgkmcnt) is completed; the asm's
+// memory clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Raw v_exp_f32 (2^x); 2^-inf = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

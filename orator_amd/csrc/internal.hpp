@@ -33,6 +33,9 @@ inline int ilog2_exact(int v) {
   return s;
 }
 
+// Compute units of the current device (cached per device); 0 if it cannot be queried.
+int device_cu_count();
+
 // Optional measurement hook: when set, the next decode launch records `start` right before
 // and `stop` right after its split kernel (on the launch stream), then clears the hook.
 void take_timing_events(hipEvent_t* start, hipEvent_t* stop);

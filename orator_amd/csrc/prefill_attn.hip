@@ -11,19 +11,24 @@
 //    the softmax weights as two (hi + lo, ~2^-17 relative); K/V are exact in bf16, so QK is
 //    fp32-exact and PV within ~1e-6 of the fp32 reference, at 2.5x the MFMA work.
 //
-// Work split (one workgroup = 8 wave64s = a block of 32 query rows x 2 waves, i.e. 64 query
-// rows = 32 tokens x 2 heads of one GQA group, and 4 key groups):
-//  * key group g of the workgroup takes the 32-key tiles g, g+4, g+8, ... of the block's
-//    causal key range with its own double-buffered LDS tiles; the 4 partial softmax states
-//    are merged through LDS at the end.  Two waves per SIMD (<= 256 VGPRs each) let one
-//    wave's softmax VALU run under the other's MFMAs, and 32-token blocks give ~2x more
-//    workgroups than CUs, so heaviest-first dispatch evens out the causal triangle.
+// Work split.  A workgroup is 8 wave64s: RW query-row waves (32 query columns each) times
+// KG = 8/RW key groups.  Key group g takes the 32-key tiles g, g+KG, g+2KG, ... of the
+// block's causal key range with its own double-buffered LDS tiles; the KG partial softmax
+// states are merged through LDS at the end.  Two waves per SIMD (<= 256 VGPRs each) let one
+// wave's softmax VALU run under the other's MFMAs.  The launcher picks
+//  * RW = 4, KG = 2 (128 query rows share every K/V tile) when that still gives every CU
+//    two workgroups: a CU then pulls 32 B/clk of K/V at full MFMA rate, half of what its
+//    vector memory path sustains, and registers hold a prefetch two rounds ahead;
+//  * RW = 2, KG = 4 (64 rows per tile, 64 B/clk at full rate) for short prompts, which need
+//    the extra workgroups.
+//
+// Per tile and wave:
 //  * S^T = K Q^T: K tile rows are the MFMA A operand (ds_read_b128 from a padded,
 //    conflict-free LDS layout), the wave's 32 query columns stay in registers as B.  In the
 //    32x32 accumulator layout every lane owns ONE query column and 16 keys, so the row
 //    max / sum of the online softmax are in-lane plus one exchange between lane halves.
-//  * S^T of the next tile is issued before the softmax of the current one, so the MFMAs of
-//    one overlap the VALU of the other inside a wave too.
+//  * S^T of the next tile is issued interleaved with the softmax of the current one, so the
+//    MFMAs of one overlap the VALU of the other inside a wave too.
 //  * the running max is a stale reference: it is only moved (and O, l rescaled) when a new
 //    score exceeds it by more than 2^8, so weights stay <= 256 and most tiles skip the
 //    64-register rescale.  Softmax is invariant to the reference, so this is exact.
@@ -31,10 +36,13 @@
 //    V stays row-major in LDS and the V^T operand is read with ds_read_b64_tr_b16 (a
 //    transposing LDS read), so no VALU work transposes V; 288-byte rows keep both the
 //    16-byte stores and the transposing reads conflict-free.
-//  * the next tile is loaded from HBM/L2 into registers a full round ahead of its LDS
-//    store (one barrier per round).
+//  * K/V tiles travel HBM/L2 -> registers -> LDS; the register copy is loaded one or two
+//    rounds before its LDS store, and barriers wait for LDS traffic only, never for these
+//    loads.
 //  * workgroups are ordered heaviest (latest tokens, most keys) first, and the kv head is
 //    the fastest-varying index, so each kv head's workgroups share an XCD (blockIdx % 8).
+#include <cstdlib>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -49,10 +57,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kDh = 128;
 constexpr int kBN = 32;                              // keys per tile
-constexpr int kGroups = 4;                           // key groups per workgroup
-constexpr int kRowWaves = 2;                         // query-row waves per key group
-constexpr int kGroupThreads = 64 * kRowWaves;        // 128
-constexpr int kThreads = kGroupThreads * kGroups;    // 512
+constexpr int kThreads = 512;                        // 8 wave64s per workgroup
 constexpr int kKRow = kDh + 8;                       // padded K row (bf16 elements): 272 B
 constexpr int kVRow = kDh + 16;                      // padded V row (bf16 elements): 288 B
 constexpr int kMaxRowGroups = 1024;                  // page-row table: up to 16384 keys
@@ -78,9 +83,6 @@ struct GroupTiles {
   uint16_t k[2][kBN][kKRow];
   uint16_t v[2][kBN][kVRow];
 };
-constexpr int kTileBytes = kGroups * static_cast<int>(sizeof(GroupTiles));          // 143360
-constexpr int kMergeBytes = 8 * 64 * 64 * 4 + 8 * 2 * 64 * 4;                        // 135168
-static_assert(kMergeBytes <= kTileBytes, "merge area reuses the tile buffers");
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
@@ -138,11 +140,21 @@ __device__ __forceinline__ void split8(float (&x)[8], uint4& hi, uint4& lo) {
   lo = make_uint4(l[0], l[1], l[2], l[3]);
 }
 
-template <int G, bool PRECISE>
+
+template <int G, bool PRECISE, int RW>
 __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
-  constexpr int TW = 32 / G;          // tokens per wave (32 query columns = TW tokens x G heads)
-  constexpr int BT = kRowWaves * TW;  // tokens per workgroup
-  __shared__ __align__(16) unsigned char smem[kTileBytes];
+  constexpr int KG = 8 / RW;                   // key groups
+  constexpr int TW = 32 / G;                   // tokens per wave (32 columns = TW tokens x G heads)
+  constexpr int BT = RW * TW;                  // tokens per workgroup
+  constexpr int GT = 64 * RW;                  // threads per key group
+  constexpr int NP = kBN * 16 / GT;            // 16-byte chunks per thread per K (or V) tile
+  constexpr int RPP = GT / 16;                 // tile rows covered by one pass of the group
+  constexpr int DIST = (!PRECISE && RW == 4) ? 2 : 1;  // register prefetch distance (rounds)
+  constexpr int D = 4 / KG;                    // 32-dim output blocks each wave finalizes
+  static_assert(KG * RW == 8 && NP * RPP == kBN, "tile split");
+  static_assert(8 * (4 - D) * 16 * 64 * 4 + 8 * 2 * 64 * 4 <= KG * (int)sizeof(GroupTiles),
+                "merge area reuses the tile buffers");
+  __shared__ __align__(16) unsigned char smem[KG * sizeof(GroupTiles)];
   __shared__ int row_lds[kMaxRowGroups];
 
   const int kvh = blockIdx.x % a.Hkv;
@@ -150,9 +162,9 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int grp = __builtin_amdgcn_readfirstlane(wave >> 1);  // key group (wave-uniform)
-  const int rw = wave & 1;                                     // query-row wave of the group
-  const int gt = tid & (kGroupThreads - 1);  // thread index within the group
+  const int grp = __builtin_amdgcn_readfirstlane(wave / RW);  // key group (wave-uniform)
+  const int rw = wave % RW;                                   // query-row wave of the group
+  const int gt = tid % GT;                                    // thread index within the group
   const int h2 = lane >> 5;   // which half of the 32x32 accumulator rows this lane holds
   const int col = lane & 31;  // this lane's query column
   const int pos0 = *a.pos0p;
@@ -162,8 +174,8 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   const int t_end = min(t_blk + BT, a.Tq);
   const int n_keys = min(pos0 + t_end, a.capacity);  // keys [0, n_keys) are needed
   const int n_tiles = (n_keys + kBN - 1) / kBN;
-  const int n_rounds = (n_tiles + kGroups - 1) / kGroups;
-  const int my_tiles = n_tiles > grp ? (n_tiles - grp + kGroups - 1) / kGroups : 0;
+  const int n_rounds = (n_tiles + KG - 1) / KG;
+  const int my_tiles = n_tiles > grp ? (n_tiles - grp + KG - 1) / KG : 0;
   // tiles with a key beyond this need the causal / capacity mask
   const int mask_from = min(pos0 + t_blk, n_keys - 1);
 
@@ -205,10 +217,10 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
       }
     }
   }
-  __syncthreads();  // row_lds ready
+  lds_barrier();  // row_lds ready
 
-  // ---- tile loader (group-local tile j = key tile grp + kGroups*j) ----
-  // K and V rows 8p + ld_row (p = 0..3), one 16-byte chunk (dims 8*ld_chunk..) per thread;
+  // ---- tile loader (group-local tile j = key tile grp + KG*j) ----
+  // K and V rows ld_row + RPP*p (p < NP), one 16-byte chunk (dims 8*ld_chunk..) per thread;
   // with the padded rows the LDS stores are conflict-free.
   const long rs = static_cast<long>(a.Hkv) * kDh;  // elements between consecutive rows
   const uint16_t* kbase = a.kpool + static_cast<long>(kvh) * kDh;
@@ -221,44 +233,46 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
     key = min(key, n_keys - 1);
     return static_cast<long>(row_lds[key >> 4] + (key & 15));
   };
-  auto load_rows = [&](const uint16_t* base, int j, u32x4_t (&r)[4]) {
-    const int k0 = (grp + kGroups * j) * kBN;  // uniform
+  auto load_rows = [&](const uint16_t* base, int j, u32x4_t (&r)[NP]) {
+    const int k0 = (grp + KG * j) * kBN;  // uniform
     if (k0 + kBN <= n_keys) {
       // whole tile valid: two 16-row groups with uniform bases
       const long rg0 = __builtin_amdgcn_readfirstlane(row_lds[k0 >> 4]);
       const long rg1 = __builtin_amdgcn_readfirstlane(row_lds[(k0 >> 4) + 1]);
       const char* b0 = reinterpret_cast<const char*>(base + rg0 * rs) + lane_off;
       const char* b1 = reinterpret_cast<const char*>(base + rg1 * rs) + lane_off;
-      r[0] = *reinterpret_cast<const u32x4_t*>(b0);
-      r[1] = *reinterpret_cast<const u32x4_t*>(b0 + 8 * rs2);
-      r[2] = *reinterpret_cast<const u32x4_t*>(b1);
-      r[3] = *reinterpret_cast<const u32x4_t*>(b1 + 8 * rs2);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int roff = RPP * p;
+        const char* bp = ((roff >> 4) ? b1 : b0) + (roff & 15) * rs2;
+        r[p] = *reinterpret_cast<const u32x4_t*>(bp);
+      }
     } else {
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
+      for (int p = 0; p < NP; ++p)
         r[p] = *reinterpret_cast<const u32x4_t*>(
-            base + row_clamped(k0 + 8 * p + ld_row) * rs + 8 * ld_chunk);
+            base + row_clamped(k0 + RPP * p + ld_row) * rs + 8 * ld_chunk);
     }
   };
-  auto load_k = [&](int j, u32x4_t (&r)[4]) { load_rows(kbase, j, r); };
-  auto load_v = [&](int j, u32x4_t (&r)[4]) { load_rows(vbase, j, r); };
-  auto store_k = [&](int buf, const u32x4_t (&r)[4]) {
+  auto load_k = [&](int j, u32x4_t (&r)[NP]) { load_rows(kbase, j, r); };
+  auto load_v = [&](int j, u32x4_t (&r)[NP]) { load_rows(vbase, j, r); };
+  auto store_k = [&](int buf, const u32x4_t (&r)[NP]) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
-      *reinterpret_cast<u32x4_t*>(&tl.k[buf][8 * p + ld_row][8 * ld_chunk]) = r[p];
+    for (int p = 0; p < NP; ++p)
+      *reinterpret_cast<u32x4_t*>(&tl.k[buf][RPP * p + ld_row][8 * ld_chunk]) = r[p];
   };
   // Keys past the end are stored as zeros in V: their weights are 0, and 0 * inf must not
   // occur.  (Keys past the end in K need nothing: their scores are replaced by the mask.)
-  auto store_v = [&](int buf, u32x4_t (&r)[4], int j) {
-    const int k0 = (grp + kGroups * j) * kBN;
+  auto store_v = [&](int buf, u32x4_t (&r)[NP], int j) {
+    const int k0 = (grp + KG * j) * kBN;
     if (k0 + kBN > n_keys) {  // uniform over the group
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
-        if (k0 + 8 * p + ld_row >= n_keys) r[p] = u32x4_t{0, 0, 0, 0};
+      for (int p = 0; p < NP; ++p)
+        if (k0 + RPP * p + ld_row >= n_keys) r[p] = u32x4_t{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
-      *reinterpret_cast<u32x4_t*>(&tl.v[buf][8 * p + ld_row][8 * ld_chunk]) = r[p];
+    for (int p = 0; p < NP; ++p)
+      *reinterpret_cast<u32x4_t*>(&tl.v[buf][RPP * p + ld_row][8 * ld_chunk]) = r[p];
   };
 
   // S^T (32 keys x this wave's 32 query columns) of the tile in K buffer `buf`.
@@ -289,9 +303,11 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   float lsum = 0.0f;    // this lane's 16 keys of each tile
   const float c = a.scale_log2e;
 
-  // Softmax of tile j (scores s) and O^T += V^T P^T from V buffer `buf`.
-  auto softmax_pv = [&](f32x16_t s, int j, int buf) {
-    const int k0 = (grp + kGroups * j) * kBN;
+  // Causal / capacity mask of tile j's scores, then the reference max: it is only moved
+  // (and O, l rescaled) when some score exceeds it by more than 2^kStaleMax.  Returns the
+  // reference to subtract (0 while nothing has been attended: all weights are then 0).
+  auto mask_and_rescale = [&](f32x16_t& s, int j) {
+    const int k0 = (grp + KG * j) * kBN;
     if (k0 + kBN - 1 > mask_from) {  // uniform over the workgroup
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -313,151 +329,247 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
     }
-    const float mref = m == -INFINITY ? 0.0f : m;  // nothing attended yet: weights are 0
+    return m == -INFINITY ? 0.0f : m;
+  };
+
+  // A operand of O^T += V^T P^T (V^T: row = dim 32dt + col, k = keys 16st + 4*h2 + 8*(e/4)
+  // + e%4) by transposed reads of the row-major V tile: 16-lane group g covers dims
+  // 16*(g & 1) .. of the 32-dim block and keys 4*(g >> 1) .. (+8 for the second half).
+  const int tg = lane >> 4, ts = lane & 15;
+  const int v_lane = (4 * (tg >> 1) + (ts >> 2)) * kVRow + 16 * (tg & 1) + 4 * (ts & 3);
+  auto read_vf = [&](int buf, int st, uint4 (&vf)[4]) {
+    const uint16_t* vsrc = &tl.v[buf][0][0] + v_lane + (16 * st) * kVRow;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint2 v0 = lds_read_tr16(vsrc + 32 * dt);
+      const uint2 v1 = lds_read_tr16(vsrc + 8 * kVRow + 32 * dt);
+      vf[dt] = make_uint4(v0.x, v0.y, v1.x, v1.y);
+    }
+  };
+
+  // Softmax of tile j (scores s) and O^T += V^T P^T from V buffer `buf` (fp32 mode).
+  auto softmax_pv = [&](f32x16_t s, int j, int buf) {
+    const float mref = mask_and_rescale(s, j);
     uint4 phi[2], plo[2];  // B operand per 16-key k-step st: keys 16st + 8(e/4) + 4*h2 + e%4
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(fmaf(s[8 * st + e], c, -mref));
-      uint32_t hw[4];
+      uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) hw[e] = cvt_bf16x2(pv[2 * e], pv[2 * e + 1]);
+      for (int e = 0; e < 4; ++e) {
+        hw[e] = cvt_bf16x2(pv[2 * e], pv[2 * e + 1]);
+        lw[e] = cvt_bf16x2(pv[2 * e] - bf16_lo(hw[e]), pv[2 * e + 1] - bf16_hi(hw[e]));
+        lsum += pv[2 * e] + pv[2 * e + 1];
+      }
       phi[st] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-      if (PRECISE) {
-        uint32_t lw[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          lw[e] = cvt_bf16x2(pv[2 * e] - bf16_lo(hw[e]), pv[2 * e + 1] - bf16_hi(hw[e]));
-          lsum += pv[2 * e] + pv[2 * e + 1];
-        }
-        plo[st] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) lsum = add_bf16x2(hw[e], lsum);
-      }
+      plo[st] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     }
-    // O^T[dims, queries] += V^T[dims, keys] P^T[keys, queries]
-    // A operand (V^T: row = dim 32dt + col, k = keys 16st + 4*h2 + 8*(e/4) + e%4) by
-    // transposed reads of the row-major V tile: 16-lane group g covers dims 16*(g & 1) ..
-    // of the 32-dim block and keys 4*(g >> 1) .. (+8 for the second half).
-    const int tg = lane >> 4, ts = lane & 15;
-    const uint16_t* vsrc = &tl.v[buf][4 * (tg >> 1) + (ts >> 2)][16 * (tg & 1) + 4 * (ts & 3)];
-    uint4 vf[2][4];
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const uint2 v0 = lds_read_tr16(vsrc + (16 * st) * kVRow + 32 * dt);
-        const uint2 v1 = lds_read_tr16(vsrc + (16 * st + 8) * kVRow + 32 * dt);
-        vf[st][dt] = make_uint4(v0.x, v0.y, v1.x, v1.y);
-      }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
+      uint4 vf[4];
+      read_vf(buf, st, vf);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const bf16x8_t va = as_bf16x8(vf[st][dt]);
-        if (PRECISE) o[dt] = mfma32(va, as_bf16x8(plo[st]), o[dt]);
+        const bf16x8_t va = as_bf16x8(vf[dt]);
+        o[dt] = mfma32(va, as_bf16x8(plo[st]), o[dt]);
         o[dt] = mfma32(va, as_bf16x8(phi[st]), o[dt]);
       }
     }
   };
 
-  u32x4_t kr[4], vr[4];
   if constexpr (!PRECISE) {
-    // ---- prologue: K0, V0, K1 into LDS, S(0); K2, V1 in flight ----
+    // Register prefetch sets: set (j % DIST) holds K(j+2), V(j+1) at the start of round j.
+    u32x4_t kr[DIST][NP], vr[DIST][NP];
+    // Phases of one bf16 round, in issue order: LDS stores of the prefetched K(j+2), V(j+1);
+    // global loads of K(j+2+DIST), V(j+1+DIST); the K fragments of S(j+1); mask / max /
+    // rescale of tile j; the transposed V reads of tile j; S(j+1) MFMAs interleaved with
+    // the weights of tile j (exp, bf16 pack, row sum); the PV MFMAs of tile j.
+    auto round = [&]<int P>(int j, f32x16_t& s_cur, f32x16_t& s_nxt) {
+      constexpr int S = DIST == 2 ? P : 0;
+      store_k(P, kr[S]);
+      store_v(P ^ 1, vr[S], j + 1);
+      load_k(j + 2 + DIST, kr[S]);
+      load_v(j + 1 + DIST, vr[S]);
+      if (j >= my_tiles) return;  // uniform: this group has no tile j
+      uint4 kf[8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+        kf[ks] = *reinterpret_cast<const uint4*>(&tl.k[P ^ 1][col][16 * ks + 8 * h2]);
+      const float mref = mask_and_rescale(s_cur, j);
+      uint4 vf[2][4];
+      read_vf(P, 0, vf[0]);
+      read_vf(P, 1, vf[1]);
+      f32x16_t sn = {};
+      uint32_t hw[8];  // bf16 weights of elements 2i, 2i+1 of s_cur
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        sn = mfma32(as_bf16x8(kf[ks]), as_bf16x8(qhi[ks]), sn);
+        const float p0 = fast_exp2(fmaf(s_cur[2 * ks], c, -mref));
+        const float p1 = fast_exp2(fmaf(s_cur[2 * ks + 1], c, -mref));
+        hw[ks] = cvt_bf16x2(p0, p1);
+        lsum = add_bf16x2(hw[ks], lsum);
+      }
+      s_nxt = sn;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const uint4 ph = make_uint4(hw[4 * st], hw[4 * st + 1], hw[4 * st + 2], hw[4 * st + 3]);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] = mfma32(as_bf16x8(vf[st][dt]), as_bf16x8(ph), o[dt]);
+      }
+      // Issue order: each dependent S MFMA followed by ~6 independent weight instructions
+      // (which run while the MFMA executes), the V reads in two batches ahead of them, then
+      // the PV MFMAs.
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i % 4 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);                  // VALU
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // MFMA
+    };
+    // ---- prologue: K0, V0, K1 into LDS, S(0); the first DIST register sets in flight ----
     {
-      u32x4_t k1[4];
-      load_k(0, kr);
-      load_v(0, vr);
+      u32x4_t k1[NP];
+      load_k(0, kr[0]);
+      load_v(0, vr[0]);
       load_k(1, k1);
-      store_k(0, kr);
-      store_v(0, vr, 0);
+      store_k(0, kr[0]);
+      store_v(0, vr[0], 0);
       store_k(1, k1);
     }
-    __syncthreads();
-    f32x16_t s_cur = qk(0);
-    load_k(2, kr);
-    load_v(1, vr);
-    __syncthreads();
-    // ---- round j: store K(j+2), V(j+1); load K(j+3), V(j+2); S(j+1) on the MFMAs while
-    // the softmax of tile j runs on the VALU; PV of tile j; one barrier ----
-    for (int j = 0; j < n_rounds; ++j) {
-      store_k(j & 1, kr);
-      store_v((j + 1) & 1, vr, j + 1);
-      load_k(j + 3, kr);
-      load_v(j + 2, vr);
-      // (S of a tile past the group's range reads stale LDS and is never used)
-      const f32x16_t s_nxt = qk((j + 1) & 1);
-      if (j < my_tiles) softmax_pv(s_cur, j, j & 1);
-      s_cur = s_nxt;
-      __syncthreads();
+    lds_barrier();
+    f32x16_t s0 = qk(0), s1;
+#pragma unroll
+    for (int d = 0; d < DIST; ++d) {
+      load_k(2 + d, kr[d]);
+      load_v(1 + d, vr[d]);
+    }
+    lds_barrier();
+    int j = 0;
+    for (; j + 1 < n_rounds; j += 2) {
+      round.template operator()<0>(j, s0, s1);
+      lds_barrier();
+      round.template operator()<1>(j + 1, s1, s0);
+      lds_barrier();
+    }
+    if (j < n_rounds) {
+      round.template operator()<0>(j, s0, s1);
+      lds_barrier();
     }
   } else {
     // fp32 mode holds three q terms, so S is not pipelined (register budget of 2 waves/SIMD):
     // round j stores tile j+1, loads tile j+2, and computes S, softmax and PV of tile j.
+    u32x4_t kr[NP], vr[NP];
     load_k(0, kr);
     load_v(0, vr);
     store_k(0, kr);
     store_v(0, vr, 0);
     load_k(1, kr);
     load_v(1, vr);
-    __syncthreads();
+    lds_barrier();
     for (int j = 0; j < n_rounds; ++j) {
       store_k((j + 1) & 1, kr);
       store_v((j + 1) & 1, vr, j + 1);
       load_k(j + 2, kr);
       load_v(j + 2, vr);
       if (j < my_tiles) softmax_pv(qk(j & 1), j, j & 1);
-      __syncthreads();
+      lds_barrier();
     }
   }
 
-  // ---- merge the 4 key groups through LDS; wave (grp, rw) finishes dims 32*grp.. of rw ----
+  // ---- merge the KG key groups through LDS.  Wave (grp, rw) finishes output dims
+  // [32*D*grp, 32*D*(grp+1)) of its query rows; every wave hands the other groups the
+  // 32-dim blocks they finish. ----
   lsum = xor32_sum(lsum);
-  float* mo = reinterpret_cast<float*>(smem);  // [wave][64 values][64 lanes]
-  float* mml = mo + 8 * 64 * 64;               // [wave][m, l][64 lanes]
+  float* mo = reinterpret_cast<float*>(smem);  // [wave][4 - D blocks][16 values][64 lanes]
+  float* mml = mo + 8 * (4 - D) * 16 * 64;     // [wave][m, l][64 lanes]
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < 4; ++dt) {
+    if (dt / D == grp) continue;  // uniform
+    const int slot = dt < grp * D ? dt : dt - D;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) mo[(wave * 64 + 16 * dt + e) * 64 + lane] = o[dt][e];
+    for (int e = 0; e < 16; ++e) mo[((wave * (4 - D) + slot) * 16 + e) * 64 + lane] = o[dt][e];
+  }
   mml[(wave * 2) * 64 + lane] = m;
   mml[(wave * 2 + 1) * 64 + lane] = lsum;
-  __syncthreads();
-  float mg[kGroups], M = -INFINITY;
+  lds_barrier();
+  float mg[KG], M = -INFINITY;
 #pragma unroll
-  for (int g = 0; g < kGroups; ++g) {
-    mg[g] = mml[((2 * g + rw) * 2) * 64 + lane];
+  for (int g = 0; g < KG; ++g) {
+    mg[g] = mml[((g * RW + rw) * 2) * 64 + lane];
     M = fmaxf(M, mg[g]);
   }
-  float f[16], L = 0.0f;
+  float L = 0.0f;
+  float w[KG];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) f[e] = 0.0f;
-#pragma unroll
-  for (int g = 0; g < kGroups; ++g) {
-    const int wv = 2 * g + rw;
-    const float w = mg[g] == -INFINITY ? 0.0f : fast_exp2(mg[g] - M);
-    L += w * mml[(wv * 2 + 1) * 64 + lane];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) f[e] += w * mo[(wv * 64 + 16 * grp + e) * 64 + lane];
+  for (int g = 0; g < KG; ++g) {
+    w[g] = mg[g] == -INFINITY ? 0.0f : fast_exp2(mg[g] - M);
+    L += w[g] * mml[((g * RW + rw) * 2 + 1) * 64 + lane];
   }
-  if (!q_valid) return;
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  float* orow = a.out + (static_cast<long>(tq) * a.Hq + hq) * kDh + 32 * grp + 4 * h2;
+  if (!q_valid) return;
+  float* orow = a.out + (static_cast<long>(tq) * a.Hq + hq) * kDh + 4 * h2;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<float4*>(orow + 8 * i) =
-        make_float4(f[4 * i] * inv, f[4 * i + 1] * inv, f[4 * i + 2] * inv, f[4 * i + 3] * inv);
+  for (int d = 0; d < D; ++d) {
+    const int dt = grp * D + d;
+    // this wave's own block dt = grp * D + d
+    f32x16_t f;
+    if constexpr (KG == 2) {
+      f = grp ? o[2 + d] : o[d];
+    } else {
+      f = grp == 0 ? o[0] : grp == 1 ? o[1] : grp == 2 ? o[2] : o[3];
+    }
+    float w_own = w[0];
+#pragma unroll
+    for (int g = 1; g < KG; ++g)
+      if (grp == g) w_own = w[g];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) f[e] *= w_own;
+#pragma unroll
+    for (int g = 0; g < KG; ++g) {
+      if (g == grp) continue;
+      const int slot = dt < g * D ? dt : dt - D;
+      const float* src = mo + ((g * RW + rw) * (4 - D) + slot) * 16 * 64 + lane;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) f[e] += w[g] * src[e * 64];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<float4*>(orow + 32 * dt + 8 * i) =
+          make_float4(f[4 * i] * inv, f[4 * i + 1] * inv, f[4 * i + 2] * inv, f[4 * i + 3] * inv);
+  }
+}
+
+template <int G, bool PRECISE>
+int launch_rw(const PrefillArgs& args, int rw, hipStream_t stream) {
+  const dim3 grid(args.n_tblocks * args.Hkv);
+  if (rw == 4)
+    hipLaunchKernelGGL((gqa_prefill_kernel<G, PRECISE, 4>), grid, dim3(kThreads), 0, stream, args);
+  else
+    hipLaunchKernelGGL((gqa_prefill_kernel<G, PRECISE, 2>), grid, dim3(kThreads), 0, stream, args);
+  return check_launch("gqa_prefill_kernel");
 }
 
 template <int G>
-int launch_g(const PrefillArgs& args, bool precise, hipStream_t stream) {
-  const dim3 grid(args.n_tblocks * args.Hkv);
-  if (precise)
-    hipLaunchKernelGGL((gqa_prefill_kernel<G, true>), grid, dim3(kThreads), 0, stream, args);
-  else
-    hipLaunchKernelGGL((gqa_prefill_kernel<G, false>), grid, dim3(kThreads), 0, stream, args);
-  return check_launch("gqa_prefill_kernel");
+int launch_g(PrefillArgs& args, bool precise, hipStream_t stream) {
+  // 128 query rows per K/V tile when that still gives every CU two workgroups (heaviest-
+  // first dispatch needs the second one to even out the causal triangle); measured on
+  // MI355X: RW = 2 is faster at 2048 tokens x 8 kv heads, RW = 4 at 4096.
+  const int cus = device_cu_count();
+  const int blocks4 = (args.Tq + 4 * (32 / G) - 1) / (4 * (32 / G));
+  int rw = static_cast<long>(blocks4) * args.Hkv >= 2L * (cus > 0 ? cus : 256) ? 4 : 2;
+  // Tuning override (read once): ORATOR_PREFILL_RW in {2, 4} fixes the row-wave count.
+  static const int rw_override = [] {
+    const char* e = std::getenv("ORATOR_PREFILL_RW");
+    const int v = e ? std::atoi(e) : 0;
+    return v == 2 || v == 4 ? v : 0;
+  }();
+  if (rw_override) rw = rw_override;
+  const int BT = rw * (32 / G);
+  args.n_tblocks = (args.Tq + BT - 1) / BT;
+  return precise ? launch_rw<G, true>(args, rw, stream) : launch_rw<G, false>(args, rw, stream);
 }
 
 int launch_prefill(const float* q, const uint16_t* q_bf16, const uint16_t* kpool,
@@ -498,8 +610,6 @@ int launch_prefill(const float* q, const uint16_t* q_bf16, const uint16_t* kpool
   args.Hkv = Hkv;
   args.capacity = capacity;
   args.scale_log2e = scale * 1.4426950408889634f;
-  const int BT = kRowWaves * (32 / G);
-  args.n_tblocks = (Tq + BT - 1) / BT;
   const bool precise = mode == ORATOR_PREFILL_FP32;
   if (G == 1) return launch_g<1>(args, precise, stream);
   if (G == 2) return launch_g<2>(args, precise, stream);

@@ -4,6 +4,7 @@
 
 #include <cmath>
 #include <map>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -41,6 +42,17 @@ int check_hip(hipError_t e, const char* what) {
 }
 
 int check_launch(const char* what) { return check_hip(hipGetLastError(), what); }
+
+int device_cu_count() {
+  static std::atomic<int> cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cached[dev].load(std::memory_order_relaxed) > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+  if (dev < 64 && n > 0) cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
 
 void* workspace(hipStream_t stream, size_t bytes, size_t counter_bytes) {
   int dev = 0;
