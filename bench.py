@@ -4,8 +4,9 @@ Headline workload (the decode target "KV length 4096")
 a 28-layer stack of GQA decode attention, Qwen3-1.7B layer shape (16 q / 8 kv heads,
 head_dim 128), B = 16 independent streams, base KV length L = 4096, bf16 KV in 16-token
 pages with per-stream page tables.  One step = for each of the 28 layers: append the new
-token's K/V to the paged cache, then attend S = L + t + 1 keys.  Inputs are synthetic and
-resident in HBM before timing.
+token's K/V to the paged cache and attend S = L + t + 1 keys (orator_gqa_decode_append_paged:
+the write and the attention share one launch, followed by the split merge).  Inputs are
+synthetic and resident in HBM before timing.
 
 `value` = decode-attention algorithmic bytes / wall time of the K timed steps, where the
 bytes per (stream, layer, step) are 2*S*Hkv*Dh*2 (K and V read once) + Hq*Dh*4 (q) +
@@ -111,13 +112,13 @@ def run_decode(steps: int, warmup: int):
         pos_ptr = dpos.ptr + t * B * 4
         v = t % n_var
         for l in range(LAYERS):
-            da.WriteKvCachePaged(ks[v], vs[v], kpools[l], vpools[l], tables[l], max_pages, PAGE,
-                                 n_pages, B, 1, HKV, DH, pos_ptr, stream)
             if evs is not None:  # the decode operation: split-K kernel + split merge kernel
                 evs[l][0].record(stream)
                 call("orator_time_next_decode", evs[l][2].handle, evs[l][3].handle)
-            da.GqaDecodeAttnPaged(qs[v], kpools[l], vpools[l], tables[l], max_pages, PAGE, pos_ptr,
-                                  outs, B, HQ, HKV, DH, scale, stream)
+            # KV append of the new token + attention over pos + 1 keys, one launch (+ merge)
+            da.GqaDecodeAttnAppendPaged(qs[v], ks[v], vs[v], kpools[l], vpools[l], tables[l],
+                                        max_pages, PAGE, n_pages, pos_ptr, outs, B, HQ, HKV, DH,
+                                        scale, stream)
             if evs is not None:
                 evs[l][1].record(stream)
 

@@ -138,6 +138,21 @@ int orator_gqa_decode_paged(const float* q, const uint16_t* kpool, const uint16_
                             const int* page_table, int max_pages, int page_size,
                             const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
                             float scale, void* stream);
+/* WriteKvCacheKernel + GqaDecodeAttnKernel of one decode step (src/model/asr_text_decoder.cu:
+ * 412-418) in one launch: the new token's K/V rows k_new/v_new [Hkv, Dh] fp32 are stored (bf16,
+ * round to nearest even) at position *d_pos, and q attends the *d_pos + 1 keys including them.
+ * Same result as orator_kv_write then orator_gqa_decode; k_new/v_new 16-byte aligned. */
+int orator_gqa_decode_append(const float* q, const float* k_new, const float* v_new,
+                             uint16_t* kc, uint16_t* vc, float* out, int Hq, int Hkv, int Dh,
+                             const int* d_pos, int capacity, float scale, void* stream);
+/* Batched paged form: stream b appends k_new/v_new [B, Hkv, Dh] at d_pos[b] through page-table
+ * row b and attends d_pos[b] + 1 keys.  Rows of pages >= n_pages are not written (as
+ * orator_kv_write_paged). */
+int orator_gqa_decode_append_paged(const float* q, const float* k_new, const float* v_new,
+                                   uint16_t* kpool, uint16_t* vpool, const int* page_table,
+                                   int max_pages, int page_size, int n_pages, const int* d_pos,
+                                   float* out, int B, int Hq, int Hkv, int Dh, float scale,
+                                   void* stream);
 
 /* ----------------------------------------------------------------- GEMM ---- */
 /* gemm::LaunchSgemm (include/model/gemm.cuh:160-174): out[M,N] = act(in[M,K] W[N,K]^T + bias),

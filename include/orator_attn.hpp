@@ -96,6 +96,14 @@ inline void GqaDecodeAttn(const float* q, const uint16_t* kc, const uint16_t* vc
                           hipStream_t stream = 0) {
   gpu::Check(orator_gqa_decode(q, kc, vc, out, Hq, Hkv, Dh, d_pos, capacity, scale, stream));
 }
+// WriteKvCache + GqaDecodeAttn in one launch (asr_text_decoder.cu:412-418).
+inline void GqaDecodeAttnAppend(const float* q, const float* k_new, const float* v_new,
+                                uint16_t* kc, uint16_t* vc, float* out, int Hq, int Hkv, int Dh,
+                                const int* d_pos, int capacity, float scale,
+                                hipStream_t stream = 0) {
+  gpu::Check(orator_gqa_decode_append(q, k_new, v_new, kc, vc, out, Hq, Hkv, Dh, d_pos, capacity,
+                                      scale, stream));
+}
 // RmsNorm(q,k) + RopeHalf(q,k) + WriteKvCache in one launch (asr_text_decoder.cu:408-413).
 inline void QkNormRopeKvWrite(float* q, float* k, const float* v, long q_stride, long kv_stride,
                               const float* q_norm, const float* k_norm, float eps,

@@ -69,6 +69,9 @@ SIGNATURES: dict[str, list] = {
     "orator_kv_write_paged": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p],
     "orator_gqa_decode": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+    "orator_gqa_decode_append": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
+    "orator_gqa_decode_append_paged": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _i, _i, _i,
+                                       _i, _f, _p],
     "orator_qk_norm_rope_kv_write": [_p, _p, _p, _l, _l, _p, _p, _f, _p, _f, _i, _i, _i, _i, _i,
                                      _p, _p, _p, _i, _i, _i, _p],
     "orator_sgemm": [_p, _p, _p, _p, _i, _i, _i, _i, _p],

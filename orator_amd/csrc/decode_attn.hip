@@ -18,11 +18,13 @@
 //    probabilities move to the PV layout with one lane shuffle per key row.
 //  * PV, "row" layout: Dh/8 lanes per key, one 16-byte load each (whole contiguous rows
 //    per instruction); per-lane accumulators hold 8 dims x G heads.
-//  * waves merge in LDS at the end; splits are merged by a second small kernel.  (A
+//  * waves merge in LDS at the end; splits are merged by a second small kernel (one memory
+//    round trip for up to 16 splits: all loads issued together, online max).  (A
 //    last-workgroup merge in the same launch needs a device-scope release fence per
 //    workgroup -- an L2 write-back on gfx950 -- and measured 7-10x slower.)
 //  * paged KV: the split's page rows are resolved once into LDS, so no K/V load waits
 //    on a page-table load.
+#include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -49,6 +51,11 @@ struct DecodeArgs {
   int max_splits;
   int capacity;
   float scale_log2e;
+  // Append (pos_mode 0, bf16 caches): the new token's K/V rows [B][Hkv][DH] fp32 are written
+  // at position pos[b] and attended as the last key; nullptr when there is nothing to append.
+  const float* k_new;
+  const float* v_new;
+  long pool_rows;  // rows the pools hold (paged writes past it are dropped)
 };
 
 // Number of keys stream b attends, clamped to the capacity.
@@ -200,6 +207,59 @@ __device__ __forceinline__ void process_chunk(const Chunk<DH, KV>& cur,
   }
 }
 
+// The appended key (bf16-rounded from the fp32 input, exactly what the cache will hold)
+// folded into a wave's running softmax state: the score in every octet (octet layout, all
+// 64 lanes hold it after the reduction), one lane adds its weight to the row sum, the r == 0
+// lanes its weighted V row.  Returns this lane's bf16 K (octet layout) and V (row layout)
+// pieces for the cache write.
+template <int DH, int G>
+__device__ __forceinline__ void append_key(const float* kn, const float* vn,
+                                           const float (&qr)[G][Chunk<DH, uint16_t>::QPL],
+                                           float (&m)[G], float (&lpart)[G], float (&acc)[G][8],
+                                           int lane, float scale_log2e,
+                                           uint4 (&kw)[Chunk<DH, uint16_t>::NCQ], uint4& vw) {
+  using CK = Chunk<DH, uint16_t>;
+  const int o = lane & 7;
+  float kf[CK::QPL];
+#pragma unroll
+  for (int cc = 0; cc < CK::NCQ; ++cc) {
+    const float4 x0 = *reinterpret_cast<const float4*>(kn + 8 * CK::EPV * cc + CK::EPV * o);
+    const float4 x1 = *reinterpret_cast<const float4*>(kn + 8 * CK::EPV * cc + CK::EPV * o + 4);
+    kw[cc] = make_uint4(pack_bf16x2(x0.x, x0.y), pack_bf16x2(x0.z, x0.w), pack_bf16x2(x1.x, x1.y),
+                        pack_bf16x2(x1.z, x1.w));
+    const uint32_t w[4] = {kw[cc].x, kw[cc].y, kw[cc].z, kw[cc].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kf[cc * 8 + e] = (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
+  }
+  const int dg = lane % CK::LPT;
+  const float4 y0 = *reinterpret_cast<const float4*>(vn + 8 * dg);
+  const float4 y1 = *reinterpret_cast<const float4*>(vn + 8 * dg + 4);
+  vw = make_uint4(pack_bf16x2(y0.x, y0.y), pack_bf16x2(y0.z, y0.w), pack_bf16x2(y1.x, y1.y),
+                  pack_bf16x2(y1.z, y1.w));
+  const uint32_t vwd[4] = {vw.x, vw.y, vw.z, vw.w};
+  const bool row0 = lane < CK::LPT;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float d = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CK::QPL; ++i) d = fmaf(qr[g][i], kf[i], d);
+    d += dpp<0xB1>(d);
+    d += dpp<0x4E>(d);
+    d += dpp<0x141>(d);
+    const float sc = d * scale_log2e;
+    const float mn = fmaxf(m[g], sc);
+    const float corr = fast_exp2(m[g] - mn);
+    const float p = fast_exp2(sc - mn);
+    m[g] = mn;
+    lpart[g] = lpart[g] * corr + (lane == 0 ? p : 0.0f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float vv = (e & 1) ? bf16_hi(vwd[e >> 1]) : bf16_lo(vwd[e >> 1]);
+      acc[g][e] = acc[g][e] * corr + (row0 ? p * vv : 0.0f);
+    }
+  }
+}
+
 template <int DH, int G, int SPLIT, typename KV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gqa_decode_kernel(
     DecodeArgs a) {
@@ -213,9 +273,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   __shared__ float red_ml[NW][G][2];
   __shared__ int row_lds[NG];
 
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+  // split index slowest: the short last splits of the streams are dispatched last, where
+  // they fill the drain of the final round instead of lengthening it
+  const int kvh = blockIdx.x;
+  const int b = blockIdx.y;
+  const int split = blockIdx.z;
   int S = stream_keys(a, b);
   if (S <= 0) {  // no keys: the reference's 1/sum guard yields zeros
     if (split == 0)
@@ -260,15 +322,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         qr[g][cc * CK::EPV + e4 + 3] = x.w;
       }
   }
-  __syncthreads();
+  lds_barrier();  // row_lds ready (the q loads may still be in flight)
 
   const long kv_base = (a.page_table ? 0 : static_cast<long>(b) * a.stream_stride) +
                        static_cast<long>(kvh) * DH;
   const KV* kbase = static_cast<const KV*>(a.kpool) + kv_base;
   const KV* vbase = static_cast<const KV*>(a.vpool) + kv_base;
   const long rs = static_cast<long>(a.Hkv) * DH;  // elements per pool row
+  // The appended key (the stream's last, S - 1) is not read from the cache: this launch
+  // writes it.  The cache holds S_cache keys; the wave streams [w0, w_end) of them and the
+  // wave whose range would hold the new key folds it in afterwards.
+  int new_key = -1;
+  if constexpr (sizeof(KV) == 2)
+    if (a.k_new && S == a.pos[b] + 1) new_key = S - 1;
+  const int S_cache = new_key >= 0 ? S - 1 : S;
   const int w0 = t0 + wave * TPW;
-  const int w1 = min(w0 + TPW, S);
+  const int w_end = min(w0 + TPW, S_cache);
+  const bool owns_new = new_key >= w0 && new_key < w0 + TPW;
+  const float* kn = nullptr;
+  const float* vn = nullptr;
+  if (owns_new) {
+    kn = a.k_new + (static_cast<long>(b) * a.Hkv + kvh) * DH;
+    vn = a.v_new + (static_cast<long>(b) * a.Hkv + kvh) * DH;
+  }
 
   float m[G], lpart[G], acc[G][8];
 #pragma unroll
@@ -280,20 +356,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   }
   const int r = lane / CK::LPT;
 
-  if (w0 < w1) {
+  if (w0 < w_end) {
     // Ping-pong buffers: the loads of one chunk are in flight while the other is computed.
     CK A, Bb;
-    load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, w0, t0, w1, lane);
+    load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, w0, t0, w_end, lane);
     int c = w0;
     while (true) {
-      if (c + CK::CH < w1) load_chunk<DH, KV>(Bb, kbase, vbase, row_lds, rs, c + CK::CH, t0, w1, lane);
-      process_chunk<DH, G, KV>(A, qr, m, lpart, acc, c, w1, lane, a.scale_log2e);
+      if (c + CK::CH < w_end)
+        load_chunk<DH, KV>(Bb, kbase, vbase, row_lds, rs, c + CK::CH, t0, w_end, lane);
+      process_chunk<DH, G, KV>(A, qr, m, lpart, acc, c, w_end, lane, a.scale_log2e);
       c += CK::CH;
-      if (c >= w1) break;
-      if (c + CK::CH < w1) load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, c + CK::CH, t0, w1, lane);
-      process_chunk<DH, G, KV>(Bb, qr, m, lpart, acc, c, w1, lane, a.scale_log2e);
+      if (c >= w_end) break;
+      if (c + CK::CH < w_end)
+        load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, c + CK::CH, t0, w_end, lane);
+      process_chunk<DH, G, KV>(Bb, qr, m, lpart, acc, c, w_end, lane, a.scale_log2e);
       c += CK::CH;
-      if (c >= w1) break;
+      if (c >= w_end) break;
+    }
+  }
+  if constexpr (sizeof(KV) == 2) {
+    if (owns_new) {  // uniform over the wave
+      uint4 kw[CK::NCQ], vw;
+      append_key<DH, G>(kn, vn, qr, m, lpart, acc, lane, a.scale_log2e, kw, vw);
+      // write the new row into the cache (dropped past the pool, as the KV write does)
+      const long row = row_lds[(new_key - t0) >> 4] + (new_key & 15);
+      if (row < a.pool_rows) {
+        uint16_t* kdst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(kbase)) + row * rs;
+        uint16_t* vdst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(vbase)) + row * rs;
+        if (lane < 8)
+#pragma unroll
+          for (int cc = 0; cc < CK::NCQ; ++cc)
+            *reinterpret_cast<uint4*>(kdst + 8 * CK::EPV * cc + CK::EPV * (lane & 7)) = kw[cc];
+        if (lane < CK::LPT) *reinterpret_cast<uint4*>(vdst + 8 * (lane % CK::LPT)) = vw;
+      }
     }
   }
 
@@ -351,13 +446,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   }
 }
 
-// Split merge: one workgroup per (stream, q head), after the split kernel.  Wave 0
-// turns the split maxima/sums into normalised weights (one per split, in LDS); then every
-// thread sums its output dims over the splits with independent loads.
+// Split merge: one workgroup per (stream, q head), after the split kernel; thread d owns
+// output dim d.  Up to 16 splits' maxima, sums and partial rows are loaded together and
+// folded in with an online max, so a stream of <= 16 splits costs one memory round trip.
 template <int DH>
-__global__ __launch_bounds__(128) void gqa_decode_combine_kernel(DecodeArgs a, int split_len,
-                                                                 int Hq) {
-  __shared__ float wsp[1024];
+__global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, int split_len,
+                                                                int Hq) {
+  constexpr int kBatch = 16;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int S = stream_keys(a, b);
@@ -365,40 +460,38 @@ __global__ __launch_bounds__(128) void gqa_decode_combine_kernel(DecodeArgs a, i
   if (n_splits <= 1) return;  // written directly by the split kernel
   const long bh = static_cast<long>(b) * Hq + h;
   const long base = bh * a.max_splits;
-  const int tid = threadIdx.x;
-  if (tid < 64) {
-    float mx = -INFINITY;
-    for (int sp = tid; sp < n_splits; sp += 64) mx = fmaxf(mx, a.part_ml[(base + sp) * 2]);
-    mx = wave_max(mx);
-    float den = 0.0f;
-    for (int sp = tid; sp < n_splits; sp += 64) {
-      const float w = fast_exp2(a.part_ml[(base + sp) * 2] - mx);
-      wsp[sp] = w;
-      den = fmaf(w, a.part_ml[(base + sp) * 2 + 1], den);
+  const int d = threadIdx.x;
+  float M = -INFINITY, L = 0.0f, acc = 0.0f;
+  for (int s0 = 0; s0 < n_splits; s0 += kBatch) {
+    float ms[kBatch], ls[kBatch], os[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const long ps = base + min(s0 + i, n_splits - 1);  // in-range address for every i
+      ms[i] = a.part_ml[ps * 2];
+      ls[i] = a.part_ml[ps * 2 + 1];
+      os[i] = a.part_o[ps * DH + d];
     }
-    den = wave_sum(den);
-    const float inv = 1.0f / den;
-    for (int sp = tid; sp < n_splits; sp += 64) wsp[sp] *= inv;
-  }
-  __syncthreads();
-  for (int d = tid; d < DH; d += 128) {
-    const float* po = a.part_o + base * DH + d;
-    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
-    int sp = 0;
-    for (; sp + 3 < n_splits; sp += 4) {
-      o0 = fmaf(wsp[sp], po[static_cast<long>(sp) * DH], o0);
-      o1 = fmaf(wsp[sp + 1], po[static_cast<long>(sp + 1) * DH], o1);
-      o2 = fmaf(wsp[sp + 2], po[static_cast<long>(sp + 2) * DH], o2);
-      o3 = fmaf(wsp[sp + 3], po[static_cast<long>(sp + 3) * DH], o3);
+    float mx = M;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (s0 + i < n_splits) mx = fmaxf(mx, ms[i]);
+    const float c_old = M == mx ? 1.0f : fast_exp2(M - mx);
+    acc *= c_old;
+    L *= c_old;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const float w = s0 + i < n_splits ? fast_exp2(ms[i] - mx) : 0.0f;
+      acc = fmaf(w, os[i], acc);
+      L = fmaf(w, ls[i], L);
     }
-    for (; sp < n_splits; ++sp) o0 = fmaf(wsp[sp], po[static_cast<long>(sp) * DH], o0);
-    a.out[bh * DH + d] = (o0 + o1) + (o2 + o3);
+    M = mx;
   }
+  a.out[bh * DH + d] = acc * (1.0f / L);
 }
 
 template <int DH, int G, int SPLIT, typename KV>
 int launch_split(const DecodeArgs& args, int B, hipStream_t stream) {
-  dim3 grid(args.max_splits, args.Hkv, B);
+  dim3 grid(args.Hkv, B, args.max_splits);
   hipEvent_t ev0, ev1;
   take_timing_events(&ev0, &ev1);
   if (ev0) (void)hipEventRecord(ev0, stream);
@@ -406,7 +499,7 @@ int launch_split(const DecodeArgs& args, int B, hipStream_t stream) {
   int rc = check_launch("gqa_decode_kernel");
   if (ev1) (void)hipEventRecord(ev1, stream);
   if (rc || args.max_splits <= 1) return rc;
-  hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(128), 0, stream,
+  hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(DH), 0, stream,
                      args, SPLIT, args.Hkv * G);
   return check_launch("gqa_decode_combine_kernel");
 }
@@ -460,6 +553,12 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (!(p.Dh == 64 || p.Dh == 128) || !(G == 1 || G == 2 || G == 4))
     return fail(ORATOR_ERR_UNSUPPORTED, "gqa_decode: supported Dh {64,128}, Hq/Hkv {1,2,4}");
   if (p.capacity <= 0) return fail(ORATOR_ERR_INVALID, "gqa_decode: capacity must be > 0");
+  if (p.k_new) {
+    if (!p.v_new || p.kv_f32 || p.pos_mode != 0)
+      return fail(ORATOR_ERR_INVALID, "gqa_decode: append needs k and v rows, bf16 caches");
+    if ((reinterpret_cast<uintptr_t>(p.k_new) | reinterpret_cast<uintptr_t>(p.v_new)) & 15u)
+      return fail(ORATOR_ERR_INVALID, "gqa_decode: appended k/v rows must be 16-byte aligned");
+  }
   int page_shift = 0;
   if (p.page_table) {
     page_shift = ilog2_exact(p.page_size);
@@ -497,6 +596,9 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   args.max_splits = max_splits;
   args.capacity = p.capacity;
   args.scale_log2e = p.scale * 1.4426950408889634f;
+  args.k_new = p.k_new;
+  args.v_new = p.v_new;
+  args.pool_rows = p.pool_rows;
 
   if (p.kv_f32) return launch_kv<float>(args, p.B, p.Dh, G, split, stream);
   return launch_kv<uint16_t>(args, p.B, p.Dh, G, split, stream);
@@ -524,6 +626,60 @@ int orator_gqa_decode(const float* q, const uint16_t* kc, const uint16_t* vc, fl
   p.Dh = Dh;
   p.capacity = capacity;
   p.scale = scale;
+  return launch_gqa_decode(p, static_cast<hipStream_t>(stream));
+}
+
+// WriteKvCacheKernel + GqaDecodeAttnKernel of one decode step (asr_text_decoder.cu:412-418)
+// in one launch: the new token's K/V rows are written at pos and attended as the last key.
+int orator_gqa_decode_append(const float* q, const float* k_new, const float* v_new,
+                             uint16_t* kc, uint16_t* vc, float* out, int Hq, int Hkv, int Dh,
+                             const int* d_pos, int capacity, float scale, void* stream) {
+  if (Hq > 0 && (!k_new || !v_new)) return fail(ORATOR_ERR_INVALID, "gqa_decode_append: null k/v");
+  DecodeProblem p{};
+  p.q = q;
+  p.kpool = kc;
+  p.vpool = vc;
+  p.pos = d_pos;
+  p.out = out;
+  p.B = 1;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.Dh = Dh;
+  p.capacity = capacity;
+  p.scale = scale;
+  p.k_new = k_new;
+  p.v_new = v_new;
+  p.pool_rows = capacity;
+  return launch_gqa_decode(p, static_cast<hipStream_t>(stream));
+}
+
+int orator_gqa_decode_append_paged(const float* q, const float* k_new, const float* v_new,
+                                   uint16_t* kpool, uint16_t* vpool, const int* page_table,
+                                   int max_pages, int page_size, int n_pages, const int* d_pos,
+                                   float* out, int B, int Hq, int Hkv, int Dh, float scale,
+                                   void* stream) {
+  if (B > 0 && (!page_table || !k_new || !v_new))
+    return fail(ORATOR_ERR_INVALID, "gqa_decode_append_paged: null page table or k/v");
+  if (B > 0 && n_pages <= 0)
+    return fail(ORATOR_ERR_INVALID, "gqa_decode_append_paged: n_pages must be > 0");
+  DecodeProblem p{};
+  p.q = q;
+  p.kpool = kpool;
+  p.vpool = vpool;
+  p.page_table = page_table;
+  p.max_pages = max_pages;
+  p.page_size = page_size;
+  p.pos = d_pos;
+  p.out = out;
+  p.B = B;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.Dh = Dh;
+  p.capacity = max_pages * page_size;
+  p.scale = scale;
+  p.k_new = k_new;
+  p.v_new = v_new;
+  p.pool_rows = static_cast<long>(n_pages) * page_size;
   return launch_gqa_decode(p, static_cast<hipStream_t>(stream));
 }
 

@@ -56,6 +56,11 @@ struct DecodeProblem {
   int B, Hq, Hkv, Dh;
   int capacity;           // max keys any stream can attend (grid sizing)
   float scale;
+  // Append (bf16 caches, pos_mode 0): K/V rows [B][Hkv][Dh] fp32 written at pos[b] and
+  // attended as the last key in the same launch; pool_rows bounds the write.
+  const float* k_new;
+  const float* v_new;
+  long pool_rows;
 };
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
 

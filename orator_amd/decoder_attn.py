@@ -42,6 +42,24 @@ def GqaDecodeAttnPaged(q, kpool, vpool, page_table, max_pages: int, page_size: i
          page_size, ptr(d_pos), ptr(out), B, Hq, Hkv, Dh, scale, _sh(stream))
 
 
+def GqaDecodeAttnAppend(q, k_new, v_new, kc, vc, out, Hq: int, Hkv: int, Dh: int, d_pos,
+                        capacity: int, scale: float, stream=None) -> None:
+    """WriteKvCacheKernel + GqaDecodeAttnKernel of one decode step in one launch: k_new/v_new
+    [Hkv, Dh] fp32 are stored at *d_pos and q attends the *d_pos + 1 keys including them."""
+    call("orator_gqa_decode_append", ptr(q), ptr(k_new), ptr(v_new), ptr(kc), ptr(vc), ptr(out),
+         Hq, Hkv, Dh, ptr(d_pos), capacity, scale, _sh(stream))
+
+
+def GqaDecodeAttnAppendPaged(q, k_new, v_new, kpool, vpool, page_table, max_pages: int,
+                             page_size: int, n_pages: int, d_pos, out, B: int, Hq: int, Hkv: int,
+                             Dh: int, scale: float, stream=None) -> None:
+    """Batched paged append + decode: stream b stores k_new/v_new[b] at d_pos[b] through
+    page-table row b and attends d_pos[b] + 1 keys."""
+    call("orator_gqa_decode_append_paged", ptr(q), ptr(k_new), ptr(v_new), ptr(kpool), ptr(vpool),
+         ptr(page_table), max_pages, page_size, n_pages, ptr(d_pos), ptr(out), B, Hq, Hkv, Dh,
+         scale, _sh(stream))
+
+
 def GqaCacheAttn(q, kc, vc, out, Tq: int, Hq: int, Hkv: int, Dh: int, d_pos0, capacity: int,
                  scale: float, stream=None) -> None:
     """Prefill: row t of q [Tq, Hq, Dh] (absolute position *d_pos0 + t) attends keys

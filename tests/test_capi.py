@@ -72,6 +72,13 @@ def test_unsupported_decode_shapes_rejected():
     # paged: page size must be a power of two >= 16
     assert lib.orator_gqa_decode_paged(FAKE, FAKE, FAKE, FAKE, 8, 24, FAKE, FAKE, 1, 16, 8, 128,
                                        0.1, None) == _lib.ORATOR_ERR_INVALID
+    # append: k/v rows required, a positive pool size for the paged form, aligned rows
+    assert lib.orator_gqa_decode_append(FAKE, None, FAKE, FAKE, FAKE, FAKE, 16, 8, 128, FAKE, 64,
+                                        0.1, None) == _lib.ORATOR_ERR_INVALID
+    assert lib.orator_gqa_decode_append_paged(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 8, 16, 0, FAKE,
+                                              FAKE, 1, 16, 8, 128, 0.1, None) == _lib.ORATOR_ERR_INVALID
+    assert lib.orator_gqa_decode_append(FAKE, FAKE + 4, FAKE, FAKE, FAKE, FAKE, 16, 8, 128, FAKE,
+                                        64, 0.1, None) == _lib.ORATOR_ERR_INVALID
 
 
 def test_python_wrapper_raises_gpu_error():

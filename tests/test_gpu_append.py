@@ -1,0 +1,117 @@
+"""GPU parity: decode with the new token appended in the same launch (WriteKvCacheKernel +
+GqaDecodeAttnKernel of one decode step, src/model/asr_text_decoder.cu:412-418).
+
+The oracle runs the two reference steps in order: the bf16 KV write of the new rows, then the
+decode over pos + 1 keys.  Bar: attention outputs max |g - r| / max(|r|, 0.05) <= 1e-4 (fp32
+q, bf16 KV, fp32 accumulation); the written cache rows bit-exact, every other row untouched."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from gpu_helpers import down, empty, say, up
+from helpers import SplitMix64, rel_err
+from orator_amd import decoder_attn as da
+
+pytestmark = pytest.mark.gpu
+
+FLOOR, TOL = 0.05, 1e-4
+
+
+@pytest.mark.parametrize("pos,cap", [(0, 64), (1, 64), (31, 64), (32, 64), (63, 64), (256, 512),
+                                     (300, 512), (4096, 4224), (4223, 4224)])
+def test_append_contiguous_matches_write_then_decode(pos, cap):
+    Hq, Hkv, Dh = 16, 8, 128
+    r = SplitMix64(pos * 7 + cap)
+    kc = orc.to_bf16(r.normal((cap, Hkv, Dh)))
+    vc = orc.to_bf16(r.normal((cap, Hkv, Dh)))
+    q, kn, vn = r.normal((Hq, Dh)), r.normal((Hkv, Dh)), r.normal((Hkv, Dh))
+    scale = 1.0 / math.sqrt(Dh)
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    orc.kv_write(kn[None], vn[None], kc_ref, vc_ref, pos)
+    ref = orc.gqa_decode(q, kc_ref, vc_ref, pos, scale)
+    dk, dv = up(kc), up(vc)
+    dout = empty((Hq, Dh), np.float32)
+    say("append contiguous", pos, cap)
+    da.GqaDecodeAttnAppend(up(q), up(kn), up(vn), dk, dv, dout, Hq, Hkv, Dh,
+                           up(np.array([pos], np.int32)), cap, scale)
+    assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL
+    np.testing.assert_array_equal(down(dk, kc.shape, np.uint16), kc_ref)
+    np.testing.assert_array_equal(down(dv, vc.shape, np.uint16), vc_ref)
+
+
+def test_append_past_capacity_is_dropped_and_clamped():
+    """pos >= capacity: nothing is written and the capacity keys are attended, as the KV
+    write (rows past the capacity dropped) followed by the clamped decode."""
+    Hq, Hkv, Dh, cap = 16, 8, 128, 96
+    r = SplitMix64(5)
+    kc = orc.to_bf16(r.normal((cap, Hkv, Dh)))
+    vc = orc.to_bf16(r.normal((cap, Hkv, Dh)))
+    q, kn, vn = r.normal((Hq, Dh)), r.normal((Hkv, Dh)), r.normal((Hkv, Dh))
+    ref = orc.gqa_decode(q, kc, vc, cap - 1, 0.1)
+    dk, dv = up(kc), up(vc)
+    dout = empty((Hq, Dh), np.float32)
+    say("append past capacity")
+    da.GqaDecodeAttnAppend(up(q), up(kn), up(vn), dk, dv, dout, Hq, Hkv, Dh,
+                           up(np.array([cap + 5], np.int32)), cap, 0.1)
+    assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL
+    np.testing.assert_array_equal(down(dk, kc.shape, np.uint16), kc)
+    np.testing.assert_array_equal(down(dv, vc.shape, np.uint16), vc)
+
+
+@pytest.mark.parametrize("lens", [[1], [1025, 2049, 17, 4097, 640, 1, 3333, 2000],
+                                  [4097 + i for i in range(16)]])
+def test_append_paged_ragged_streams(lens):
+    """lens[b] = keys after the append (pos = lens[b] - 1); random page tables over a pool with
+    spare pages."""
+    Hq, Hkv, Dh, ps = 16, 8, 128, 16
+    r = SplitMix64(sum(lens) + 3)
+    B = len(lens)
+    max_pages = max((n + ps - 1) // ps for n in lens)
+    n_pages = B * max_pages + 3
+    kp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    vp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    table = np.array(r.uniform(n_pages).argsort(), np.int32)[:B * max_pages].reshape(B, max_pages)
+    q, kn, vn = r.normal((B, Hq, Dh)), r.normal((B, Hkv, Dh)), r.normal((B, Hkv, Dh))
+    pos = np.array(lens, np.int32) - 1
+    scale = 1.0 / math.sqrt(Dh)
+    kp_ref, vp_ref = kp.copy(), vp.copy()
+    for b in range(B):
+        orc.kv_write_paged(kn[b][None], vn[b][None], kp_ref, vp_ref, table[b], ps, int(pos[b]))
+    ref = orc.gqa_decode_paged(q, kp_ref, vp_ref, table, ps, pos, scale, threads=8)
+    dk, dv = up(kp), up(vp)
+    dout = empty((B, Hq, Dh), np.float32)
+    say("append paged", lens[:4], B)
+    da.GqaDecodeAttnAppendPaged(up(q), up(kn), up(vn), dk, dv, up(table), max_pages, ps, n_pages,
+                                up(pos), dout, B, Hq, Hkv, Dh, scale)
+    assert rel_err(down(dout, (B, Hq, Dh)), ref, FLOOR) <= TOL
+    np.testing.assert_array_equal(down(dk, kp.shape, np.uint16), kp_ref)
+    np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp_ref)
+
+
+def test_append_equals_write_then_decode_on_device():
+    """Same inputs through orator_kv_write_paged + orator_gqa_decode_paged: same cache bits,
+    outputs equal to fp32 rounding (the appended key is folded in last)."""
+    Hq, Hkv, Dh, ps, B, L = 16, 8, 128, 16, 4, 2500
+    r = SplitMix64(99)
+    max_pages = (L + 1 + ps - 1) // ps
+    n_pages = B * max_pages
+    kp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    vp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    table = np.array(r.uniform(n_pages).argsort(), np.int32).reshape(B, max_pages)
+    q, kn, vn = r.normal((B, Hq, Dh)), r.normal((B, Hkv, Dh)), r.normal((B, Hkv, Dh))
+    pos = np.array([L, L - 7, 100, 0], np.int32)
+    dq, dkn, dvn, dt, dpos = up(q), up(kn), up(vn), up(table), up(pos)
+    k1, v1, k2, v2 = up(kp), up(vp), up(kp), up(vp)
+    o1, o2 = empty((B, Hq, Dh), np.float32), empty((B, Hq, Dh), np.float32)
+    say("append vs two launches")
+    da.WriteKvCachePaged(dkn, dvn, k1, v1, dt, max_pages, ps, n_pages, B, 1, Hkv, Dh, dpos)
+    da.GqaDecodeAttnPaged(dq, k1, v1, dt, max_pages, ps, dpos, o1, B, Hq, Hkv, Dh, 0.09)
+    da.GqaDecodeAttnAppendPaged(dq, dkn, dvn, k2, v2, dt, max_pages, ps, n_pages, dpos, o2, B, Hq,
+                                Hkv, Dh, 0.09)
+    np.testing.assert_array_equal(down(k1, kp.shape, np.uint16), down(k2, kp.shape, np.uint16))
+    np.testing.assert_array_equal(down(v1, vp.shape, np.uint16), down(v2, vp.shape, np.uint16))
+    assert rel_err(down(o2, (B, Hq, Dh)), down(o1, (B, Hq, Dh)), FLOOR) <= 2e-6
