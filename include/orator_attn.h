@@ -154,6 +154,95 @@ int orator_gqa_decode_append_paged(const float* q, const float* k_new, const flo
                                    float* out, int B, int Hq, int Hkv, int Dh, float scale,
                                    void* stream);
 
+/* ----------------------------------------------------- bf16-weight linear ---- */
+/* asr_gemm::LinearPre (include/model/asr_gemm.h:33-38, src/model/asr_gemm.cu:175-208):
+ * out[M,N] fp32 = act(in[M,K] W[N,K]^T + bias), in and W bf16, fp32 accumulation; act 0 none,
+ * 1 exact-erf GELU, 2 ReLU; bias may be NULL.  M == 1 runs a streaming GEMV, M > 1 an MFMA
+ * GEMM.  K % 8 == 0, in and W 16-byte aligned. */
+int orator_linear_pre(const uint16_t* in_bf16, const uint16_t* W_bf16, const float* bias,
+                      float* out, int M, int K, int N, int act, void* stream);
+/* asr_gemm::Linear (asr_gemm.h:27-31, asr_gemm.cu:160-167): the same with fp32 `in`, cast to
+ * bf16 (round to nearest even) into library workspace first. */
+int orator_linear(const float* in_f32, const uint16_t* W_bf16, const float* bias, float* out,
+                  int M, int K, int N, int act, void* stream);
+/* gemm::LaunchBf16Gemm (include/model/gemm.cuh:484-501): the MFMA GEMM for any M >= 1. */
+int orator_bf16_gemm(const uint16_t* in_bf16, const uint16_t* W_bf16, const float* bias,
+                     float* out, int M, int K, int N, int act, void* stream);
+
+/* ------------------------------------------------------- decode-step glue ---- */
+/* EmbedGatherKernel (src/model/asr_text_decoder.cu:38-45): out[i] = table[*d_token][i]
+ * (bf16 table [vocab, hidden] widened); hidden % 8 == 0, 16-byte aligned. */
+int orator_embed_gather(const uint16_t* table, const int* d_token, float* out, int hidden,
+                        void* stream);
+/* AddResidualKernel (asr_text_decoder.cu:30-34): a[i] += b[i]; 16-byte aligned. */
+int orator_add_residual(float* a, const float* b, long n, void* stream);
+/* RecordTokenKernel (asr_text_decoder.cu:50-55): out[*d_count] = *d_token (dropped at or past
+ * `capacity`), ++*d_count.  IncPosKernel (:58): ++*d_pos. */
+int orator_record_token(int* out, int* d_count, const int* d_token, int capacity, void* stream);
+int orator_inc_pos(int* d_pos, void* stream);
+
+/* ----------------------------------------------------------------- decoder ---- */
+/* AsrTextConfig (include/model/asr_text_decoder.h:30-42). */
+typedef struct OratorDecoderConfig {
+  int num_layers, hidden_size, num_q_heads, num_kv_heads, head_dim, intermediate_size,
+      vocab_size, max_seq_len;
+  float rms_norm_eps, rope_theta;
+} OratorDecoderConfig;
+/* One layer's device weights, in the reference's fused layout
+ * (src/model/asr_text_decoder.cu:288-307): qkv_w = q | k | v rows [(Hq + 2 Hkv) Dh, hidden],
+ * gateup_w = gate | up rows [2 I, hidden], o_w [hidden, Hq Dh], down_w [hidden, I], bf16;
+ * norms fp32 ([hidden], [Dh], [Dh], [hidden]).  The caller keeps them alive. */
+typedef struct OratorDecoderLayer {
+  const float* in_ln;
+  const float* q_norm;
+  const float* k_norm;
+  const float* post_ln;
+  const uint16_t* qkv_w;
+  const uint16_t* o_w;
+  const uint16_t* gateup_w;
+  const uint16_t* down_w;
+} OratorDecoderLayer;
+/* AsrTextDecoder (include/model/asr_text_decoder.h:45-112) over caller-owned device weights:
+ * embed [vocab, hidden] bf16, final_norm [hidden] fp32, lm_head [vocab, hidden] bf16 (NULL:
+ * tied to embed), layers[num_layers].  Owns the bf16 KV caches [max_seq_len][Hkv][Dh] per
+ * layer and all scratch.  head_dim must be 128. */
+int orator_decoder_create(const OratorDecoderConfig* cfg, const uint16_t* embed,
+                          const float* final_norm, const uint16_t* lm_head,
+                          const OratorDecoderLayer* layers, void** handle);
+int orator_decoder_destroy(void* handle);
+/* ResetCache (asr_text_decoder.h:51, .cu:338): cache length 0. */
+int orator_decoder_reset(void* handle);
+/* Embed (asr_text_decoder.h:53-54, .cu:340-346): the bf16 row of token_id widened into the
+ * host array out[hidden]. */
+int orator_decoder_embed(void* handle, int token_id, float* out);
+/* PrefillAt (asr_text_decoder.h:62-69, .cu:589-617): T embeddings [T, hidden] (host or
+ * device memory) at positions pos0 .. pos0+T-1; leaves the last row's logits; synchronises
+ * the stream. */
+int orator_decoder_prefill_at(void* handle, const float* embeds, int T, int pos0,
+                              void* stream);
+/* DecodeStep (asr_text_decoder.h:78, .cu:618-633): one embedding [hidden] (host or device)
+ * at pos; synchronises the stream. */
+int orator_decoder_decode_step(void* handle, const float* embed, int pos, void* stream);
+/* DecodeStepDevice (asr_text_decoder.h:80-85, .cu:656-671): gathers the embedding of the
+ * token id held in the device scalar d_token and runs the step at pos; no final sync. */
+int orator_decoder_decode_step_device(void* handle, const int* d_token, int pos, void* stream);
+/* Argmax (asr_text_decoder.h:89, .cu:635-641) over the current logits, two bans (-1 none). */
+int orator_decoder_argmax(void* handle, int ban0, int ban1, int* token, void* stream);
+/* ArgmaxToDevice (asr_text_decoder.h:91-93, .cu:643-647): the winning id into *d_out. */
+int orator_decoder_argmax_to_device(void* handle, int* d_out, int ban0, int ban1, void* stream);
+/* Device pointer to the current logits [vocab] (CopyLogits reads them). */
+int orator_decoder_logits(void* handle, float** d_logits);
+/* DecodeGreedy (asr_text_decoder.h:96-107, .cu:698-889): seeds from the current logits, emits
+ * up to max_new tokens into `tokens`, stops at eos0/eos1 (not emitted) or 6 identical tokens;
+ * EOS banned for the first ban_steps tokens; host sync every `batch` steps; use_graph replays
+ * captured step graphs.  *n_tokens = tokens emitted; the cache length counts every step run. */
+int orator_decoder_decode_greedy(void* handle, int start_pos, int max_new, int eos0, int eos1,
+                                 int ban_steps, int batch, int use_graph, int* tokens,
+                                 int* n_tokens, void* stream);
+/* TruncateCache / cache_len (asr_text_decoder.h:73-76). */
+int orator_decoder_truncate(void* handle, int len);
+int orator_decoder_cache_len(void* handle, int* len);
+
 /* ----------------------------------------------------------------- GEMM ---- */
 /* gemm::LaunchSgemm (include/model/gemm.cuh:160-174): out[M,N] = act(in[M,K] W[N,K]^T + bias),
  * act 0 none, 1 SiLU, 2 ReLU, 3 sigmoid (gemm.cuh:38-45); bias may be NULL. */

@@ -26,6 +26,8 @@
  *   orc_sgemm(_batched)     the reference's own test pattern (test_gemm_batched.cu:12-61)
  *                           against fp64 numpy matmul
  *   orc_argmax_banned       numpy argmax with bans; the reference tie rule on planted ties
+ *   orc_linear_bf16         fp64 numpy matmul of the bf16-decoded operands; GELU against
+ *                           math.erf; ReLU; bias
  */
 #include "orator_oracle.h"
 
@@ -615,6 +617,31 @@ void orc_sgemm_batched(const float* in, const float* W, float* out, int M, int K
                        int batch, long stride_in, long stride_w, long stride_out) {
   for (int b = 0; b < batch; ++b)
     orc_sgemm(in + b * stride_in, W + b * stride_w, NULL, out + b * stride_out, M, K, N, act);
+}
+
+/* asr_gemm::LinearPre (src/model/asr_gemm.cu:175-208; kernels :62-155): out[m,n] =
+ * act(sum_k bf16(in[m,k]) bf16(W[n,k]) + bias[n]), fp32 accumulation in k order; act 0 none,
+ * 1 exact-erf GELU 0.5 v (1 + erf(v / sqrt 2)) (:93-94), 2 ReLU (:95-96). */
+static float linear_act(float v, int act) {
+  if (act == 1) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+  if (act == 2) return v > 0.0f ? v : 0.0f;
+  return v;
+}
+
+void orc_linear_bf16(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
+                     int K, int N, int act) {
+  float* x = (float*)malloc(sizeof(float) * (size_t)K);
+  for (int m = 0; m < M; ++m) {
+    for (int kk = 0; kk < K; ++kk) x[kk] = orc_bf16_to_f32(in[(size_t)m * K + kk]);
+    for (int n = 0; n < N; ++n) {
+      const uint16_t* w = W + (size_t)n * K;
+      float acc = 0.0f;
+      for (int kk = 0; kk < K; ++kk) acc += x[kk] * orc_bf16_to_f32(w[kk]);
+      if (bias) acc += bias[n];
+      out[(size_t)m * N + n] = linear_act(acc, act);
+    }
+  }
+  free(x);
 }
 
 /* ------------------------------------------------------------------------- */

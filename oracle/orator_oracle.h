@@ -107,6 +107,10 @@ void orc_sgemm(const float* in, const float* W, const float* bias, float* out, i
 void orc_sgemm_batched(const float* in, const float* W, float* out, int M, int K, int N, int act,
                        int batch, long stride_in, long stride_w, long stride_out);
 
+/* ---- asr_gemm::LinearPre (src/model/asr_gemm.cu:175-208): bf16 in/W, fp32 accumulate ---- */
+void orc_linear_bf16(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
+                     int K, int N, int act);
+
 /* ---- a14 ArgmaxBanned (src/model/asr_ops.cu:300-333) ---- */
 int orc_argmax_banned(const float* x, int n, int ban0, int ban1);
 

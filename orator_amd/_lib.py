@@ -32,8 +32,46 @@ _l = C.c_long
 _f = C.c_float
 _sz = C.c_size_t
 
+class DecoderConfig(C.Structure):
+    """OratorDecoderConfig (AsrTextConfig, include/model/asr_text_decoder.h:30-42)."""
+    _fields_ = [("num_layers", _i), ("hidden_size", _i), ("num_q_heads", _i),
+                ("num_kv_heads", _i), ("head_dim", _i), ("intermediate_size", _i),
+                ("vocab_size", _i), ("max_seq_len", _i), ("rms_norm_eps", _f),
+                ("rope_theta", _f)]
+
+
+class DecoderLayer(C.Structure):
+    """OratorDecoderLayer: one layer's device weight pointers (fused qkv and gate|up)."""
+    _fields_ = [("in_ln", _p), ("q_norm", _p), ("k_norm", _p), ("post_ln", _p),
+                ("qkv_w", _p), ("o_w", _p), ("gateup_w", _p), ("down_w", _p)]
+
+
 # name -> argument types (all return int status)
 SIGNATURES: dict[str, list] = {
+    # bf16-weight linear and decode-step glue
+    "orator_linear_pre": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "orator_linear": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "orator_bf16_gemm": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "orator_embed_gather": [_p, _p, _p, _i, _p],
+    "orator_add_residual": [_p, _p, _l, _p],
+    "orator_record_token": [_p, _p, _p, _i, _p],
+    "orator_inc_pos": [_p, _p],
+    # decoder
+    "orator_decoder_create": [C.POINTER(DecoderConfig), _p, _p, _p, C.POINTER(DecoderLayer),
+                              C.POINTER(_p)],
+    "orator_decoder_destroy": [_p],
+    "orator_decoder_prefill_at": [_p, _p, _i, _i, _p],
+    "orator_decoder_decode_step": [_p, _p, _i, _p],
+    "orator_decoder_decode_step_device": [_p, _p, _i, _p],
+    "orator_decoder_argmax_to_device": [_p, _p, _i, _i, _p],
+    "orator_decoder_embed": [_p, _i, _p],
+    "orator_decoder_reset": [_p],
+    "orator_decoder_argmax": [_p, _i, _i, C.POINTER(_i), _p],
+    "orator_decoder_logits": [_p, C.POINTER(_p)],
+    "orator_decoder_decode_greedy": [_p, _i, _i, _i, _i, _i, _i, _i, C.POINTER(_i),
+                                     C.POINTER(_i), _p],
+    "orator_decoder_truncate": [_p, _i],
+    "orator_decoder_cache_len": [_p, C.POINTER(_i)],
     # runtime
     "orator_version": [],
     "orator_device_count": [C.POINTER(_i)],

@@ -544,6 +544,13 @@ int split_override() {
 
 }  // namespace
 
+size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity) {
+  int split = 256;
+  if (split_override()) split = split_override();
+  const size_t max_splits = (static_cast<size_t>(capacity) + split - 1) / split;
+  return static_cast<size_t>(B) * Hq * max_splits * (Dh + 2) * sizeof(float);
+}
+
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (p.B <= 0 || p.Hq <= 0 || p.Hkv <= 0 || p.Dh <= 0) return ORATOR_OK;  // reference no-op
   if (!p.q || !p.kpool || !p.vpool || (!p.pos && p.pos_mode == 0) || !p.out)

@@ -1,0 +1,552 @@
+// The ASR text decoder on the attention path: prefill, single-token decode and greedy
+// decoding with the reference's stop rules, composed from this library's operators.
+//
+// Mirrors AsrTextDecoder (include/model/asr_text_decoder.h:45-186,
+// src/model/asr_text_decoder.cu:360-889):
+//  * Forward (prefill, :457-583): per layer RmsNorm -> bf16 -> q, k, v projections ->
+//    QK-RMSNorm + RoPE + KV write (one fused launch here) -> causal attention over the cache
+//    (fp32-mode MFMA kernel) -> o projection + residual -> RmsNorm -> gate, up -> SwiGLU ->
+//    down + residual; then the last row's final norm and the LM head.
+//  * DecodeForwardOnStream (:360-455): the same with M = 1 projections (one fused q|k|v and
+//    one gate|up GEMV) and the split-K decode attention; everything on the stream, reading
+//    the position from a device scalar, allocation-free -- so one step can be captured in a
+//    graph and replayed at any position.
+//  * DecodeGreedy (:698-889): seed argmax of the prefill logits (EOS banned while fewer than
+//    ban_steps tokens exist), then step bodies (record token, embed gather, forward, banned
+//    argmax, position + 1) in batches with one host sync per batch; the host harvests the
+//    recorded tokens and stops at EOS (not emitted) or after 6 identical tokens in a row (the
+//    6th is emitted).  Steps past the stop in the same batch still advance the cache length,
+//    as in the reference.  Two graphs (EOS banned / not) are captured once and replayed;
+//    without graphs the same bodies run eagerly.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace orator_hip {
+namespace {
+
+template <typename T>
+int dalloc(T** p, size_t n) {
+  *p = nullptr;
+  if (n == 0) return ORATOR_OK;
+  return check_hip(hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T)), "decoder hipMalloc");
+}
+
+struct Decoder {
+  OratorDecoderConfig c{};
+  const uint16_t* embed = nullptr;
+  const float* final_norm = nullptr;
+  const uint16_t* lm_head = nullptr;
+  std::vector<OratorDecoderLayer> layers;
+  std::vector<uint16_t*> kc, vc;  // per layer [max_seq_len][Hkv][Dh] bf16
+  int cache_len = 0;
+
+  // prefill scratch (grown to the prefill length)
+  int cap_t = 0;
+  float *x = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr,
+        *proj = nullptr, *gate = nullptr, *up = nullptr;
+  uint16_t* norm_bf16 = nullptr;
+  int* pos_dev = nullptr;  // [cap_t + 1]: positions, then pos0
+  int* pos_host = nullptr; // pinned staging
+  // decode-step scratch (fixed addresses: captured graphs bake them in)
+  float *sx = nullptr, *snorm = nullptr, *sqkv = nullptr, *sattn = nullptr, *sproj = nullptr,
+        *sgateup = nullptr, *slastn = nullptr, *logits = nullptr;
+  uint16_t *snorm_bf16 = nullptr, *sattn_bf16 = nullptr, *sgate_bf16 = nullptr,
+           *slastn_bf16 = nullptr;
+  int *spos = nullptr, *stok = nullptr, *scount = nullptr, *sout = nullptr;
+  int sout_cap = 0;
+  int* host_int = nullptr;  // pinned staging for scalars
+  hipStream_t capture_stream = nullptr;
+  hipGraphExec_t graph = nullptr, graph_banned = nullptr;
+  bool graph_ready = false;
+  int graph_ban0 = -1, graph_ban1 = -1;
+
+  int Qd() const { return c.num_q_heads * c.head_dim; }
+  int KVd() const { return c.num_kv_heads * c.head_dim; }
+  float scale() const { return 1.0f / std::sqrt(static_cast<float>(c.head_dim)); }
+
+  ~Decoder() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+    if (graph_banned) (void)hipGraphExecDestroy(graph_banned);
+    if (capture_stream) (void)hipStreamDestroy(capture_stream);
+    for (auto* p : kc) (void)hipFree(p);
+    for (auto* p : vc) (void)hipFree(p);
+    free_prefill();
+    for (void* p : {(void*)sx, (void*)snorm, (void*)sqkv, (void*)sattn, (void*)sproj,
+                    (void*)sgateup, (void*)slastn, (void*)logits, (void*)snorm_bf16,
+                    (void*)sattn_bf16, (void*)sgate_bf16, (void*)slastn_bf16, (void*)spos,
+                    (void*)stok, (void*)scount, (void*)sout})
+      if (p) (void)hipFree(p);
+    if (host_int) (void)hipHostFree(host_int);
+  }
+
+  void free_prefill() {
+    for (void* p : {(void*)x, (void*)norm, (void*)q, (void*)k, (void*)v, (void*)attn, (void*)proj,
+                    (void*)gate, (void*)up, (void*)norm_bf16, (void*)pos_dev})
+      if (p) (void)hipFree(p);
+    if (pos_host) (void)hipHostFree(pos_host);
+    x = norm = q = k = v = attn = proj = gate = up = nullptr;
+    norm_bf16 = nullptr;
+    pos_dev = pos_host = nullptr;
+    cap_t = 0;
+  }
+
+  int init() {
+    const size_t cache = static_cast<size_t>(c.max_seq_len) * KVd();
+    kc.assign(c.num_layers, nullptr);
+    vc.assign(c.num_layers, nullptr);
+    for (int l = 0; l < c.num_layers; ++l) {
+      if (int rc = dalloc(&kc[l], cache)) return rc;
+      if (int rc = dalloc(&vc[l], cache)) return rc;
+      if (int rc = check_hip(hipMemset(kc[l], 0, cache * 2), "decoder cache clear")) return rc;
+      if (int rc = check_hip(hipMemset(vc[l], 0, cache * 2), "decoder cache clear")) return rc;
+    }
+    const int H = c.hidden_size, I = c.intermediate_size;
+    int rc = 0;
+    if ((rc = dalloc(&sx, H)) || (rc = dalloc(&snorm, H)) || (rc = dalloc(&sqkv, Qd() + 2 * KVd())) ||
+        (rc = dalloc(&sattn, Qd())) || (rc = dalloc(&sproj, H)) || (rc = dalloc(&sgateup, 2 * I)) ||
+        (rc = dalloc(&slastn, H)) || (rc = dalloc(&logits, c.vocab_size)) ||
+        (rc = dalloc(&snorm_bf16, H)) || (rc = dalloc(&sattn_bf16, Qd())) ||
+        (rc = dalloc(&sgate_bf16, I)) || (rc = dalloc(&slastn_bf16, H)) || (rc = dalloc(&spos, 1)) ||
+        (rc = dalloc(&stok, 1)) || (rc = dalloc(&scount, 1)))
+      return rc;
+    if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&host_int), 4 * sizeof(int)),
+                        "decoder pinned scalars")))
+      return rc;
+    return check_hip(hipStreamCreate(&capture_stream), "decoder capture stream");
+  }
+
+  int grow_prefill(int T) {
+    if (T <= cap_t) return ORATOR_OK;
+    free_prefill();
+    const size_t H = c.hidden_size, I = c.intermediate_size, t = T;
+    int rc = 0;
+    if ((rc = dalloc(&x, t * H)) || (rc = dalloc(&norm, t * H)) || (rc = dalloc(&q, t * Qd())) ||
+        (rc = dalloc(&k, t * KVd())) || (rc = dalloc(&v, t * KVd())) ||
+        (rc = dalloc(&attn, t * Qd())) || (rc = dalloc(&proj, t * H)) ||
+        (rc = dalloc(&gate, t * I)) || (rc = dalloc(&up, t * I)) ||
+        (rc = dalloc(&norm_bf16, t * H)) || (rc = dalloc(&pos_dev, t + 1)))
+      return rc;
+    if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&pos_host), (t + 1) * sizeof(int)),
+                        "decoder pinned positions")))
+      return rc;
+    cap_t = T;
+    return ORATOR_OK;
+  }
+
+  // Forward of T rows of residual stream x at positions pos0.. (asr_text_decoder.cu:457-583).
+  int forward(int T, int pos0, hipStream_t s) {
+    const int H = c.hidden_size, I = c.intermediate_size, Hq = c.num_q_heads,
+              Hkv = c.num_kv_heads, Dh = c.head_dim;
+    const float eps = c.rms_norm_eps;
+    for (int t = 0; t < T; ++t) pos_host[t] = pos0 + t;
+    pos_host[T] = pos0;
+    int rc = check_hip(hipMemcpyAsync(pos_dev, pos_host, sizeof(int) * (T + 1),
+                                      hipMemcpyHostToDevice, s),
+                       "decoder positions");
+    const int* d_pos0 = pos_dev + T;
+    const long TH = static_cast<long>(T) * H;
+    for (int li = 0; li < c.num_layers && !rc; ++li) {
+      const OratorDecoderLayer& L = layers[li];
+      (rc = orator_rms_norm(x, L.in_ln, norm, T, H, eps, s)) ||
+          (rc = orator_f32_to_bf16(norm, norm_bf16, TH, s)) ||
+          (rc = orator_linear_pre(norm_bf16, L.qkv_w, nullptr, q, T, H, Qd(), 0, s)) ||
+          (rc = orator_linear_pre(norm_bf16, L.qkv_w + static_cast<size_t>(Qd()) * H, nullptr, k,
+                                  T, H, KVd(), 0, s)) ||
+          (rc = orator_linear_pre(norm_bf16, L.qkv_w + static_cast<size_t>(Qd() + KVd()) * H,
+                                  nullptr, v, T, H, KVd(), 0, s)) ||
+          (rc = orator_qk_norm_rope_kv_write(q, k, v, Qd(), KVd(), L.q_norm, L.k_norm, eps,
+                                             pos_dev, c.rope_theta, T, T, Hq, Hkv, Dh, kc[li],
+                                             vc[li], nullptr, 0, 0, c.max_seq_len, s)) ||
+          (rc = orator_gqa_prefill(q, kc[li], vc[li], attn, T, Hq, Hkv, Dh, d_pos0,
+                                   c.max_seq_len, scale(), s)) ||
+          (rc = orator_linear(attn, L.o_w, nullptr, proj, T, Qd(), H, 0, s)) ||
+          (rc = orator_add_residual(x, proj, TH, s)) ||
+          (rc = orator_rms_norm(x, L.post_ln, norm, T, H, eps, s)) ||
+          (rc = orator_f32_to_bf16(norm, norm_bf16, TH, s)) ||
+          (rc = orator_linear_pre(norm_bf16, L.gateup_w, nullptr, gate, T, H, I, 0, s)) ||
+          (rc = orator_linear_pre(norm_bf16, L.gateup_w + static_cast<size_t>(I) * H, nullptr, up,
+                                  T, H, I, 0, s)) ||
+          (rc = orator_swiglu(gate, up, gate, T * I, s)) ||
+          (rc = orator_linear(gate, L.down_w, nullptr, proj, T, I, H, 0, s)) ||
+          (rc = orator_add_residual(x, proj, TH, s));
+    }
+    if (rc) return rc;
+    cache_len = pos0 + T;
+    const float* last = x + static_cast<size_t>(T - 1) * H;
+    (rc = orator_rms_norm(last, final_norm, slastn, 1, H, eps, s)) ||
+        (rc = orator_linear(slastn, lm_head, nullptr, logits, 1, H, c.vocab_size, 0, s));
+    return rc;
+  }
+
+  // One-token forward of sx at the device position spos (asr_text_decoder.cu:360-455).
+  int decode_forward(hipStream_t s) {
+    const int H = c.hidden_size, I = c.intermediate_size, Hq = c.num_q_heads,
+              Hkv = c.num_kv_heads, Dh = c.head_dim;
+    const float eps = c.rms_norm_eps;
+    float* dq = sqkv;
+    float* dk = sqkv + Qd();
+    float* dv = sqkv + Qd() + KVd();
+    int rc = 0;
+    for (int li = 0; li < c.num_layers && !rc; ++li) {
+      const OratorDecoderLayer& L = layers[li];
+      (rc = orator_rms_norm(sx, L.in_ln, snorm, 1, H, eps, s)) ||
+          (rc = orator_f32_to_bf16(snorm, snorm_bf16, H, s)) ||
+          (rc = orator_linear_pre(snorm_bf16, L.qkv_w, nullptr, sqkv, 1, H, Qd() + 2 * KVd(), 0,
+                                  s)) ||
+          (rc = orator_qk_norm_rope_kv_write(dq, dk, dv, 0, 0, L.q_norm, L.k_norm, eps, spos,
+                                             c.rope_theta, 1, 1, Hq, Hkv, Dh, kc[li], vc[li],
+                                             nullptr, 0, 0, c.max_seq_len, s)) ||
+          (rc = orator_gqa_decode(dq, kc[li], vc[li], sattn, Hq, Hkv, Dh, spos, c.max_seq_len,
+                                  scale(), s)) ||
+          (rc = orator_f32_to_bf16(sattn, sattn_bf16, Qd(), s)) ||
+          (rc = orator_linear_pre(sattn_bf16, L.o_w, nullptr, sproj, 1, Qd(), H, 0, s)) ||
+          (rc = orator_add_residual(sx, sproj, H, s)) ||
+          (rc = orator_rms_norm(sx, L.post_ln, snorm, 1, H, eps, s)) ||
+          (rc = orator_f32_to_bf16(snorm, snorm_bf16, H, s)) ||
+          (rc = orator_linear_pre(snorm_bf16, L.gateup_w, nullptr, sgateup, 1, H, 2 * I, 0, s)) ||
+          (rc = orator_swiglu(sgateup, sgateup + I, sgateup, I, s)) ||
+          (rc = orator_f32_to_bf16(sgateup, sgate_bf16, I, s)) ||
+          (rc = orator_linear_pre(sgate_bf16, L.down_w, nullptr, sproj, 1, I, H, 0, s)) ||
+          (rc = orator_add_residual(sx, sproj, H, s));
+    }
+    if (rc) return rc;
+    (rc = orator_rms_norm(sx, final_norm, slastn, 1, H, eps, s)) ||
+        (rc = orator_f32_to_bf16(slastn, slastn_bf16, H, s)) ||
+        (rc = orator_linear_pre(slastn_bf16, lm_head, nullptr, logits, 1, H, c.vocab_size, 0, s));
+    return rc;
+  }
+
+  // Greedy step body (asr_text_decoder.cu:677-691): record, gather, forward, argmax, pos + 1.
+  int body(hipStream_t s, int ban0, int ban1) {
+    int rc = 0;
+    (rc = orator_record_token(sout, scount, stok, sout_cap, s)) ||
+        (rc = orator_embed_gather(embed, stok, sx, c.hidden_size, s)) ||
+        (rc = decode_forward(s)) ||
+        (rc = orator_argmax_banned(logits, c.vocab_size, ban0, ban1, stok, s)) ||
+        (rc = orator_inc_pos(spos, s));
+    return rc;
+  }
+
+  int set_int(int* dst, int v, hipStream_t s) {
+    *host_int = v;
+    int rc = check_hip(hipMemcpyAsync(dst, host_int, sizeof(int), hipMemcpyHostToDevice, s),
+                       "decoder scalar");
+    return rc ? rc : check_hip(hipStreamSynchronize(s), "decoder sync");
+  }
+
+  void drop_graphs() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+    if (graph_banned) (void)hipGraphExecDestroy(graph_banned);
+    graph = graph_banned = nullptr;
+    graph_ready = false;
+  }
+
+  int capture(int b0, int b1, hipGraphExec_t* exec) {
+    *exec = nullptr;
+    if (int rc = check_hip(hipStreamBeginCapture(capture_stream, hipStreamCaptureModeThreadLocal),
+                           "decoder begin capture"))
+      return rc;
+    const int rc_body = body(capture_stream, b0, b1);
+    hipGraph_t g = nullptr;
+    const hipError_t end = hipStreamEndCapture(capture_stream, &g);
+    if (rc_body) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc_body;
+    }
+    if (int rc = check_hip(end, "decoder end capture")) return rc;
+    const hipError_t inst = hipGraphInstantiate(exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    return check_hip(inst, "decoder graph instantiate");
+  }
+
+  int decode_greedy(int start_pos, int max_new, int eos0, int eos1, int ban_steps, int batch,
+                    bool use_graph, std::vector<int>& out, hipStream_t s) {
+    out.clear();
+    if (max_new <= 0) return ORATOR_OK;
+    if (batch <= 0) batch = 1;
+    if (max_new > sout_cap) {
+      if (sout) (void)hipFree(sout);
+      sout = nullptr;
+      sout_cap = 0;
+      if (int rc = dalloc(&sout, max_new)) return rc;
+      sout_cap = max_new;
+      drop_graphs();  // the graphs baked the old token buffer
+    }
+    if (graph_ready && (graph_ban0 != eos0 || graph_ban1 != eos1)) drop_graphs();
+    int rc = check_hip(hipStreamSynchronize(s), "decoder sync");
+    if (rc || (rc = set_int(spos, start_pos, s)) || (rc = set_int(scount, 0, s))) return rc;
+    std::vector<int> h_out(max_new);
+    bool stop = false;
+    auto harvest = [&](int upto) -> int {
+      if (int e = check_hip(hipMemcpy(h_out.data(), sout, sizeof(int) * upto,
+                                      hipMemcpyDeviceToHost),
+                            "decoder harvest"))
+        return e;
+      for (int i = static_cast<int>(out.size()); i < upto; ++i) {
+        const int t = h_out[i];
+        if (t == eos0 || t == eos1) {
+          stop = true;
+          return ORATOR_OK;
+        }
+        out.push_back(t);
+        if (out.size() >= 6) {
+          bool same = true;
+          for (size_t kk = out.size() - 6; kk + 1 < out.size(); ++kk)
+            if (out[kk] != out.back()) {
+              same = false;
+              break;
+            }
+          if (same) {
+            stop = true;
+            return ORATOR_OK;
+          }
+        }
+      }
+      return ORATOR_OK;
+    };
+    // seed: argmax of the prefill logits -> the first token
+    const bool seed_ban = 0 < ban_steps;
+    if ((rc = orator_argmax_banned(logits, c.vocab_size, seed_ban ? eos0 : -1,
+                                   seed_ban ? eos1 : -1, stok, s)) ||
+        (rc = check_hip(hipStreamSynchronize(s), "decoder sync")))
+      return rc;
+    int emitted = 0;
+    if (use_graph && !graph_ready) {
+      const bool ban_first = (0 + 1) < ban_steps;
+      if ((rc = body(s, ban_first ? eos0 : -1, ban_first ? eos1 : -1)) ||
+          (rc = check_hip(hipStreamSynchronize(s), "decoder sync")))
+        return rc;
+      ++emitted;
+      // the decode attention's split partials live in the capture stream's workspace
+      if ((rc = orator_workspace_reserve(
+               decode_workspace_bytes(1, c.num_q_heads, c.head_dim, c.max_seq_len),
+               capture_stream)))
+        return rc;
+      graph_ban0 = eos0;
+      graph_ban1 = eos1;
+      if (capture(eos0, eos1, &graph_banned) || capture(-1, -1, &graph)) {
+        // as the reference (asr_text_decoder.cu:846-847): a failed capture leaves the
+        // eager bodies in charge for this decoder
+        drop_graphs();
+        (void)hipGetLastError();
+      }
+      graph_ready = true;
+      if ((rc = harvest(emitted))) return rc;
+      if (stop) {
+        cache_len = start_pos + emitted;
+        return ORATOR_OK;
+      }
+    }
+    if (!(use_graph && graph && graph_banned)) {
+      while (emitted < max_new) {
+        const bool next_ban = (emitted + 1) < ban_steps;
+        const int this_batch = next_ban ? 1 : std::min(batch, max_new - emitted);
+        for (int b = 0; b < this_batch && !rc; ++b)
+          rc = body(s, next_ban ? eos0 : -1, next_ban ? eos1 : -1);
+        if (rc || (rc = check_hip(hipStreamSynchronize(s), "decoder sync"))) return rc;
+        emitted += this_batch;
+        if ((rc = harvest(emitted))) return rc;
+        if (stop) break;
+      }
+      cache_len = start_pos + emitted;
+      return ORATOR_OK;
+    }
+    while (emitted < max_new) {
+      const bool in_ban = (emitted + 1) < ban_steps;
+      hipGraphExec_t g = in_ban ? graph_banned : graph;
+      const int limit = in_ban ? std::min(ban_steps - 1, max_new) : max_new;
+      const int this_batch = std::max(1, std::min(batch, limit - emitted));
+      for (int b = 0; b < this_batch && !rc; ++b) rc = check_hip(hipGraphLaunch(g, s), "graph launch");
+      if (rc || (rc = check_hip(hipStreamSynchronize(s), "decoder sync"))) return rc;
+      emitted += this_batch;
+      if ((rc = harvest(emitted))) return rc;
+      if (stop) break;
+    }
+    cache_len = start_pos + emitted;
+    return ORATOR_OK;
+  }
+};
+
+Decoder* as_dec(void* h) { return static_cast<Decoder*>(h); }
+
+}  // namespace
+}  // namespace orator_hip
+
+using namespace orator_hip;
+
+extern "C" {
+
+int orator_decoder_create(const OratorDecoderConfig* cfg, const uint16_t* embed,
+                          const float* final_norm, const uint16_t* lm_head,
+                          const OratorDecoderLayer* layers, void** handle) {
+  if (!handle) return fail(ORATOR_ERR_INVALID, "decoder_create: null handle");
+  *handle = nullptr;
+  if (!cfg || !embed || !final_norm || !layers)
+    return fail(ORATOR_ERR_INVALID, "decoder_create: null pointer");
+  const OratorDecoderConfig& c = *cfg;
+  if (c.num_layers <= 0 || c.hidden_size <= 0 || c.num_q_heads <= 0 || c.num_kv_heads <= 0 ||
+      c.intermediate_size <= 0 || c.vocab_size <= 0 || c.max_seq_len <= 0)
+    return fail(ORATOR_ERR_INVALID, "decoder_create: sizes must be positive");
+  if (c.head_dim != 128 || c.num_q_heads % c.num_kv_heads ||
+      c.hidden_size % 8 || c.intermediate_size % 8)
+    return fail(ORATOR_ERR_UNSUPPORTED,
+                "decoder_create: head_dim 128, Hq multiple of Hkv, hidden and intermediate % 8");
+  for (int l = 0; l < c.num_layers; ++l) {
+    const OratorDecoderLayer& L = layers[l];
+    if (!L.in_ln || !L.q_norm || !L.k_norm || !L.post_ln || !L.qkv_w || !L.o_w || !L.gateup_w ||
+        !L.down_w)
+      return fail(ORATOR_ERR_INVALID, "decoder_create: null layer weight");
+  }
+  Decoder* d = new (std::nothrow) Decoder();
+  if (!d) return fail(ORATOR_ERR_CAPACITY, "decoder_create: out of host memory");
+  d->c = c;
+  d->embed = embed;
+  d->final_norm = final_norm;
+  d->lm_head = lm_head ? lm_head : embed;  // tied (asr_text_decoder.cu:255-257)
+  d->layers.assign(layers, layers + c.num_layers);
+  if (int rc = d->init()) {
+    delete d;
+    return rc;
+  }
+  *handle = d;
+  return ORATOR_OK;
+}
+
+int orator_decoder_destroy(void* handle) {
+  delete as_dec(handle);
+  return ORATOR_OK;
+}
+
+int orator_decoder_prefill_at(void* handle, const float* embeds, int T, int pos0, void* stream) {
+  Decoder* d = as_dec(handle);
+  if (!d || !embeds) return fail(ORATOR_ERR_INVALID, "decoder_prefill: null pointer");
+  if (T <= 0) return ORATOR_OK;
+  if (pos0 < 0 || pos0 + T > d->c.max_seq_len)
+    return fail(ORATOR_ERR_CAPACITY, "decoder_prefill: positions past max_seq_len");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = d->grow_prefill(T);
+  if (!rc)
+    rc = check_hip(hipMemcpyAsync(d->x, embeds, sizeof(float) * T * d->c.hidden_size,
+                                  hipMemcpyDefault, s),
+                   "decoder embeds");
+  if (!rc) rc = d->forward(T, pos0, s);
+  return rc ? rc : check_hip(hipStreamSynchronize(s), "decoder sync");
+}
+
+int orator_decoder_decode_step(void* handle, const float* embed, int pos, void* stream) {
+  Decoder* d = as_dec(handle);
+  if (!d || !embed) return fail(ORATOR_ERR_INVALID, "decoder_decode_step: null pointer");
+  if (pos < 0 || pos >= d->c.max_seq_len)
+    return fail(ORATOR_ERR_CAPACITY, "decoder_decode_step: position past max_seq_len");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = check_hip(hipMemcpyAsync(d->sx, embed, sizeof(float) * d->c.hidden_size,
+                                    hipMemcpyDefault, s),
+                     "decoder embed");
+  if (!rc) rc = d->set_int(d->spos, pos, s);
+  d->cache_len = pos + 1;
+  if (!rc) rc = d->decode_forward(s);
+  return rc ? rc : check_hip(hipStreamSynchronize(s), "decoder sync");
+}
+
+int orator_decoder_decode_step_device(void* handle, const int* d_token, int pos, void* stream) {
+  Decoder* d = as_dec(handle);
+  if (!d || !d_token) return fail(ORATOR_ERR_INVALID, "decoder_decode_step_device: null pointer");
+  if (pos < 0 || pos >= d->c.max_seq_len)
+    return fail(ORATOR_ERR_CAPACITY, "decoder_decode_step_device: position past max_seq_len");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = d->set_int(d->spos, pos, s);
+  d->cache_len = pos + 1;
+  if (!rc) rc = orator_embed_gather(d->embed, d_token, d->sx, d->c.hidden_size, s);
+  return rc ? rc : d->decode_forward(s);
+}
+
+int orator_decoder_argmax_to_device(void* handle, int* d_out, int ban0, int ban1, void* stream) {
+  Decoder* d = as_dec(handle);
+  if (!d || !d_out) return fail(ORATOR_ERR_INVALID, "decoder_argmax_to_device: null pointer");
+  return orator_argmax_banned(d->logits, d->c.vocab_size, ban0, ban1, d_out,
+                              static_cast<hipStream_t>(stream));
+}
+
+int orator_decoder_embed(void* handle, int token_id, float* out) {
+  Decoder* d = as_dec(handle);
+  if (!d || !out) return fail(ORATOR_ERR_INVALID, "decoder_embed: null pointer");
+  if (token_id < 0 || token_id >= d->c.vocab_size)
+    return fail(ORATOR_ERR_INVALID, "decoder_embed: token id out of range");
+  const int H = d->c.hidden_size;
+  std::vector<uint16_t> row(H);
+  if (int rc = check_hip(hipMemcpy(row.data(), d->embed + static_cast<size_t>(token_id) * H,
+                                   sizeof(uint16_t) * H, hipMemcpyDeviceToHost),
+                         "decoder_embed copy"))
+    return rc;
+  for (int i = 0; i < H; ++i) {
+    const uint32_t bits = static_cast<uint32_t>(row[i]) << 16;
+    std::memcpy(out + i, &bits, sizeof(float));
+  }
+  return ORATOR_OK;
+}
+
+int orator_decoder_reset(void* handle) {
+  Decoder* d = as_dec(handle);
+  if (!d) return fail(ORATOR_ERR_INVALID, "decoder_reset: null handle");
+  d->cache_len = 0;
+  return ORATOR_OK;
+}
+
+int orator_decoder_argmax(void* handle, int ban0, int ban1, int* token, void* stream) {
+  Decoder* d = as_dec(handle);
+  if (!d || !token) return fail(ORATOR_ERR_INVALID, "decoder_argmax: null pointer");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = orator_argmax_banned(d->logits, d->c.vocab_size, ban0, ban1, d->stok, s);
+  if (!rc) rc = check_hip(hipMemcpyAsync(d->host_int, d->stok, sizeof(int), hipMemcpyDeviceToHost, s),
+                          "decoder argmax copy");
+  if (!rc) rc = check_hip(hipStreamSynchronize(s), "decoder sync");
+  if (!rc) *token = *d->host_int;
+  return rc;
+}
+
+int orator_decoder_logits(void* handle, float** d_logits) {
+  Decoder* d = as_dec(handle);
+  if (!d || !d_logits) return fail(ORATOR_ERR_INVALID, "decoder_logits: null pointer");
+  *d_logits = d->logits;
+  return ORATOR_OK;
+}
+
+int orator_decoder_decode_greedy(void* handle, int start_pos, int max_new, int eos0, int eos1,
+                                 int ban_steps, int batch, int use_graph, int* tokens,
+                                 int* n_tokens, void* stream) {
+  Decoder* d = as_dec(handle);
+  if (!d || !n_tokens || (max_new > 0 && !tokens))
+    return fail(ORATOR_ERR_INVALID, "decoder_decode_greedy: null pointer");
+  *n_tokens = 0;
+  if (start_pos < 0 || start_pos + max_new > d->c.max_seq_len)
+    return fail(ORATOR_ERR_CAPACITY, "decoder_decode_greedy: positions past max_seq_len");
+  std::vector<int> out;
+  const int rc = d->decode_greedy(start_pos, max_new, eos0, eos1, ban_steps, batch, use_graph != 0,
+                                  out, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  if (!out.empty()) std::memcpy(tokens, out.data(), sizeof(int) * out.size());
+  *n_tokens = static_cast<int>(out.size());
+  return ORATOR_OK;
+}
+
+int orator_decoder_truncate(void* handle, int len) {
+  Decoder* d = as_dec(handle);
+  if (!d) return fail(ORATOR_ERR_INVALID, "decoder_truncate: null handle");
+  d->cache_len = len;
+  return ORATOR_OK;
+}
+
+int orator_decoder_cache_len(void* handle, int* len) {
+  Decoder* d = as_dec(handle);
+  if (!d || !len) return fail(ORATOR_ERR_INVALID, "decoder_cache_len: null pointer");
+  *len = d->cache_len;
+  return ORATOR_OK;
+}
+
+}  // extern "C"

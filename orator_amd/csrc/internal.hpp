@@ -63,6 +63,8 @@ struct DecodeProblem {
   long pool_rows;
 };
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
+// Workspace bytes a decode launch over B streams of `capacity` keys needs (split partials).
+size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity);
 
 int launch_sgemm(const float* in, const float* W, const float* bias, float* out, int M, int K,
                  int N, int act, int batch, long stride_in, long stride_w, long stride_out,

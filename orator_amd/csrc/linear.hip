@@ -1,0 +1,243 @@
+// bf16-weight linear layers of the decoder (gfx950): out[M,N] = act(bf16(in)[M,K] W[N,K]^T
+// + bias), fp32 accumulation.
+//
+// Replaces asr_gemm::Linear / LinearPre (include/model/asr_gemm.h:27-38,
+// src/model/asr_gemm.cu:160-208) and gemm::LaunchBf16Gemm (include/model/gemm.cuh:384-501):
+// activation 0 none, 1 exact-erf GELU, 2 ReLU (gemm.cuh:289-293).
+//
+//  * M == 1 (decode step) is HBM-bound: a weight stream of N*K*2 bytes.  One wave computes
+//    4 output rows; each lane reads 16 contiguous bytes of each row per step, so a wave
+//    instruction moves one contiguous 1 KB piece of a row, and the k loop is unrolled so a
+//    lane keeps 16 such loads in flight.  x (4-12 KB) is read through the caches.
+//  * M > 1 (prefill) is MFMA-bound: 128 x 128 output tiles per workgroup, 4 waves of
+//    64 x 64 (2 x 2 v_mfma_f32_32x32x16_bf16 blocks); both operands are K-contiguous in
+//    memory, exactly the MFMA fragment layout, staged through double-buffered padded LDS
+//    (K steps of 32; 80-byte rows keep the fragment reads conflict-free).
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace orator_hip {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+  if (act == 1) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+  if (act == 2) return fmaxf(v, 0.0f);
+  return v;
+}
+
+// ------------------------------------------------------------------- GEMV (M = 1) ----
+constexpr int kGemvRows = 4;    // output rows per wave
+constexpr int kGemvWaves = 4;   // waves per workgroup
+constexpr int kGemvUnroll = 4;  // 512-element k steps per loop iteration
+
+__device__ __forceinline__ float dot8(const u32x4_t w, const u32x4_t x) {
+  float d = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    d = fmaf(bf16_lo(w[j]), bf16_lo(x[j]), d);
+    d = fmaf(bf16_hi(w[j]), bf16_hi(x[j]), d);
+  }
+  return d;
+}
+
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_bf16_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ W,
+    const float* __restrict__ bias, float* __restrict__ out, int K, int N, int act) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * kGemvWaves + wave) * kGemvRows;
+  if (row0 >= N) return;
+  const int nchunk = K >> 3;  // 16-byte chunks per row
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x);
+  const u32x4_t* wr[kGemvRows];
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r)
+    wr[r] = reinterpret_cast<const u32x4_t*>(W + static_cast<long>(min(row0 + r, N - 1)) * K);
+  float acc[kGemvRows] = {};
+  int c = lane;
+  for (; c + 64 * (kGemvUnroll - 1) < nchunk; c += 64 * kGemvUnroll) {
+    u32x4_t wv[kGemvUnroll][kGemvRows], xx[kGemvUnroll];
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; ++u) {
+      xx[u] = xv[c + 64 * u];
+#pragma unroll
+      for (int r = 0; r < kGemvRows; ++r) wv[u][r] = __builtin_nontemporal_load(wr[r] + c + 64 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; ++u)
+#pragma unroll
+      for (int r = 0; r < kGemvRows; ++r) acc[r] += dot8(wv[u][r], xx[u]);
+  }
+  for (; c < nchunk; c += 64) {
+    const u32x4_t xx = xv[c];
+#pragma unroll
+    for (int r = 0; r < kGemvRows; ++r) acc[r] += dot8(__builtin_nontemporal_load(wr[r] + c), xx);
+  }
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane < kGemvRows && row0 + lane < N) {
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < kGemvRows; ++r)
+      if (lane == r) v = acc[r];
+    if (bias) v += bias[row0 + lane];
+    out[row0 + lane] = apply_act(v, act);
+  }
+}
+
+// ------------------------------------------------------------------- GEMM (M > 1) ----
+constexpr int kTM = 128, kTN = 128, kTK = 32;
+constexpr int kLRow = kTK + 8;  // padded LDS row (bf16): 80 bytes
+
+__device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restrict__ A,
+                                                        const uint16_t* __restrict__ W,
+                                                        const float* __restrict__ bias,
+                                                        float* __restrict__ out, int M, int K,
+                                                        int N, int act) {
+  __shared__ __align__(16) uint16_t as[2][kTM][kLRow];
+  __shared__ __align__(16) uint16_t ws[2][kTN][kLRow];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;  // this wave's 64 x 64 quadrant
+  const int m0 = blockIdx.y * kTM, n0 = blockIdx.x * kTN;
+  // loader: rows tid/4 and tid/4 + 64 of each tile, 16-byte chunk tid%4 (8 k values)
+  const int lr = tid >> 2, lc = tid & 3;
+  u32x4_t ra[2], rw[2];
+  auto load = [&](int k0) {
+    const int kk = k0 + 8 * lc;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int m = m0 + lr + 64 * h, n = n0 + lr + 64 * h;
+      ra[h] = (m < M && kk < K)
+                  ? *reinterpret_cast<const u32x4_t*>(A + static_cast<long>(m) * K + kk)
+                  : u32x4_t{0, 0, 0, 0};
+      rw[h] = (n < N && kk < K)
+                  ? *reinterpret_cast<const u32x4_t*>(W + static_cast<long>(n) * K + kk)
+                  : u32x4_t{0, 0, 0, 0};
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      *reinterpret_cast<u32x4_t*>(&as[buf][lr + 64 * h][8 * lc]) = ra[h];
+      *reinterpret_cast<u32x4_t*>(&ws[buf][lr + 64 * h][8 * lc]) = rw[h];
+    }
+  };
+  f32x16_t acc[2][2] = {};
+  const int n_k = (K + kTK - 1) / kTK;
+  load(0);
+  store(0);
+  lds_barrier();
+  for (int t = 0; t < n_k; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < n_k) load((t + 1) * kTK);
+#pragma unroll
+    for (int ks = 0; ks < kTK / 16; ++ks) {
+      bf16x8_t fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        fa[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(
+                                                 &as[buf][64 * wm + 32 * i + (lane & 31)]
+                                                    [16 * ks + 8 * (lane >> 5)]));
+        fb[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(
+                                                 &ws[buf][64 * wn + 32 * i + (lane & 31)]
+                                                    [16 * ks + 8 * (lane >> 5)]));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+    }
+    if (t + 1 < n_k) store(buf ^ 1);
+    lds_barrier();
+  }
+  // C block (i, j): lane holds column n = 32j + lane%32 and rows 8q + 4(lane/32) + e
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + 64 * wn + 32 * j + (lane & 31);
+    if (n >= N) continue;
+    const float bv = bias ? bias[n] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (m < M) out[static_cast<long>(m) * N + n] = apply_act(acc[i][j][e] + bv, act);
+      }
+  }
+}
+
+int check_linear(const void* in, const uint16_t* W, const float* out, int K, int act,
+                 const char* who) {
+  if (!in || !W || !out) return fail(ORATOR_ERR_INVALID, std::string(who) + ": null pointer");
+  if (act < 0 || act > 2) return fail(ORATOR_ERR_INVALID, std::string(who) + ": act must be 0-2");
+  if (K % 8) return fail(ORATOR_ERR_UNSUPPORTED, std::string(who) + ": K must be a multiple of 8");
+  if ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15u)
+    return fail(ORATOR_ERR_INVALID, std::string(who) + ": in and W must be 16-byte aligned");
+  return ORATOR_OK;
+}
+
+}  // namespace
+
+int launch_bf16_gemm(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
+                     int K, int N, int act, hipStream_t stream) {
+  if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;  // reference no-op
+  if (int rc = check_linear(in, W, out, K, act, "bf16_gemm")) return rc;
+  const dim3 grid((N + kTN - 1) / kTN, (M + kTM - 1) / kTM);
+  hipLaunchKernelGGL(gemm_bf16_kernel, grid, dim3(256), 0, stream, in, W, bias, out, M, K, N, act);
+  return check_launch("gemm_bf16_kernel");
+}
+
+int launch_linear_pre(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
+                      int K, int N, int act, hipStream_t stream) {
+  if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;
+  if (int rc = check_linear(in, W, out, K, act, "linear")) return rc;
+  if (M == 1) {
+    const int per_wg = kGemvRows * kGemvWaves;
+    hipLaunchKernelGGL(gemv_bf16_kernel, dim3((N + per_wg - 1) / per_wg), dim3(64 * kGemvWaves), 0,
+                       stream, in, W, bias, out, K, N, act);
+    return check_launch("gemv_bf16_kernel");
+  }
+  return launch_bf16_gemm(in, W, bias, out, M, K, N, act, stream);
+}
+
+}  // namespace orator_hip
+
+using namespace orator_hip;
+
+extern "C" {
+
+int orator_linear_pre(const uint16_t* in_bf16, const uint16_t* W_bf16, const float* bias,
+                      float* out, int M, int K, int N, int act, void* stream) {
+  return launch_linear_pre(in_bf16, W_bf16, bias, out, M, K, N, act,
+                           static_cast<hipStream_t>(stream));
+}
+
+int orator_linear(const float* in_f32, const uint16_t* W_bf16, const float* bias, float* out,
+                  int M, int K, int N, int act, void* stream) {
+  if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;
+  if (!in_f32) return fail(ORATOR_ERR_INVALID, "linear: null pointer");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const long n = static_cast<long>(M) * K;
+  uint16_t* in_bf16 = static_cast<uint16_t*>(workspace(s, n * sizeof(uint16_t), 0));
+  if (!in_bf16) return ORATOR_ERR_HIP;
+  if (int rc = orator_f32_to_bf16(in_f32, in_bf16, n, stream)) return rc;
+  return launch_linear_pre(in_bf16, W_bf16, bias, out, M, K, N, act, s);
+}
+
+int orator_bf16_gemm(const uint16_t* in_bf16, const uint16_t* W_bf16, const float* bias,
+                     float* out, int M, int K, int N, int act, void* stream) {
+  return launch_bf16_gemm(in_bf16, W_bf16, bias, out, M, K, N, act,
+                          static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

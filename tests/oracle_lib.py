@@ -58,6 +58,7 @@ def lib() -> C.CDLL:
             "orc_sgemm": ([_F, _F, _F, _F, i, i, i, i], None),
             "orc_sgemm_batched": ([_F, _F, _F, i, i, i, i, i, l, l, l], None),
             "orc_argmax_banned": ([_F, i, i, i], i),
+            "orc_linear_bf16": ([_U16, _U16, _F, _F, i, i, i, i], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -274,3 +275,190 @@ def sgemm_batched(inp, W, act=0) -> np.ndarray:
     out = np.empty((B, M, N), np.float32)
     lib().orc_sgemm_batched(_f(inp), _f(W), _f(out), M, K, N, act, B, M * K, N * K, M * N)
     return out
+
+
+# ------------------------------------------------------------- bf16 linear ----
+def linear_bf16(inp, W, bias=None, act=0, threads: int = 1) -> np.ndarray:
+    """asr_gemm::LinearPre: inp [M,K] and W [N,K] as uint16 bf16 bits; fp32 out [M,N].
+    threads > 1 splits the N rows over a thread pool (ctypes drops the GIL)."""
+    inp = np.ascontiguousarray(inp, dtype=np.uint16)
+    W = np.ascontiguousarray(W, dtype=np.uint16)
+    M, K = inp.shape
+    N = W.shape[0]
+    b = f32c(bias) if bias is not None else None
+
+    def part(n0, n1):
+        o = np.empty((M, n1 - n0), np.float32)
+        bb = np.ascontiguousarray(b[n0:n1]) if b is not None else None
+        lib().orc_linear_bf16(_u16(inp), _u16(W[n0:n1]), _f(bb) if bb is not None else None,
+                              _f(o), M, K, n1 - n0, act)
+        return o
+
+    if threads <= 1 or N < 2 * threads:
+        return part(0, N)
+    from concurrent.futures import ThreadPoolExecutor
+    cuts = np.linspace(0, N, threads + 1).astype(int)
+    with ThreadPoolExecutor(threads) as ex:
+        parts = list(ex.map(lambda t: part(cuts[t], cuts[t + 1]), range(threads)))
+    return np.concatenate(parts, axis=1)
+
+
+# ----------------------------------------------------------------- decoder ----
+EOS_IDS = (151645, 151643)  # src/model/qwen3_asr.cc:160-161
+REPEAT_STOP = 6             # src/model/asr_text_decoder.cu:741-757
+
+
+class OracleDecoder:
+    """AsrTextDecoder restated on the oracle primitives (src/model/asr_text_decoder.cu).
+
+    cfg: dict with num_layers, hidden_size, num_q_heads, num_kv_heads, head_dim,
+    intermediate_size, vocab_size, max_seq_len, rms_norm_eps, rope_theta.  Weights are numpy:
+    embed / lm_head uint16 [vocab, hidden] (lm_head None = tied), final_norm fp32, and per layer
+    in_ln, q_norm, k_norm, post_ln fp32 plus qkv_w, o_w, gateup_w, down_w uint16 (fused)."""
+
+    def __init__(self, cfg, embed, final_norm, lm_head, layers, threads: int = 1):
+        self.c = dict(cfg)
+        self.embed = embed
+        self.final_norm = f32c(final_norm)
+        self.lm_head = embed if lm_head is None else lm_head
+        self.layers = layers
+        self.threads = threads
+        c = self.c
+        shape = (c["max_seq_len"], c["num_kv_heads"], c["head_dim"])
+        self.kc = [np.zeros(shape, np.uint16) for _ in range(c["num_layers"])]
+        self.vc = [np.zeros(shape, np.uint16) for _ in range(c["num_layers"])]
+        self.cache_len = 0
+        self.logits = np.zeros(c["vocab_size"], np.float32)
+
+    def _lin(self, x_bf16, W):
+        return linear_bf16(x_bf16, W, None, 0, self.threads)
+
+    def _layer_qkv(self, L, x, pos):
+        """RmsNorm -> bf16 -> q, k, v -> QK-RMSNorm -> RopeHalf (:518-535 / :398-411)."""
+        c = self.c
+        Hq, Hkv, Dh, H = c["num_q_heads"], c["num_kv_heads"], c["head_dim"], c["hidden_size"]
+        Qd, KVd = Hq * Dh, Hkv * Dh
+        T = x.shape[0]
+        nb = to_bf16(rms_norm(x, L["in_ln"], c["rms_norm_eps"]))
+        q = self._lin(nb, L["qkv_w"][:Qd])
+        k = self._lin(nb, L["qkv_w"][Qd:Qd + KVd])
+        v = self._lin(nb, L["qkv_w"][Qd + KVd:Qd + 2 * KVd])
+        q = rms_norm(q.reshape(T * Hq, Dh), L["q_norm"], c["rms_norm_eps"]).reshape(T, Hq, Dh)
+        k = rms_norm(k.reshape(T * Hkv, Dh), L["k_norm"], c["rms_norm_eps"]).reshape(T, Hkv, Dh)
+        q = rope_half(q, pos, c["rope_theta"])
+        k = rope_half(k, pos, c["rope_theta"])
+        assert H == x.shape[1]
+        return q, k, v.reshape(T, Hkv, Dh)
+
+    def _layer_tail(self, L, x, attn):
+        """o projection + residual, RmsNorm, gate/up, SwiGLU, down + residual (:542-556)."""
+        c = self.c
+        I, T = c["intermediate_size"], x.shape[0]
+        x = x + self._lin(to_bf16(attn.reshape(T, -1)), L["o_w"])
+        nb = to_bf16(rms_norm(x, L["post_ln"], c["rms_norm_eps"]))
+        gate = self._lin(nb, L["gateup_w"][:I])
+        up = self._lin(nb, L["gateup_w"][I:2 * I])
+        return x + self._lin(to_bf16(swiglu(gate, up)), L["down_w"])
+
+    def _head(self, last):
+        c = self.c
+        n = rms_norm(last.reshape(1, -1), self.final_norm, c["rms_norm_eps"])
+        self.logits = self._lin(to_bf16(n), self.lm_head)[0]
+
+    def prefill_at(self, embeds, pos0: int) -> None:
+        """Forward (:457-583) over T rows at positions pos0.. (causal attention a5)."""
+        x = f32c(embeds).copy()
+        T = x.shape[0]
+        pos = np.arange(pos0, pos0 + T, dtype=np.int32)
+        scale = 1.0 / np.sqrt(np.float32(self.c["head_dim"]))
+        for li, L in enumerate(self.layers):
+            q, k, v = self._layer_qkv(L, x, pos)
+            kv_write(k, v, self.kc[li], self.vc[li], pos0)
+            attn = gqa_prefill(q, self.kc[li], self.vc[li], pos0, float(scale),
+                               threads=self.threads)
+            x = self._layer_tail(L, x, attn)
+        self.cache_len = pos0 + T
+        self._head(x[-1])
+
+    def decode_step(self, embed_row, pos: int) -> None:
+        """DecodeForwardOnStream (:360-455): one row at pos, decode attention a6."""
+        x = f32c(embed_row).reshape(1, -1).copy()
+        scale = 1.0 / np.sqrt(np.float32(self.c["head_dim"]))
+        p = np.array([pos], np.int32)
+        for li, L in enumerate(self.layers):
+            q, k, v = self._layer_qkv(L, x, p)
+            kv_write(k, v, self.kc[li], self.vc[li], pos)
+            attn = gqa_decode(q[0], self.kc[li], self.vc[li], pos, float(scale))
+            x = self._layer_tail(L, x, attn[None])
+        self.cache_len = pos + 1
+        self._head(x[0])
+
+    def embed_row(self, token: int) -> np.ndarray:
+        return from_bf16(self.embed[token])
+
+    def argmax(self, ban0=-1, ban1=-1) -> int:
+        return argmax_banned(self.logits, ban0, ban1)
+
+    def decode_greedy(self, start_pos, max_new, eos0, eos1, ban_steps=3, batch=32,
+                      use_graph=True, graph_ready=False, choose=None):
+        """DecodeGreedy (:698-889).  Token j is the argmax with EOS banned iff j < ban_steps
+        (seed :767-770 and body argmax :690 under the schedules' ban flags); body k records
+        token k and forwards it at start_pos + k.  The host harvests at batch ends and stops at
+        EOS (excluded) or the 6th identical token in a row (included); every body of the last
+        batch still ran, so cache_len = start_pos + bodies run.  Returns (tokens, bodies).
+
+        choose(j, logits, ban0, ban1) -> token picks stream token j instead of the banned
+        argmax (a checker uses it to follow another implementation through near ties)."""
+        if max_new <= 0:
+            return [], 0
+        if choose is None:
+            def choose(_j, _logits, b0, b1):
+                return self.argmax(b0, b1)
+        cums = greedy_schedule(max_new, ban_steps, batch, use_graph, graph_ready)
+        toks = [choose(0, self.logits, *((eos0, eos1) if 0 < ban_steps else (-1, -1)))]
+        out, stop_at, bodies = [], None, 0
+        for end in cums:
+            while bodies < end:  # run body `bodies`
+                k = bodies
+                self.decode_step(self.embed_row(toks[k]), start_pos + k)
+                ban = (eos0, eos1) if (k + 1) < ban_steps else (-1, -1)
+                toks.append(choose(k + 1, self.logits, *ban))
+                bodies += 1
+            for i in range(len(out), end):
+                t = toks[i]
+                if t in (eos0, eos1):
+                    stop_at = i
+                    break
+                out.append(t)
+                if len(out) >= REPEAT_STOP and len(set(out[-REPEAT_STOP:])) == 1:
+                    stop_at = i
+                    break
+            if stop_at is not None:
+                break
+        self.cache_len = start_pos + bodies
+        return out, bodies
+
+
+def greedy_schedule(max_new, ban_steps, batch, use_graph, graph_ready):
+    """Cumulative body counts at each host harvest of DecodeGreedy
+    (src/model/asr_text_decoder.cu:801-884): the eager loop runs banned bodies one at a time
+    then batches (:855-866); the graph path first runs one eager warm-up body when the graphs
+    are not captured yet (:802-830), then replays the banned graph up to ban_steps - 1 bodies
+    and the unbanned graph in batches (:871-884)."""
+    batch = max(1, batch)
+    cums, emitted = [], 0
+    if not use_graph:
+        while emitted < max_new:
+            nb = (emitted + 1) < ban_steps
+            emitted += 1 if nb else min(batch, max_new - emitted)
+            cums.append(emitted)
+        return cums
+    if not graph_ready:
+        emitted = 1
+        cums.append(1)
+    while emitted < max_new:
+        in_ban = (emitted + 1) < ban_steps
+        limit = min(ban_steps - 1, max_new) if in_ban else max_new
+        emitted += max(1, min(batch, limit - emitted))
+        cums.append(emitted)
+    return cums

@@ -86,3 +86,31 @@ def test_python_wrapper_raises_gpu_error():
     with pytest.raises(_lib.GpuError) as e:
         asr_ops.RmsNorm(None, FAKE, FAKE, 4, 128, 1e-6)
     assert e.value.code == _lib.ORATOR_ERR_INVALID
+
+
+def test_linear_and_decoder_validation():
+    """asr_gemm / decoder argument checks run before any device work."""
+    import ctypes as C
+    lib = _lib.lib()
+    assert lib.orator_linear_pre(FAKE, FAKE, None, FAKE, 1, 12, 8, 0, None) == \
+        _lib.ORATOR_ERR_UNSUPPORTED  # K % 8
+    assert lib.orator_linear_pre(FAKE, FAKE, None, FAKE, 4, 16, 8, 3, None) == \
+        _lib.ORATOR_ERR_INVALID  # act
+    assert lib.orator_linear_pre(FAKE + 2, FAKE, None, FAKE, 4, 16, 8, 0, None) == \
+        _lib.ORATOR_ERR_INVALID  # alignment
+    assert lib.orator_linear_pre(None, None, None, None, 0, 16, 8, 0, None) == _lib.ORATOR_OK
+    cfg = _lib.DecoderConfig(1, 512, 4, 2, 64, 1024, 4096, 64, 1e-6, 1e6)
+    layers = (_lib.DecoderLayer * 1)(_lib.DecoderLayer(*([FAKE] * 8)))
+    h = C.c_void_p()
+    assert lib.orator_decoder_create(C.byref(cfg), FAKE, FAKE, None, layers, C.byref(h)) == \
+        _lib.ORATOR_ERR_UNSUPPORTED  # head_dim 64
+    assert h.value is None
+    cfg.head_dim, cfg.num_q_heads = 128, 3
+    assert lib.orator_decoder_create(C.byref(cfg), FAKE, FAKE, None, layers, C.byref(h)) == \
+        _lib.ORATOR_ERR_UNSUPPORTED  # Hq % Hkv
+    cfg.num_q_heads = 4
+    layers[0].o_w = None
+    assert lib.orator_decoder_create(C.byref(cfg), FAKE, FAKE, None, layers, C.byref(h)) == \
+        _lib.ORATOR_ERR_INVALID
+    assert lib.orator_decoder_prefill_at(None, FAKE, 4, 0, None) == _lib.ORATOR_ERR_INVALID
+    assert lib.orator_embed_gather(FAKE, FAKE, FAKE, 12, None) == _lib.ORATOR_ERR_INVALID

@@ -1,0 +1,301 @@
+"""GPU parity: the bf16 linear layers, the decode-step glue kernels and the ASR text decoder
+(AsrTextDecoder: Prefill/PrefillAt, DecodeStep, TruncateCache, DecodeGreedy) against the oracle.
+
+Bars:
+  * linear: |g - r| <= 3e-5 * (sum_k |x_k w_k| + 1) against the fp64 product of the bf16
+    operands (fp32 accumulation in another order);
+  * glue kernels: bit-exact;
+  * decoder logits: max |g - r| <= 1e-2 * max |r| and identical argmax.  The composition
+    re-rounds activations to bf16 before every projection, so fp32-level differences move
+    elements by whole bf16 steps and the steps cascade: the oracle itself moves by 0.38% of
+    max |r| (small config) when its input embeddings move by one fp32 ulp, or when its
+    linear layers accumulate in fp64 instead of fp32 (0.40%).  The reference's own bar for
+    the same check is max |g - r| <= 2.0 (test/unit/model/test_asr_decoder.cc:66-72);
+  * greedy tokens: identical ids and cache length.  The oracle follows the device's token
+    wherever the two differ only on a near tie (the device's pick within the logit bar of the
+    oracle's maximum, never a banned id); every such step is printed, and everywhere else the
+    oracle's own argmax must be the device's token."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import decoder_model as dm
+import oracle_lib as orc
+from gpu_helpers import down, empty, say, up
+from helpers import SplitMix64
+from orator_amd import asr_gemm, decoder_ops
+from orator_amd.decoder import AsrTextConfig, AsrTextDecoder
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-2
+
+
+# ----------------------------------------------------------------------- linear ----
+@pytest.mark.parametrize("M,K,N", [(1, 2048, 4096), (1, 6144, 2048), (1, 512, 37), (1, 8, 5),
+                                   (2, 512, 130), (17, 1024, 257), (128, 2048, 128),
+                                   (300, 2048, 1024), (503, 2048, 4096)])
+@pytest.mark.parametrize("act,with_bias", [(0, False), (1, True), (2, True)])
+def test_linear_pre_vs_oracle(M, K, N, act, with_bias):
+    r = SplitMix64(M * 7 + K + N + act)
+    x = orc.to_bf16(r.normal((M, K)))
+    W = orc.to_bf16(r.normal((N, K), 0.05))
+    bias = r.normal(N) if with_bias else None
+    xd, Wd = orc.from_bf16(x).astype(np.float64), orc.from_bf16(W).astype(np.float64)
+    ref = xd @ Wd.T + (bias if with_bias else 0.0)
+    ref = {0: ref, 1: 0.5 * ref * (1 + np.vectorize(math.erf)(ref / math.sqrt(2))),
+           2: np.maximum(ref, 0)}[act]
+    bound = 3e-5 * (np.abs(xd) @ np.abs(Wd).T + 1.0)
+    out = empty((M, N), np.float32)
+    say("linear_pre", M, K, N, act)
+    asr_gemm.LinearPre(up(x), up(W), up(bias) if with_bias else None, out, M, K, N, act)
+    got = down(out, (M, N))
+    assert np.all(np.abs(got - ref) <= bound), np.max(np.abs(got - ref) / bound)
+
+
+@pytest.mark.parametrize("M", [1, 33])
+def test_linear_f32_input_casts_rne(M):
+    """Linear == F32ToBf16 + LinearPre (the cast is round-to-nearest-even, bit-exact)."""
+    K, N = 1024, 300
+    r = SplitMix64(M)
+    x = r.normal((M, K))
+    W = orc.to_bf16(r.normal((N, K), 0.05))
+    a, b = empty((M, N), np.float32), empty((M, N), np.float32)
+    Wd = up(W)
+    say("linear f32", M)
+    asr_gemm.Linear(up(x), Wd, None, a, M, K, N, 0)
+    asr_gemm.LinearPre(up(orc.to_bf16(x)), Wd, None, b, M, K, N, 0)
+    np.testing.assert_array_equal(down(a, (M, N)), down(b, (M, N)))
+
+
+def test_bf16_gemm_m1_matches_gemv():
+    K, N = 2048, 1000
+    r = SplitMix64(11)
+    x, W = orc.to_bf16(r.normal((1, K))), orc.to_bf16(r.normal((N, K), 0.05))
+    a, b = empty((1, N), np.float32), empty((1, N), np.float32)
+    say("bf16_gemm M=1")
+    xd, Wd = up(x), up(W)
+    asr_gemm.LinearPre(xd, Wd, None, a, 1, K, N, 0)
+    from orator_amd import gemm
+    gemm.LaunchBf16Gemm(xd, Wd, None, b, 1, K, N, 0)
+    ga, gb = down(a, (N,)), down(b, (N,))
+    ref = orc.linear_bf16(x, W)[0]
+    assert np.max(np.abs(ga - ref)) < 1e-3 and np.max(np.abs(gb - ref)) < 1e-3
+
+
+# ------------------------------------------------------------------ glue kernels ----
+def test_glue_kernels_bit_exact():
+    r = SplitMix64(5)
+    V, H = 64, 2048
+    table = orc.to_bf16(r.normal((V, H)))
+    tok = up(np.array([37], np.int32))
+    out = empty((H,), np.float32)
+    say("embed_gather")
+    decoder_ops.EmbedGather(up(table), tok, out, H)
+    np.testing.assert_array_equal(down(out, (H,)), orc.from_bf16(table[37]))
+    a, b = r.normal(1027), r.normal(1027)
+    da = up(a)
+    decoder_ops.AddResidual(da, up(b), 1027)
+    np.testing.assert_array_equal(down(da, (1027,)), a + b)
+    rec, cnt, pos = up(np.full(4, -1, np.int32)), up(np.zeros(1, np.int32)), up(np.array([9], np.int32))
+    for t in (5, 6, 7, 8, 9):  # the fifth record is past the capacity of 4
+        decoder_ops.RecordToken(rec, cnt, up(np.array([t], np.int32)), 4)
+        decoder_ops.IncPos(pos)
+    np.testing.assert_array_equal(down(rec, (4,), np.int32), [5, 6, 7, 8])
+    assert int(down(cnt, (1,), np.int32)[0]) == 5 and int(down(pos, (1,), np.int32)[0]) == 14
+
+
+# ---------------------------------------------------------------------- decoder ----
+def build(cfg, weights):
+    embed, final_norm, lm_head, layers = weights
+    dl = [{k: up(v) for k, v in L.items()} for L in layers]
+    dec = AsrTextDecoder(AsrTextConfig(**cfg), up(embed), up(final_norm),
+                         up(lm_head) if lm_head is not None else None, dl)
+    return dec
+
+
+def top2_gap(logits, ban=()):
+    x = np.array(logits, np.float64)
+    for b in ban:
+        if b >= 0:
+            x[b] = -np.inf
+    s = np.sort(x)
+    return s[-1] - s[-2]
+
+
+def follower(got):
+    """choose() for OracleDecoder.decode_greedy: take the device's token j when it is the
+    oracle's banned argmax or within the logit bar of it (a near tie); else the argmax."""
+    near = []
+
+    def choose(j, logits, b0, b1):
+        best = orc.argmax_banned(logits, b0, b1)
+        if j < len(got) and int(got[j]) != best:
+            t = int(got[j])
+            gap = float(logits[best] - logits[t])
+            assert t not in (b0, b1) and gap <= LOGIT_TOL * np.max(np.abs(logits)), (j, t, best,
+                                                                                     gap)
+            near.append((j, t, best, gap))
+            return t
+        return best
+    return choose, near
+
+
+def greedy_check(o, got, *args, **kw):
+    choose, near = follower(got)
+    want, bodies = o.decode_greedy(*args, **kw, choose=choose)
+    print("tokens", got, "near ties followed", near)
+    assert [int(t) for t in got] == want
+    return bodies
+
+
+def check_logits(got, ref, what):
+    err = np.max(np.abs(got - ref))
+    assert err <= LOGIT_TOL * np.max(np.abs(ref)), (what, err, np.max(np.abs(ref)))
+    assert int(np.argmax(got)) == int(np.argmax(ref)), what
+
+
+@pytest.fixture(scope="module")
+def small():
+    cfg = dm.SMALL
+    w = dm.make_weights(cfg, 21)
+    return cfg, w
+
+
+def test_prefill_logits_and_incremental(small):
+    """test/unit/model/test_asr_decoder.cc:50-123 on synthetic weights: Prefill logits and
+    argmax vs the oracle, split PrefillAt == one Prefill, TruncateCache + re-prefill."""
+    cfg, w = small
+    T = 97
+    emb = SplitMix64(7).normal((T, cfg["hidden_size"]), 0.02)
+    o = orc.OracleDecoder(cfg, *w, threads=8)
+    o.prefill_at(emb, 0)
+    say("decoder prefill", T)
+    dec = build(cfg, w)
+    dec.ResetCache()
+    dec.Prefill(emb, T)
+    assert dec.cache_len() == T
+    full = dec.CopyLogits()
+    check_logits(full, o.logits, "prefill")
+    assert dec.Argmax() == o.argmax()
+    split = T // 2
+    dec.ResetCache()
+    dec.PrefillAt(emb[:split], split, 0)
+    dec.PrefillAt(up(emb[split:]), T - split, split)  # device embeddings too
+    assert dec.cache_len() == T
+    inc = dec.CopyLogits()
+    assert dec.Argmax() == int(np.argmax(full))
+    assert np.max(np.abs(inc - full)) <= LOGIT_TOL * np.max(np.abs(full))
+    dec.TruncateCache(split)
+    assert dec.cache_len() == split
+    dec.PrefillAt(emb[split:], T - split, split)
+    assert dec.Argmax() == int(np.argmax(full))
+    dec.close()
+
+
+def test_decode_steps_teacher_forced(small):
+    """DecodeStep / DecodeStepDevice + Argmax logits vs the oracle, the oracle's tokens fed."""
+    cfg, w = small
+    T = 40
+    emb = SplitMix64(8).normal((T, cfg["hidden_size"]), 0.02)
+    o = orc.OracleDecoder(cfg, *w, threads=8)
+    o.prefill_at(emb, 0)
+    dec = build(cfg, w)
+    say("decoder decode steps")
+    dec.Prefill(emb, T)
+    tok = o.argmax()
+    dtok = up(np.array([tok], np.int32))
+    for step in range(12):
+        pos = T + step
+        o.decode_step(o.embed_row(tok), pos)
+        if step % 2:
+            dec.DecodeStep(dec.Embed(tok), pos)
+        else:
+            dec.DecodeStepDevice(dtok, pos)
+        assert dec.cache_len() == pos + 1
+        check_logits(dec.CopyLogits(), o.logits, f"step {step}")
+        tok = o.argmax()
+        dec.ArgmaxToDevice(dtok)
+        assert int(down(dtok, (1,), np.int32)[0]) == tok
+    dec.close()
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+@pytest.mark.parametrize("batch", [1, 4, 32])
+def test_decode_greedy_tokens(small, use_graph, batch):
+    """DecodeGreedy token ids and cache length identical to the oracle's greedy loop, across
+    two calls (the second replays already-captured graphs), with EOS ids that do and do not
+    occur."""
+    cfg, w = small
+    T = 64
+    emb = SplitMix64(9).normal((T, cfg["hidden_size"]), 0.02)
+    o = orc.OracleDecoder(cfg, *w, threads=8)
+    o.prefill_at(emb, 0)
+    free_run, _ = orc.OracleDecoder(cfg, *w, threads=8), None
+    free_run.prefill_at(emb, 0)
+    stream, _ = free_run.decode_greedy(T, 30, -5, -5, ban_steps=0, batch=30, use_graph=False)
+    # an EOS id that the free run emits at index 9 (first occurrence) and one it never emits
+    eos0 = stream[9] if stream[9] not in stream[:9] else -7
+    eos1 = next(t for t in range(cfg["vocab_size"]) if t not in stream)
+    dec = build(cfg, w)
+    say("decoder greedy", use_graph, batch)
+    dec.Prefill(emb, T)
+    got = dec.DecodeGreedy(T, 30, eos0, eos1, ban_steps=3, batch=batch, use_graph=use_graph)
+    bodies = greedy_check(o, got, T, 30, eos0, eos1, 3, batch, use_graph, graph_ready=False)
+    assert dec.cache_len() == T + bodies
+    # second call continues from the cache end: prefill 5 more rows then greedy again
+    more = SplitMix64(10).normal((5, cfg["hidden_size"]), 0.02)
+    p0 = o.cache_len
+    o.prefill_at(more, p0)
+    dec.PrefillAt(more, 5, p0)
+    check_logits(dec.CopyLogits(), o.logits, "prefill after greedy")
+    got2 = dec.DecodeGreedy(p0 + 5, 20, eos0, eos1, ban_steps=3, batch=batch,
+                            use_graph=use_graph)
+    bodies2 = greedy_check(o, got2, p0 + 5, 20, eos0, eos1, 3, batch, use_graph,
+                           graph_ready=use_graph)
+    assert dec.cache_len() == p0 + 5 + bodies2
+    dec.close()
+
+
+def test_decode_greedy_repetition_stop():
+    """Tied embeddings and tiny layer weights make the model repeat its input token: the
+    greedy loop stops after the 6th identical token (included)."""
+    cfg = dict(dm.SMALL, num_layers=1)
+    w = dm.make_weights(cfg, 31, tied=True, layer_scale=0.01)
+    T = 16
+    emb = SplitMix64(12).normal((T, cfg["hidden_size"]), 0.02)
+    o = orc.OracleDecoder(cfg, *w)
+    o.prefill_at(emb, 0)
+    dec = build(cfg, w)
+    say("decoder repetition stop")
+    dec.Prefill(emb, T)
+    got = dec.DecodeGreedy(T, 40, -3, -4, ban_steps=3, batch=4, use_graph=True)
+    bodies = greedy_check(o, got, T, 40, -3, -4, 3, 4, True, graph_ready=False)
+    assert len(got) < 40 and len(set(got[-6:])) == 1
+    assert dec.cache_len() == T + bodies
+    dec.close()
+
+
+def test_decoder_qwen_shapes():
+    """The real layer shapes (hidden 2048, 16/8 heads, MLP 6144, vocab 151936) on 2 layers:
+    prefill logits, then greedy tokens eager and graph-replayed."""
+    cfg = dm.QWEN_2L
+    w = dm.make_weights(cfg, 41, tied=True)  # lm_head tied to embed (asr_text_decoder.cu:255-257)
+    T = 128
+    emb = SplitMix64(13).normal((T, cfg["hidden_size"]), 0.02)
+    o = orc.OracleDecoder(cfg, *w, threads=16)
+    o.prefill_at(emb, 0)
+    dec = build(cfg, w)
+    say("decoder qwen shapes prefill", T)
+    dec.Prefill(emb, T)
+    check_logits(dec.CopyLogits(), o.logits, "qwen prefill")
+    print("top-2 gap at the seed", top2_gap(o.logits, orc.EOS_IDS))
+    got = dec.DecodeGreedy(T, 8, *orc.EOS_IDS, ban_steps=3, batch=4, use_graph=True)
+    greedy_check(o, got, T, 8, *orc.EOS_IDS, 3, 4, True, graph_ready=False)
+    dec.Prefill(emb, T)
+    got_eager = dec.DecodeGreedy(T, 8, *orc.EOS_IDS, ban_steps=3, batch=4, use_graph=False)
+    assert got_eager == got  # same device arithmetic, eager or replayed
+    dec.close()

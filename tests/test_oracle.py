@@ -441,3 +441,127 @@ def test_host_build_pos_emb_matches_oracle():
     from orator_amd.conformer_attn import BuildPosEmb
     for T, D in ((1, 512), (23, 512), (717, 512), (5, 7)):
         np.testing.assert_array_equal(BuildPosEmb(T, D), orc.build_pos_emb(T, D))
+
+
+# ---------------------------------------------------------------- bf16 linear ----
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 512, 37), (5, 1024, 64), (3, 2048, 9)])
+def test_linear_bf16_vs_fp64(M, K, N):
+    """asr_gemm::LinearPre on bf16 bits: fp64 matmul of the decoded operands, then bias and
+    the activation formulas (GELU from math.erf)."""
+    r = SplitMix64(M * K + N)
+    x, W = orc.to_bf16(r.normal((M, K))), orc.to_bf16(r.normal((N, K), 0.05))
+    bias = r.normal(N)
+    ref = orc.from_bf16(x).astype(np.float64) @ orc.from_bf16(W).astype(np.float64).T + bias
+    scale = np.abs(orc.from_bf16(x)).astype(np.float64) @ np.abs(orc.from_bf16(W)).T
+    for act, f in [(0, lambda v: v), (1, lambda v: 0.5 * v * (1 + math.erf(v / math.sqrt(2)))),
+                   (2, lambda v: max(v, 0.0))]:
+        got = orc.linear_bf16(x, W, bias, act)
+        want = np.vectorize(f)(ref)
+        assert np.max(np.abs(got - want) / (scale + 1.0)) < 1e-5, act
+    # no bias, threaded split over N is the same computation
+    np.testing.assert_array_equal(orc.linear_bf16(x, W, None, 0, threads=4),
+                                  orc.linear_bf16(x, W, None, 0))
+
+
+# -------------------------------------------------------------------- decoder ----
+
+
+def _fake_decoder(script, alt):
+    """A decoder whose argmax follows `script` (token k of the stream), answering `alt[k]`
+    when the scripted token is banned: isolates the greedy loop's host rules."""
+    d = orc.OracleDecoder.__new__(orc.OracleDecoder)
+    d.step = 0
+    d.steps_run = []
+    d.logits = None
+
+    def decode_step(_row, pos):
+        d.steps_run.append(pos)
+        d.step += 1
+
+    def argmax(b0=-1, b1=-1):
+        t = script[d.step]
+        return alt[d.step] if t in (b0, b1) else t
+
+    d.decode_step = decode_step
+    d.argmax = argmax
+    d.embed_row = lambda t: None
+    return d
+
+
+def test_greedy_schedule_known_answers():
+    """Batch boundaries of DecodeGreedy (src/model/asr_text_decoder.cu:801-884), worked by
+    hand for ban_steps 3, batch 4, max_new 10."""
+    assert orc.greedy_schedule(10, 3, 4, False, False) == [1, 2, 6, 10]
+    assert orc.greedy_schedule(10, 3, 4, True, False) == [1, 2, 6, 10]
+    assert orc.greedy_schedule(10, 3, 4, True, True) == [2, 6, 10]
+    assert orc.greedy_schedule(10, 0, 4, True, True) == [4, 8, 10]
+    assert orc.greedy_schedule(10, 0, 4, False, False) == [4, 8, 10]
+    assert orc.greedy_schedule(1, 3, 4, True, False) == [1]
+    assert orc.greedy_schedule(2, 5, 32, True, True) == [2]
+
+
+def test_greedy_stop_rules():
+    E0, E1 = 900, 901
+    # EOS at stream index 4 is not emitted; the batch [2, 6) ran to its end
+    d = _fake_decoder([5, 6, 7, 8, E0, 3, 3, 3, 3, 3, 3], [0] * 11)
+    out, bodies = d.decode_greedy(100, 10, E0, E1, ban_steps=3, batch=4, use_graph=False)
+    assert out == [5, 6, 7, 8] and bodies == 6 and d.cache_len == 106
+    assert d.steps_run == list(range(100, 106))
+    # six identical tokens in a row: the sixth is emitted
+    d = _fake_decoder([1, 2, 9, 9, 9, 9, 9, 9, 9, 9, 9, 9, 9], [0] * 13)
+    out, bodies = d.decode_greedy(0, 12, E0, E1, ban_steps=0, batch=32, use_graph=False)
+    assert out == [1, 2, 9, 9, 9, 9, 9, 9] and bodies == 12
+    # EOS banned for stream tokens 0..ban_steps-1 (the seed included), allowed after
+    d = _fake_decoder([E1, E0, E0, E1, 4], [11, 12, 13, 14, 15])
+    out, bodies = d.decode_greedy(0, 4, E0, E1, ban_steps=3, batch=1, use_graph=True)
+    assert out == [11, 12, 13] and bodies == 4
+    # no stop: max_new tokens
+    d = _fake_decoder(list(range(20)), [0] * 20)
+    out, bodies = d.decode_greedy(7, 9, E0, E1, ban_steps=3, batch=4, use_graph=True,
+                                  graph_ready=True)
+    assert out == list(range(9)) and bodies == 9 and d.cache_len == 16
+
+
+def _small_decoder(seed=1, **kw):
+    import decoder_model as dm
+    cfg = dict(dm.SMALL, num_layers=1, max_seq_len=64)
+    return cfg, orc.OracleDecoder(cfg, *dm.make_weights(cfg, seed, **kw))
+
+
+def test_decoder_split_prefill_and_decode_step_equivalence():
+    """The reference's T010 check (test/unit/model/test_asr_decoder.cc:76-123) on the
+    oracle: PrefillAt in two parts == one Prefill; TruncateCache + re-prefill; and a decode
+    step == the last row of a prefill one token longer."""
+    cfg, d = _small_decoder()
+    r = SplitMix64(3)
+    emb = r.normal((21, cfg["hidden_size"]), 0.02)
+    d.prefill_at(emb, 0)
+    full = d.logits.copy()
+    d.prefill_at(emb[:9], 0)
+    d.prefill_at(emb[9:], 9)
+    assert d.cache_len == 21
+    assert rel_err(d.logits, full, 0.05) < 1e-5
+    d.cache_len = 9
+    d.prefill_at(emb[9:], 9)
+    assert rel_err(d.logits, full, 0.05) < 1e-5
+    d.prefill_at(emb[:20], 0)
+    d.decode_step(emb[20], 20)
+    assert d.cache_len == 21
+    assert rel_err(d.logits, full, 0.05) < 1e-5
+
+
+def test_decoder_zero_layers_is_embedding_head():
+    """Zero projection weights leave the residual stream at the input: logits =
+    lm_head . bf16(RmsNorm(x) * final_norm), checked with fp64 numpy."""
+    cfg, d = _small_decoder(seed=2)
+    for L in d.layers:
+        for k in ("qkv_w", "o_w", "gateup_w", "down_w"):
+            L[k] = np.zeros_like(L[k])
+    x = SplitMix64(4).normal((5, cfg["hidden_size"]), 0.02)
+    d.prefill_at(x, 0)
+    last = x[-1].astype(np.float64)
+    n = last / np.sqrt(np.mean(last * last) + cfg["rms_norm_eps"]) * d.final_norm
+    want = orc.from_bf16(d.lm_head).astype(np.float64) @ orc.from_bf16(orc.to_bf16(n))
+    assert np.max(np.abs(d.logits - want)) < 1e-4 * np.max(np.abs(want))
