@@ -46,7 +46,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "conformer", "sweep"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "conformer", "sweep", "decoder"],
+                    default=None,
                     help="run one part (for profiling); prints that part's numbers only")
     return ap.parse_args()
 
@@ -257,6 +258,82 @@ def run_conformer(T: int = 717, layers: int = 17, H: int = 8, Dk: int = 64):
             "fp32_reference_order_us_per_layer": round(us_f32, 2)}
 
 
+def run_decoder_e2e(T: int = 2048, new: int = 256):
+    """the full synthetic Qwen3-ASR text decoder (28 layers, hidden 2048,
+    16/8 heads, head_dim 128, SwiGLU 6144, vocab 151936, lm_head tied to embed as
+    asr_text_decoder.cu:255-257), random-init bf16 weights, a 2048-row prefill of N(0, 0.02)
+    embeddings, then `new` greedy tokens through DecodeGreedy (graph replay, batch 32).  EOS is
+    disabled (ids -1) so the run is not cut short by a random model; the repetition stop of
+    the reference stays, and the tokens actually run are reported.  Per-token bytes: every
+    weight once (layers + lm_head) plus the K/V rows attended."""
+    from orator_amd._lib import call
+    from orator_amd.decoder import AsrTextConfig, AsrTextDecoder
+    from orator_amd.runtime import DeviceBuffer, synchronize
+
+    cfg = AsrTextConfig(max_seq_len=T + new)
+    H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    Qd, KVd = cfg.num_q_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+    rng = np.random.default_rng(77)
+    pool_n = 1 << 25
+    pool = DeviceBuffer.from_array(
+        (rng.standard_normal(pool_n, dtype=np.float32) * np.float32(0.02)).view(np.uint32)
+        .__rshift__(16).astype(np.uint16))
+
+    def weight(n):
+        # windows of the random pool at random offsets: every matrix differs, no host
+        # generation of 3.4 GB
+        buf = DeviceBuffer(n * 2)
+        off = 0
+        while off < n:
+            m = min(n - off, pool_n // 2)
+            src = int(rng.integers(0, pool_n - m + 1))
+            call("orator_memcpy_dtod", buf.ptr + 2 * off, pool.ptr + 2 * src, 2 * m, None)
+            off += m
+        return buf
+
+    def gain(n):
+        return DeviceBuffer.from_array((1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32))
+
+    embed = weight(V * H)
+    final_norm = gain(H)
+    layers = [dict(in_ln=gain(H), q_norm=gain(cfg.head_dim), k_norm=gain(cfg.head_dim),
+                   post_ln=gain(H), qkv_w=weight((Qd + 2 * KVd) * H), o_w=weight(H * Qd),
+                   gateup_w=weight(2 * I * H), down_w=weight(H * I))
+              for _ in range(cfg.num_layers)]
+    synchronize()
+    dec = AsrTextDecoder(cfg, embed, final_norm, None, layers)
+    emb = DeviceBuffer.from_array((0.02 * rng.standard_normal((T, H))).astype(np.float32))
+    # warm-up: one prefill and a short greedy run (captures the step graphs)
+    dec.Prefill(emb, T)
+    dec.DecodeGreedy(T, 8, -1, -1, ban_steps=3, batch=32)
+    t0 = time.perf_counter()
+    dec.Prefill(emb, T)  # synchronises
+    prefill_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    toks = dec.DecodeGreedy(T, new, -1, -1, ban_steps=3, batch=32, use_graph=True)
+    decode_s = time.perf_counter() - t0
+    bodies = dec.cache_len() - T
+    # eager bodies must give the same tokens as the replayed graphs
+    dec.Prefill(emb, T)
+    n_chk = min(32, len(toks))
+    eager = dec.DecodeGreedy(T, n_chk, -1, -1, ban_steps=3, batch=32, use_graph=False)
+    layer_w = (Qd + 2 * KVd) * H + H * Qd + 2 * I * H + H * I
+    w_bytes = 2 * (cfg.num_layers * layer_w + V * H)
+    kv_bytes = np.mean([cfg.num_layers * (T + k + 1) * KVd * 2 * 2 for k in range(bodies)])
+    tok_s = bodies / decode_s
+    dec.close()
+    return {"workload": "configs[4]: 28-layer Qwen3-ASR-shaped decoder, prefill 2048 + "
+                        f"{new} greedy tokens, batch 1",
+            "prefill_ms": round(prefill_s * 1e3, 2),
+            "prefill_tok_s": round(T / prefill_s, 1),
+            "decode_tokens": len(toks), "decode_steps_run": int(bodies),
+            "decode_tok_s": round(tok_s, 1), "decode_ms_per_token": round(decode_s * 1e3 / bodies, 4),
+            "decode_bytes_per_token": int(w_bytes + kv_bytes),
+            "decode_achieved_gbs": round((w_bytes + kv_bytes) * tok_s / 1e9, 1),
+            "decode_frac_of_hbm_peak": round((w_bytes + kv_bytes) * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+            "graph_equals_eager_first_tokens": [int(t) for t in eager] == [int(t) for t in toks[:n_chk]]}
+
+
 def run_decode_sweep():
     """BASELINE configs[2] sweep: decode kernel GB/s at L in {1024, 2048, 4096}, B in {1, 16}
     (one launch per layer over 28 layers' paged caches)."""
@@ -392,7 +469,8 @@ def main():
         part = {"decode": lambda: run_decode(args.steps, args.warmup),
                 "prefill": lambda: [run_prefill(503, da.PREFILL_BF16),
                                     run_prefill(2048, da.PREFILL_BF16)],
-                "conformer": run_conformer, "sweep": run_decode_sweep}[args.only]()
+                "conformer": run_conformer, "sweep": run_decode_sweep,
+                "decoder": run_decoder_e2e}[args.only]()
         print(json.dumps({"only": args.only, "result": part}, default=float))
         return
     dec = run_decode(args.steps, args.warmup)
@@ -406,6 +484,8 @@ def main():
     log("conformer:", conf)
     sweep = run_decode_sweep()
     log("decode sweep:", sweep)
+    e2e = run_decoder_e2e()
+    log("decoder e2e:", e2e)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": "GQA decode-attn HBM GB/s (% peak); prefill-attn TFLOP/s (% MFMA peak)",
@@ -440,6 +520,7 @@ def main():
         "prefill": pre,
         "conformer_relpos": conf,
         "decode_sweep": sweep,
+        "decoder_e2e": e2e,
     }
     print(json.dumps(line))
 
