@@ -544,8 +544,19 @@ int split_override() {
 
 }  // namespace
 
+// Split length: 256 keys (measured best for B = 16 at 4K keys: 128 makes the merge dominate,
+// 512+ leaves too few workgroups and lengthens the tail); 128 when the 256-key grid would not
+// give every CU a workgroup (a single stream: B = 1, 8 KV heads, ~2K keys -> 72 workgroups).
+int choose_split(int B, int Hkv, int G, int capacity) {
+  if (split_override()) return split_override();
+  if (G == 4) return 256;
+  const long wgs = static_cast<long>(B) * Hkv * ((capacity + 255) / 256);
+  const int cus = device_cu_count();
+  return (cus > 0 && wgs < cus) ? 128 : 256;
+}
+
 size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity) {
-  int split = 256;
+  int split = 128;  // the shortest split choose_split() returns
   if (split_override()) split = split_override();
   const size_t max_splits = (static_cast<size_t>(capacity) + split - 1) / split;
   return static_cast<size_t>(B) * Hq * max_splits * (Dh + 2) * sizeof(float);
@@ -574,11 +585,7 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
     if (static_cast<long>(p.max_pages) * p.page_size < p.capacity)
       return fail(ORATOR_ERR_CAPACITY, "gqa_decode: capacity exceeds max_pages*page_size");
   }
-  // 256-key splits: measured best on MI355X for B = 1 and B = 16 at 4K keys (128 makes the
-  // merge dominate, 512+ leaves too few workgroups and lengthens the tail).
-  int split = 256;
-  if (split_override()) split = split_override();
-  if (G == 4) split = 256;
+  const int split = choose_split(p.B, p.Hkv, G, p.capacity);
   const int max_splits = (p.capacity + split - 1) / split;
   const size_t part_o = static_cast<size_t>(p.B) * p.Hq * max_splits * p.Dh * sizeof(float);
   const size_t part_ml = static_cast<size_t>(p.B) * p.Hq * max_splits * 2 * sizeof(float);

@@ -54,10 +54,8 @@ struct Decoder {
   int* pos_dev = nullptr;  // [cap_t + 1]: positions, then pos0
   int* pos_host = nullptr; // pinned staging
   // decode-step scratch (fixed addresses: captured graphs bake them in)
-  float *sx = nullptr, *snorm = nullptr, *sqkv = nullptr, *sattn = nullptr, *sproj = nullptr,
-        *sgateup = nullptr, *slastn = nullptr, *logits = nullptr;
-  uint16_t *snorm_bf16 = nullptr, *sattn_bf16 = nullptr, *sgate_bf16 = nullptr,
-           *slastn_bf16 = nullptr;
+  float *sx = nullptr, *sqkv = nullptr, *sattn = nullptr, *sgateup = nullptr, *logits = nullptr;
+  void* argmax_scratch = nullptr;
   int *spos = nullptr, *stok = nullptr, *scount = nullptr, *sout = nullptr;
   int sout_cap = 0;
   int* host_int = nullptr;  // pinned staging for scalars
@@ -77,10 +75,8 @@ struct Decoder {
     for (auto* p : kc) (void)hipFree(p);
     for (auto* p : vc) (void)hipFree(p);
     free_prefill();
-    for (void* p : {(void*)sx, (void*)snorm, (void*)sqkv, (void*)sattn, (void*)sproj,
-                    (void*)sgateup, (void*)slastn, (void*)logits, (void*)snorm_bf16,
-                    (void*)sattn_bf16, (void*)sgate_bf16, (void*)slastn_bf16, (void*)spos,
-                    (void*)stok, (void*)scount, (void*)sout})
+    for (void* p : {(void*)sx, (void*)sqkv, (void*)sattn, (void*)sgateup, (void*)logits,
+                    argmax_scratch, (void*)spos, (void*)stok, (void*)scount, (void*)sout})
       if (p) (void)hipFree(p);
     if (host_int) (void)hipHostFree(host_int);
   }
@@ -108,13 +104,13 @@ struct Decoder {
     }
     const int H = c.hidden_size, I = c.intermediate_size;
     int rc = 0;
-    if ((rc = dalloc(&sx, H)) || (rc = dalloc(&snorm, H)) || (rc = dalloc(&sqkv, Qd() + 2 * KVd())) ||
-        (rc = dalloc(&sattn, Qd())) || (rc = dalloc(&sproj, H)) || (rc = dalloc(&sgateup, 2 * I)) ||
-        (rc = dalloc(&slastn, H)) || (rc = dalloc(&logits, c.vocab_size)) ||
-        (rc = dalloc(&snorm_bf16, H)) || (rc = dalloc(&sattn_bf16, Qd())) ||
-        (rc = dalloc(&sgate_bf16, I)) || (rc = dalloc(&slastn_bf16, H)) || (rc = dalloc(&spos, 1)) ||
+    if ((rc = dalloc(&sx, H)) || (rc = dalloc(&sqkv, Qd() + 2 * KVd())) ||
+        (rc = dalloc(&sattn, Qd())) || (rc = dalloc(&sgateup, 2 * I)) ||
+        (rc = dalloc(&logits, c.vocab_size)) || (rc = dalloc(&spos, 1)) ||
         (rc = dalloc(&stok, 1)) || (rc = dalloc(&scount, 1)))
       return rc;
+    if (const size_t n = argmax_scratch_bytes(c.vocab_size))
+      if ((rc = dalloc(reinterpret_cast<char**>(&argmax_scratch), n))) return rc;
     if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&host_int), 4 * sizeof(int)),
                         "decoder pinned scalars")))
       return rc;
@@ -179,12 +175,14 @@ struct Decoder {
     if (rc) return rc;
     cache_len = pos0 + T;
     const float* last = x + static_cast<size_t>(T - 1) * H;
-    (rc = orator_rms_norm(last, final_norm, slastn, 1, H, eps, s)) ||
-        (rc = orator_linear(slastn, lm_head, nullptr, logits, 1, H, c.vocab_size, 0, s));
-    return rc;
+    return launch_gemv_fused(kGemvInRmsNorm, last, final_norm, eps, lm_head, logits, H,
+                             c.vocab_size, false, s);
   }
 
   // One-token forward of sx at the device position spos (asr_text_decoder.cu:360-455).
+  // Each projection is one fused GEMV that builds its bf16 input row from the fp32 producer
+  // (RmsNorm -> cast, cast, SwiGLU -> cast) and the o / down projections add into the
+  // residual stream in their store: per layer 6 launches instead of the reference's 16.
   int decode_forward(hipStream_t s) {
     const int H = c.hidden_size, I = c.intermediate_size, Hq = c.num_q_heads,
               Hkv = c.num_kv_heads, Dh = c.head_dim;
@@ -195,31 +193,26 @@ struct Decoder {
     int rc = 0;
     for (int li = 0; li < c.num_layers && !rc; ++li) {
       const OratorDecoderLayer& L = layers[li];
-      (rc = orator_rms_norm(sx, L.in_ln, snorm, 1, H, eps, s)) ||
-          (rc = orator_f32_to_bf16(snorm, snorm_bf16, H, s)) ||
-          (rc = orator_linear_pre(snorm_bf16, L.qkv_w, nullptr, sqkv, 1, H, Qd() + 2 * KVd(), 0,
-                                  s)) ||
+      (rc = launch_gemv_fused(kGemvInRmsNorm, sx, L.in_ln, eps, L.qkv_w, sqkv, H,
+                              Qd() + 2 * KVd(), false, s)) ||
           (rc = orator_qk_norm_rope_kv_write(dq, dk, dv, 0, 0, L.q_norm, L.k_norm, eps, spos,
                                              c.rope_theta, 1, 1, Hq, Hkv, Dh, kc[li], vc[li],
                                              nullptr, 0, 0, c.max_seq_len, s)) ||
           (rc = orator_gqa_decode(dq, kc[li], vc[li], sattn, Hq, Hkv, Dh, spos, c.max_seq_len,
                                   scale(), s)) ||
-          (rc = orator_f32_to_bf16(sattn, sattn_bf16, Qd(), s)) ||
-          (rc = orator_linear_pre(sattn_bf16, L.o_w, nullptr, sproj, 1, Qd(), H, 0, s)) ||
-          (rc = orator_add_residual(sx, sproj, H, s)) ||
-          (rc = orator_rms_norm(sx, L.post_ln, snorm, 1, H, eps, s)) ||
-          (rc = orator_f32_to_bf16(snorm, snorm_bf16, H, s)) ||
-          (rc = orator_linear_pre(snorm_bf16, L.gateup_w, nullptr, sgateup, 1, H, 2 * I, 0, s)) ||
-          (rc = orator_swiglu(sgateup, sgateup + I, sgateup, I, s)) ||
-          (rc = orator_f32_to_bf16(sgateup, sgate_bf16, I, s)) ||
-          (rc = orator_linear_pre(sgate_bf16, L.down_w, nullptr, sproj, 1, I, H, 0, s)) ||
-          (rc = orator_add_residual(sx, sproj, H, s));
+          (rc = launch_gemv_fused(kGemvInF32, sattn, nullptr, 0.0f, L.o_w, sx, Qd(), H, true, s)) ||
+          (rc = launch_gemv_fused(kGemvInRmsNorm, sx, L.post_ln, eps, L.gateup_w, sgateup, H,
+                                  2 * I, false, s)) ||
+          (rc = launch_gemv_fused(kGemvInSwiglu, sgateup, sgateup + I, 0.0f, L.down_w, sx, I, H,
+                                  true, s));
     }
     if (rc) return rc;
-    (rc = orator_rms_norm(sx, final_norm, slastn, 1, H, eps, s)) ||
-        (rc = orator_f32_to_bf16(slastn, slastn_bf16, H, s)) ||
-        (rc = orator_linear_pre(slastn_bf16, lm_head, nullptr, logits, 1, H, c.vocab_size, 0, s));
-    return rc;
+    return launch_gemv_fused(kGemvInRmsNorm, sx, final_norm, eps, lm_head, logits, H,
+                             c.vocab_size, false, s);
+  }
+
+  int argmax(int ban0, int ban1, int* d_out, hipStream_t s) {
+    return launch_argmax_banned(logits, c.vocab_size, ban0, ban1, d_out, argmax_scratch, s);
   }
 
   // Greedy step body (asr_text_decoder.cu:677-691): record, gather, forward, argmax, pos + 1.
@@ -228,7 +221,7 @@ struct Decoder {
     (rc = orator_record_token(sout, scount, stok, sout_cap, s)) ||
         (rc = orator_embed_gather(embed, stok, sx, c.hidden_size, s)) ||
         (rc = decode_forward(s)) ||
-        (rc = orator_argmax_banned(logits, c.vocab_size, ban0, ban1, stok, s)) ||
+        (rc = argmax(ban0, ban1, stok, s)) ||
         (rc = orator_inc_pos(spos, s));
     return rc;
   }
@@ -312,8 +305,7 @@ struct Decoder {
     };
     // seed: argmax of the prefill logits -> the first token
     const bool seed_ban = 0 < ban_steps;
-    if ((rc = orator_argmax_banned(logits, c.vocab_size, seed_ban ? eos0 : -1,
-                                   seed_ban ? eos1 : -1, stok, s)) ||
+    if ((rc = argmax(seed_ban ? eos0 : -1, seed_ban ? eos1 : -1, stok, s)) ||
         (rc = check_hip(hipStreamSynchronize(s), "decoder sync")))
       return rc;
     int emitted = 0;
@@ -393,10 +385,12 @@ int orator_decoder_create(const OratorDecoderConfig* cfg, const uint16_t* embed,
   if (c.num_layers <= 0 || c.hidden_size <= 0 || c.num_q_heads <= 0 || c.num_kv_heads <= 0 ||
       c.intermediate_size <= 0 || c.vocab_size <= 0 || c.max_seq_len <= 0)
     return fail(ORATOR_ERR_INVALID, "decoder_create: sizes must be positive");
-  if (c.head_dim != 128 || c.num_q_heads % c.num_kv_heads ||
-      c.hidden_size % 8 || c.intermediate_size % 8)
+  if (c.head_dim != 128 || c.num_q_heads % c.num_kv_heads || c.hidden_size % 8 ||
+      c.intermediate_size % 8 || c.hidden_size > kFusedMaxK || c.intermediate_size > kFusedMaxK ||
+      c.num_q_heads * c.head_dim > kFusedMaxK)
     return fail(ORATOR_ERR_UNSUPPORTED,
-                "decoder_create: head_dim 128, Hq multiple of Hkv, hidden and intermediate % 8");
+                "decoder_create: head_dim 128, Hq multiple of Hkv, hidden and intermediate % 8, "
+                "hidden, Hq * head_dim and intermediate <= 8192");
   for (int l = 0; l < c.num_layers; ++l) {
     const OratorDecoderLayer& L = layers[l];
     if (!L.in_ln || !L.q_norm || !L.k_norm || !L.post_ln || !L.qkv_w || !L.o_w || !L.gateup_w ||
@@ -469,8 +463,7 @@ int orator_decoder_decode_step_device(void* handle, const int* d_token, int pos,
 int orator_decoder_argmax_to_device(void* handle, int* d_out, int ban0, int ban1, void* stream) {
   Decoder* d = as_dec(handle);
   if (!d || !d_out) return fail(ORATOR_ERR_INVALID, "decoder_argmax_to_device: null pointer");
-  return orator_argmax_banned(d->logits, d->c.vocab_size, ban0, ban1, d_out,
-                              static_cast<hipStream_t>(stream));
+  return d->argmax(ban0, ban1, d_out, static_cast<hipStream_t>(stream));
 }
 
 int orator_decoder_embed(void* handle, int token_id, float* out) {
@@ -502,7 +495,7 @@ int orator_decoder_argmax(void* handle, int ban0, int ban1, int* token, void* st
   Decoder* d = as_dec(handle);
   if (!d || !token) return fail(ORATOR_ERR_INVALID, "decoder_argmax: null pointer");
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc = orator_argmax_banned(d->logits, d->c.vocab_size, ban0, ban1, d->stok, s);
+  int rc = d->argmax(ban0, ban1, d->stok, s);
   if (!rc) rc = check_hip(hipMemcpyAsync(d->host_int, d->stok, sizeof(int), hipMemcpyDeviceToHost, s),
                           "decoder argmax copy");
   if (!rc) rc = check_hip(hipStreamSynchronize(s), "decoder sync");

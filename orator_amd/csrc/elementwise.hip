@@ -161,6 +161,65 @@ __global__ __launch_bounds__(256) void argmax_banned_kernel(const float* __restr
   if (threadIdx.x == 0) *out_idx = sidx[0];
 }
 
+// Two-stage form for long rows (the vocabulary).  The single-block kernel above fixes the
+// tie rule: thread t keeps the first maximum of its strided subsequence i = t (mod 256),
+// then the tree above picks among the 256 thread candidates.  Stage 1 splits every thread's
+// subsequence into row ranges (row r = elements [256 r, 256 r + 256)), one range per
+// workgroup, and keeps each range's first maximum per thread; stage 2 folds the ranges in
+// order per thread (strict >, so the first maximum survives) and runs the same tree.  The
+// result is the single-block kernel's on every input.
+constexpr int kArgmaxRows = 8;  // rows of 256 elements per stage-1 workgroup
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ x, int n,
+                                                             int ban0, int ban1,
+                                                             float* __restrict__ pval,
+                                                             int* __restrict__ pidx) {
+  const int t = threadIdx.x;
+  float best = -1e30f;
+  int bi = 0;
+  const int r0 = blockIdx.x * kArgmaxRows;
+#pragma unroll
+  for (int r = 0; r < kArgmaxRows; ++r) {
+    const int i = (r0 + r) * 256 + t;
+    if (i < n && i != ban0 && i != ban1) {
+      const float v = x[i];
+      if (v > best) {
+        best = v;
+        bi = i;
+      }
+    }
+  }
+  pval[blockIdx.x * 256 + t] = best;
+  pidx[blockIdx.x * 256 + t] = bi;
+}
+
+__global__ __launch_bounds__(256) void argmax_finish_kernel(const float* __restrict__ pval,
+                                                            const int* __restrict__ pidx,
+                                                            int parts, int* __restrict__ out_idx) {
+  __shared__ float sval[256];
+  __shared__ int sidx[256];
+  float best = -1e30f;
+  int bi = 0;
+  for (int g = 0; g < parts; ++g) {
+    const float v = pval[g * 256 + threadIdx.x];
+    if (v > best) {
+      best = v;
+      bi = pidx[g * 256 + threadIdx.x];
+    }
+  }
+  sval[threadIdx.x] = best;
+  sidx[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s && sval[threadIdx.x + s] > sval[threadIdx.x]) {
+      sval[threadIdx.x] = sval[threadIdx.x + s];
+      sidx[threadIdx.x] = sidx[threadIdx.x + s];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out_idx = sidx[0];
+}
+
 // ----------------------------------------------------------------- KV write ----
 // One lane per 4 elements of one (t, h) row; both K and V rows are converted in the
 // same lane.  Rows at or past the capacity (or with an out-of-range page) are dropped.
@@ -280,6 +339,34 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 }  // namespace
 }  // namespace orator_hip
 
+namespace orator_hip {
+
+size_t argmax_scratch_bytes(int n) {
+  const int rows = (n + 255) / 256;
+  const int parts = (rows + kArgmaxRows - 1) / kArgmaxRows;
+  return parts > 1 ? static_cast<size_t>(parts) * 256 * (sizeof(float) + sizeof(int)) : 0;
+}
+
+int launch_argmax_banned(const float* logits, int n, int ban0, int ban1, int* out_idx,
+                         void* scratch, hipStream_t s) {
+  const int rows = (n + 255) / 256;
+  const int parts = (rows + kArgmaxRows - 1) / kArgmaxRows;
+  if (parts <= 1) {
+    hipLaunchKernelGGL(argmax_banned_kernel, dim3(1), dim3(256), 0, s, logits, n, ban0, ban1,
+                       out_idx);
+    return check_launch("argmax_banned");
+  }
+  if (!scratch) return fail(ORATOR_ERR_INVALID, "argmax_banned: scratch needed");
+  float* pval = static_cast<float*>(scratch);
+  int* pidx = reinterpret_cast<int*>(pval + static_cast<size_t>(parts) * 256);
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(parts), dim3(256), 0, s, logits, n, ban0, ban1,
+                     pval, pidx);
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, s, pval, pidx, parts, out_idx);
+  return check_launch("argmax_banned");
+}
+
+}  // namespace orator_hip
+
 using namespace orator_hip;
 
 extern "C" {
@@ -354,9 +441,13 @@ int orator_argmax_banned(const float* logits, int n, int ban0, int ban1, int* ou
                          void* stream) {
   if (n <= 0) return ORATOR_OK;
   if (!logits || !out_idx) return fail(ORATOR_ERR_INVALID, "argmax_banned: null pointer");
-  hipLaunchKernelGGL(argmax_banned_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     logits, n, ban0, ban1, out_idx);
-  return check_launch("argmax_banned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* scratch = nullptr;
+  if (argmax_scratch_bytes(n)) {
+    scratch = workspace(s, argmax_scratch_bytes(n), 0);
+    if (!scratch) return ORATOR_ERR_HIP;
+  }
+  return launch_argmax_banned(logits, n, ban0, ban1, out_idx, scratch, s);
 }
 
 int orator_kv_write(const float* k, const float* v, uint16_t* kc, uint16_t* vc, int Tq, int Hkv,

@@ -33,6 +33,19 @@ inline int ilog2_exact(int v) {
   return s;
 }
 
+// Decode-step GEMV over an fp32 producer (linear.hip): mode selects how the bf16 input row is
+// built (cast, RMSNorm with gain `aux`, SwiGLU with up = `aux`); accumulate adds into out.
+enum { kGemvInF32 = 1, kGemvInRmsNorm = 2, kGemvInSwiglu = 3 };
+constexpr int kFusedMaxK = 8192;
+int launch_gemv_fused(int mode, const float* x, const float* aux, float eps, const uint16_t* W,
+                      float* out, int K, int N, bool accumulate, hipStream_t s);
+
+// ArgmaxBanned with caller-provided scratch of argmax_scratch_bytes(n) bytes (0: none
+// needed, one workgroup does it).
+size_t argmax_scratch_bytes(int n);
+int launch_argmax_banned(const float* logits, int n, int ban0, int ban1, int* out_idx,
+                         void* scratch, hipStream_t s);
+
 // Compute units of the current device (cached per device); 0 if it cannot be queried.
 int device_cu_count();
 

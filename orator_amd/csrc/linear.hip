@@ -89,6 +89,145 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_bf16_kernel(
   }
 }
 
+// ------------------------------------------------------ fused decode-step GEMV ----
+// out[n] (=, or += with ACC) sum_k xb[k] W[n,k] for one input row, where the bf16 row xb is
+// built in LDS by the workgroup from the fp32 producer of the decode step:
+//   kGemvInF32      xb = bf16(x)                                 (F32ToBf16 + LinearPre)
+//   kGemvInRmsNorm  xb = bf16(x * rsqrt(mean(x^2) + eps) * w)     (RmsNorm + F32ToBf16)
+//   kGemvInSwiglu   xb = bf16(silu(g) * u), g = x, u = aux        (SwiGLU + F32ToBf16)
+// so one launch replaces three of asr_text_decoder.cu:398-429; ACC folds the residual add
+// (AddResidualKernel) into the store.  The per-element arithmetic is the standalone
+// kernels'; only the order of the RMSNorm sum of squares differs.  The first batch of weight
+// loads is issued before the row is built so the prologue hides under the HBM latency; the
+// k loop then ping-pongs two register batches of kFusedU 16-byte chunks per row.
+constexpr int kFusedU = 4;
+
+template <int MODE, int R, bool ACC>
+__global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict__ x,
+                                                         const float* __restrict__ aux, float eps,
+                                                         const uint16_t* __restrict__ W,
+                                                         float* __restrict__ out, int K, int N) {
+#pragma clang fp contract(off)
+  __shared__ __align__(16) uint16_t xs[kFusedMaxK];
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  const int nchunk = K >> 3;
+  const u32x4_t* wr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    wr[r] = reinterpret_cast<const u32x4_t*>(W + static_cast<long>(min(row0 + r, N - 1)) * K);
+  u32x4_t A[kFusedU][R], Bb[kFusedU][R];
+  auto load = [&](u32x4_t(&dst)[kFusedU][R], int base) {
+#pragma unroll
+    for (int u = 0; u < kFusedU; ++u) {
+      const int c = base + 64 * u + lane;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        dst[u][r] = c < nchunk ? __builtin_nontemporal_load(wr[r] + c) : u32x4_t{0, 0, 0, 0};
+    }
+  };
+  load(A, 0);
+
+  // ---- the bf16 input row, in LDS ----
+  if constexpr (MODE == kGemvInRmsNorm) {
+    float local = 0.0f;
+    for (int d = 4 * tid; d < K; d += 1024) {
+      const float4 v = *reinterpret_cast<const float4*>(x + d);
+      local += v.x * v.x;
+      local += v.y * v.y;
+      local += v.z * v.z;
+      local += v.w * v.w;
+    }
+    const float ws = wave_sum(local);
+    if (lane == 0) red[wave] = ws;
+    lds_barrier();
+    const float sum = (red[0] + red[1]) + (red[2] + red[3]);
+    const float ms = sum / static_cast<float>(K) + eps;
+    const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+    for (int d = 4 * tid; d < K; d += 1024) {
+      const float4 v = *reinterpret_cast<const float4*>(x + d);
+      const float4 g = *reinterpret_cast<const float4*>(aux + d);
+      *reinterpret_cast<uint2*>(xs + d) =
+          make_uint2(pack_bf16x2(v.x * inv * g.x, v.y * inv * g.y),
+                     pack_bf16x2(v.z * inv * g.z, v.w * inv * g.w));
+    }
+  } else {
+    for (int d = 4 * tid; d < K; d += 1024) {
+      const float4 v = *reinterpret_cast<const float4*>(x + d);
+      if constexpr (MODE == kGemvInSwiglu) {
+        const float4 u = *reinterpret_cast<const float4*>(aux + d);
+        *reinterpret_cast<uint2*>(xs + d) =
+            make_uint2(pack_bf16x2((v.x / (1.0f + expf(-v.x))) * u.x,
+                                   (v.y / (1.0f + expf(-v.y))) * u.y),
+                       pack_bf16x2((v.z / (1.0f + expf(-v.z))) * u.z,
+                                   (v.w / (1.0f + expf(-v.w))) * u.w));
+      } else {
+        *reinterpret_cast<uint2*>(xs + d) =
+            make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+      }
+    }
+  }
+  lds_barrier();
+
+  float acc[R] = {};
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(xs);
+  auto comp = [&](const u32x4_t(&src)[kFusedU][R], int base) {
+#pragma unroll
+    for (int u = 0; u < kFusedU; ++u) {
+      const int c = base + 64 * u + lane;
+      if (c < nchunk) {
+        const u32x4_t xx = xv[c];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] += dot8(src[u][r], xx);
+      }
+    }
+  };
+  constexpr int kStep = 64 * kFusedU;
+  int base = 0;
+  while (true) {
+    if (base + kStep < nchunk) load(Bb, base + kStep);
+    comp(A, base);
+    base += kStep;
+    if (base >= nchunk) break;
+    if (base + kStep < nchunk) load(A, base + kStep);
+    comp(Bb, base);
+    base += kStep;
+    if (base >= nchunk) break;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane < R && row0 + lane < N) {
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r)
+      if (lane == r) v = acc[r];
+    float* o = out + row0 + lane;
+    if constexpr (ACC) v = *o + v;
+    *o = v;
+  }
+}
+
+template <int MODE, bool ACC>
+int launch_fused_mode(const float* x, const float* aux, float eps, const uint16_t* W, float* out,
+                      int K, int N, hipStream_t s) {
+  // rows per wave: enough waves to cover the chip for small N, fewer input-row rebuilds
+  // (one per workgroup) for the vocabulary-sized projection
+  if (N >= 32768) {
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 4, ACC>), dim3((N + 15) / 16), dim3(256), 0, s, x,
+                       aux, eps, W, out, K, N);
+  } else if (N >= 8192) {
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC>), dim3((N + 7) / 8), dim3(256), 0, s, x,
+                       aux, eps, W, out, K, N);
+  } else {
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 1, ACC>), dim3((N + 3) / 4), dim3(256), 0, s, x,
+                       aux, eps, W, out, K, N);
+  }
+  return check_launch("gemv_fused_kernel");
+}
+
 // ------------------------------------------------------------------- GEMM (M > 1) ----
 constexpr int kTM = 128, kTN = 128, kTK = 32;
 constexpr int kLRow = kTK + 8;  // padded LDS row (bf16): 80 bytes
@@ -195,6 +334,31 @@ int launch_bf16_gemm(const uint16_t* in, const uint16_t* W, const float* bias, f
   const dim3 grid((N + kTN - 1) / kTN, (M + kTM - 1) / kTM);
   hipLaunchKernelGGL(gemm_bf16_kernel, grid, dim3(256), 0, stream, in, W, bias, out, M, K, N, act);
   return check_launch("gemm_bf16_kernel");
+}
+
+int launch_gemv_fused(int mode, const float* x, const float* aux, float eps, const uint16_t* W,
+                      float* out, int K, int N, bool accumulate, hipStream_t s) {
+  if (K <= 0 || N <= 0) return ORATOR_OK;
+  if (!x || !W || !out || (mode != kGemvInF32 && !aux))
+    return fail(ORATOR_ERR_INVALID, "gemv_fused: null pointer");
+  if (K % 8 || K > kFusedMaxK)
+    return fail(ORATOR_ERR_UNSUPPORTED, "gemv_fused: K must be a multiple of 8, at most 8192");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W) |
+       reinterpret_cast<uintptr_t>(aux)) & 15u)
+    return fail(ORATOR_ERR_INVALID, "gemv_fused: x, aux and W must be 16-byte aligned");
+  switch (mode) {
+    case kGemvInF32:
+      return accumulate ? launch_fused_mode<kGemvInF32, true>(x, aux, eps, W, out, K, N, s)
+                        : launch_fused_mode<kGemvInF32, false>(x, aux, eps, W, out, K, N, s);
+    case kGemvInRmsNorm:
+      return accumulate ? launch_fused_mode<kGemvInRmsNorm, true>(x, aux, eps, W, out, K, N, s)
+                        : launch_fused_mode<kGemvInRmsNorm, false>(x, aux, eps, W, out, K, N, s);
+    case kGemvInSwiglu:
+      return accumulate ? launch_fused_mode<kGemvInSwiglu, true>(x, aux, eps, W, out, K, N, s)
+                        : launch_fused_mode<kGemvInSwiglu, false>(x, aux, eps, W, out, K, N, s);
+    default:
+      return fail(ORATOR_ERR_INVALID, "gemv_fused: unknown input mode");
+  }
 }
 
 int launch_linear_pre(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,

@@ -100,6 +100,23 @@ def test_argmax_banned_random_and_ties():
         assert _argmax_gpu(y) == orc.argmax_banned(y), idx
 
 
+@pytest.mark.parametrize("n", [2049, 4096, 151936])
+def test_argmax_two_stage_keeps_the_tie_rule(n):
+    """Rows longer than 2048 run the two-stage kernels: planted ties inside one slot across
+    stage-1 ranges, across slots in different ranges, bans and an all -inf row give the
+    single-pass rule's answers."""
+    cases = [[2, 2 + 256 * 7, 2 + 256 * 8], [1, 2 + 256 * 9], [3 + 256 * 8, 1], [130 + 2048, 2],
+             [5, 5 + 256 * 7, 99, 99 + 256 * 8], [n - 1, (n - 1) % 256]]
+    for idx in cases:
+        y = np.zeros(n, np.float32)
+        y[[i for i in idx if i < n]] = 5.0
+        assert _argmax_gpu(y) == orc.argmax_banned(y), (n, idx)
+        assert _argmax_gpu(y, idx[0], idx[1]) == orc.argmax_banned(y, idx[0], idx[1]), (n, idx)
+    assert _argmax_gpu(np.full(n, -np.inf, np.float32)) == 0
+    x = SplitMix64(n).normal((n,))
+    assert _argmax_gpu(x, 7, 9) == orc.argmax_banned(x, 7, 9)
+
+
 def test_gqa_attention_fixture(golden):
     """The reference's own GQA check: T=24, 16/8 heads, causal, max-abs 5e-4 against torch
     SDPA (test/unit/model/test_asr_ops.cc:145-169)."""
