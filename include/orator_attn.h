@@ -154,6 +154,15 @@ int orator_gqa_decode_append_paged(const float* q, const float* k_new, const flo
                                    float* out, int B, int Hq, int Hkv, int Dh, float scale,
                                    void* stream);
 
+/* WindowAttnKernel (src/model/asr_audio_tower.cu:204-258, launch :573-575): the audio tower's
+ * self-attention, q/k/v fp32 [N, H, Dh] with Dh in {64, 128}; query i attends keys
+ * [seg_start[i], seg_end[i]) (device int arrays, clamped into [0, N)); online softmax, zeros
+ * for an empty window.  The kernel has no reference launcher: the parameters mirror its
+ * arguments. */
+int orator_window_attention(const float* q, const float* k, const float* v, float* out,
+                            const int* d_seg_start, const int* d_seg_end, int N, int H, int Dh,
+                            float scale, void* stream);
+
 /* ----------------------------------------------------- bf16-weight linear ---- */
 /* asr_gemm::LinearPre (include/model/asr_gemm.h:33-38, src/model/asr_gemm.cu:175-208):
  * out[M,N] fp32 = act(in[M,K] W[N,K]^T + bias), in and W bf16, fp32 accumulation; act 0 none,

@@ -28,6 +28,9 @@
  *   orc_argmax_banned       numpy argmax with bans; the reference tie rule on planted ties
  *   orc_linear_bf16         fp64 numpy matmul of the bf16-decoded operands; GELU against
  *                           math.erf; ReLU; bias
+ *   orc_window_attention    full windows == orc_gqa_attention non-causal (torch SDPA pinned);
+ *                           block-diagonal windows == per-segment SDPA; empty window -> 0;
+ *                           fp64 softmax brute force
  */
 #include "orator_oracle.h"
 
@@ -617,6 +620,39 @@ void orc_sgemm_batched(const float* in, const float* W, float* out, int M, int K
                        int batch, long stride_in, long stride_w, long stride_out) {
   for (int b = 0; b < batch; ++b)
     orc_sgemm(in + b * stride_in, W + b * stride_w, NULL, out + b * stride_out, M, K, N, act);
+}
+
+/* WindowAttnKernel (src/model/asr_audio_tower.cu:204-258): per (query i, head h) an online
+ * softmax over keys j in [seg_start[i], seg_end[i]): m starts at -1e30, score = (q.k) * scale
+ * with the dot in dimension order, corr = exp(m - nm), p = exp(score - nm), l = l corr + p,
+ * acc = acc corr + p v; out = acc / l, or 0 when l == 0. */
+void orc_window_attention(const float* q, const float* k, const float* v, float* out,
+                          const int* seg_start, const int* seg_end, int N, int H, int Dh,
+                          float scale) {
+  float* acc = (float*)malloc(sizeof(float) * (size_t)Dh);
+  for (int i = 0; i < N; ++i)
+    for (int h = 0; h < H; ++h) {
+      const float* qr = q + ((size_t)i * H + h) * Dh;
+      float m = -1e30f, l = 0.0f;
+      for (int d = 0; d < Dh; ++d) acc[d] = 0.0f;
+      for (int j = seg_start[i]; j < seg_end[i]; ++j) {
+        const float* kr = k + ((size_t)j * H + h) * Dh;
+        const float* vr = v + ((size_t)j * H + h) * Dh;
+        float dot = 0.0f;
+        for (int d = 0; d < Dh; ++d) dot += qr[d] * kr[d];
+        const float score = dot * scale;
+        const float nm = score > m ? score : m;
+        const float corr = expf(m - nm);
+        const float p = expf(score - nm);
+        l = l * corr + p;
+        for (int d = 0; d < Dh; ++d) acc[d] = acc[d] * corr + p * vr[d];
+        m = nm;
+      }
+      const float invl = l > 0.0f ? 1.0f / l : 0.0f;
+      float* o = out + ((size_t)i * H + h) * Dh;
+      for (int d = 0; d < Dh; ++d) o[d] = acc[d] * invl;
+    }
+  free(acc);
 }
 
 /* asr_gemm::LinearPre (src/model/asr_gemm.cu:175-208; kernels :62-155): out[m,n] =

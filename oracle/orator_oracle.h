@@ -107,6 +107,11 @@ void orc_sgemm(const float* in, const float* W, const float* bias, float* out, i
 void orc_sgemm_batched(const float* in, const float* W, float* out, int M, int K, int N, int act,
                        int batch, long stride_in, long stride_w, long stride_out);
 
+/* ---- WindowAttnKernel (src/model/asr_audio_tower.cu:204-258) ---- */
+void orc_window_attention(const float* q, const float* k, const float* v, float* out,
+                          const int* seg_start, const int* seg_end, int N, int H, int Dh,
+                          float scale);
+
 /* ---- asr_gemm::LinearPre (src/model/asr_gemm.cu:175-208): bf16 in/W, fp32 accumulate ---- */
 void orc_linear_bf16(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
                      int K, int N, int act);

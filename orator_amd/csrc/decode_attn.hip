@@ -40,7 +40,10 @@ struct DecodeArgs {
   const void* vpool;
   const int* page_table;
   const int* pos;      // [B]: stream b attends pos[b]+1 keys (pos_mode 0)
-  int pos_mode;        // 0: pos[b]+1 keys; 1: b+1 keys (causal self-attn); 2: capacity keys
+  int pos_mode;        // 0: pos[b]+1 keys; 1: b+1 keys (causal self-attn); 2: capacity keys;
+                       // 3: keys [seg_start[b], seg_end[b]) (windowed self-attention)
+  const int* seg_start;
+  const int* seg_end;
   float* out;
   float* part_o;       // [B*Hq][max_splits][DH]
   float* part_ml;      // [B*Hq][max_splits][2]
@@ -60,8 +63,17 @@ struct DecodeArgs {
 
 // Number of keys stream b attends, clamped to the capacity.
 __device__ __forceinline__ int stream_keys(const DecodeArgs& a, int b) {
+  if (a.pos_mode == 3) {  // window [seg_start, seg_end) clamped into [0, capacity)
+    const int j0 = min(max(a.seg_start[b], 0), a.capacity);
+    return min(max(a.seg_end[b], j0), a.capacity) - j0;
+  }
   const int S = a.pos_mode == 0 ? a.pos[b] + 1 : (a.pos_mode == 1 ? b + 1 : a.capacity);
   return S > a.capacity ? a.capacity : S;
+}
+
+// First key row of stream b's range (non-zero only for windows).
+__device__ __forceinline__ int stream_key0(const DecodeArgs& a, int b) {
+  return a.pos_mode == 3 ? min(max(a.seg_start[b], 0), a.capacity) : 0;
 }
 
 // Element helpers: K/V rows are bf16 (cache) or fp32 (self-attention over fp32 K/V).
@@ -297,7 +309,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   // ---- first pool row of every 16-key group of the split (pages hold >= 16 aligned keys) ----
   if (tid < NG) {
     const int j0 = t0 + 16 * tid;
-    int row = j0;
+    int row = j0 + stream_key0(a, b);
     if (a.page_table && j0 < S) {
       const int page = a.page_table[static_cast<long>(b) * a.max_pages + (j0 >> a.page_shift)];
       row = (page << a.page_shift) | (j0 & ((1 << a.page_shift) - 1));
@@ -356,7 +368,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   }
   const int r = lane / CK::LPT;
 
-  if (w0 < w_end) {
+  if constexpr (TPW == CK::CH) {
+    // one chunk per wave (128-key splits): no second buffer
+    if (w0 < w_end) {
+      CK A;
+      load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, w0, t0, w_end, lane);
+      process_chunk<DH, G, KV>(A, qr, m, lpart, acc, w0, w_end, lane, a.scale_log2e);
+    }
+  } else if (w0 < w_end) {
     // Ping-pong buffers: the loads of one chunk are in flight while the other is computed.
     CK A, Bb;
     load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, w0, t0, w_end, lane);
@@ -544,15 +563,12 @@ int split_override() {
 
 }  // namespace
 
-// Split length: 256 keys (measured best for B = 16 at 4K keys: 128 makes the merge dominate,
-// 512+ leaves too few workgroups and lengthens the tail); 128 when the 256-key grid would not
-// give every CU a workgroup (a single stream: B = 1, 8 KV heads, ~2K keys -> 72 workgroups).
-int choose_split(int B, int Hkv, int G, int capacity) {
+// Split length: 128 keys (one 32-key chunk per wave, 117 VGPRs, 4 waves/SIMD), measured
+// ahead of 256 (2 waves/SIMD) on every configs[2] case: B = 16 at 1K/2K/4K keys by 4-5%, a
+// single stream by 6-23%.  G = 4 keeps 4 heads of state per lane and runs 256-key splits.
+int choose_split(int /*B*/, int /*Hkv*/, int G, int /*capacity*/) {
   if (split_override()) return split_override();
-  if (G == 4) return 256;
-  const long wgs = static_cast<long>(B) * Hkv * ((capacity + 255) / 256);
-  const int cus = device_cu_count();
-  return (cus > 0 && wgs < cus) ? 128 : 256;
+  return G == 4 ? 256 : 128;
 }
 
 size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity) {
@@ -564,9 +580,11 @@ size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity) {
 
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (p.B <= 0 || p.Hq <= 0 || p.Hkv <= 0 || p.Dh <= 0) return ORATOR_OK;  // reference no-op
-  if (!p.q || !p.kpool || !p.vpool || (!p.pos && p.pos_mode == 0) || !p.out)
+  if (!p.q || !p.kpool || !p.vpool || (!p.pos && p.pos_mode == 0) || !p.out ||
+      (p.pos_mode == 3 && (!p.seg_start || !p.seg_end)))
     return fail(ORATOR_ERR_INVALID, "gqa_decode: null pointer");
   if (p.Hq % p.Hkv) return fail(ORATOR_ERR_INVALID, "gqa_decode: Hq must be a multiple of Hkv");
+  if (p.B > 65535) return fail(ORATOR_ERR_UNSUPPORTED, "gqa_decode: at most 65535 streams / rows");
   const int G = p.Hq / p.Hkv;
   if (!(p.Dh == 64 || p.Dh == 128) || !(G == 1 || G == 2 || G == 4))
     return fail(ORATOR_ERR_UNSUPPORTED, "gqa_decode: supported Dh {64,128}, Hq/Hkv {1,2,4}");
@@ -595,6 +613,8 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
 
   DecodeArgs args;
   args.pos_mode = p.pos_mode;
+  args.seg_start = p.seg_start;
+  args.seg_end = p.seg_end;
   args.q = p.q;
   args.kpool = p.kpool;
   args.vpool = p.vpool;
@@ -739,6 +759,30 @@ int orator_gqa_attention(const float* q, const float* k, const float* v, float* 
   p.capacity = T;
   p.scale = scale;
   return launch_gqa_decode(p, nullptr);
+}
+
+// WindowAttnKernel (src/model/asr_audio_tower.cu:204-258): audio-tower self-attention, q/k/v
+// fp32 [N, H, Dh], query i attends keys [seg_start[i], seg_end[i]) (device arrays), online
+// softmax, 0 for an empty window.  Ranges are clamped into [0, N).
+int orator_window_attention(const float* q, const float* k, const float* v, float* out,
+                            const int* d_seg_start, const int* d_seg_end, int N, int H, int Dh,
+                            float scale, void* stream) {
+  DecodeProblem p{};
+  p.q = q;
+  p.kpool = k;
+  p.vpool = v;
+  p.kv_f32 = true;
+  p.pos_mode = 3;
+  p.seg_start = d_seg_start;
+  p.seg_end = d_seg_end;
+  p.out = out;
+  p.B = N;
+  p.Hq = H;
+  p.Hkv = H;
+  p.Dh = Dh;
+  p.capacity = N;
+  p.scale = scale;
+  return launch_gqa_decode(p, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -59,7 +59,10 @@ struct DecodeProblem {
   const void* kpool;      // bf16 bits, or fp32 when kv_f32
   const void* vpool;
   bool kv_f32;
-  int pos_mode;           // 0: stream b attends pos[b]+1 keys; 1: b+1 keys; 2: capacity keys
+  int pos_mode;           // 0: stream b attends pos[b]+1 keys; 1: b+1 keys; 2: capacity keys;
+                          // 3: keys [seg_start[b], seg_end[b]) (windowed self-attention)
+  const int* seg_start;   // pos_mode 3
+  const int* seg_end;
   const int* page_table;  // nullptr => contiguous caches
   int max_pages;          // page-table row length (paged)
   int page_size;          // paged only (power of two >= 16)

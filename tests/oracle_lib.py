@@ -59,6 +59,7 @@ def lib() -> C.CDLL:
             "orc_sgemm_batched": ([_F, _F, _F, i, i, i, i, i, l, l, l], None),
             "orc_argmax_banned": ([_F, i, i, i], i),
             "orc_linear_bf16": ([_U16, _U16, _F, _F, i, i, i, i], None),
+            "orc_window_attention": ([_F, _F, _F, _F, _I, _I, i, i, i, f], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -274,6 +275,17 @@ def sgemm_batched(inp, W, act=0) -> np.ndarray:
     N = W.shape[1]
     out = np.empty((B, M, N), np.float32)
     lib().orc_sgemm_batched(_f(inp), _f(W), _f(out), M, K, N, act, B, M * K, N * K, M * N)
+    return out
+
+
+# ------------------------------------------------------- window attention ----
+def window_attention(q, k, v, seg_start, seg_end, scale) -> np.ndarray:
+    q, k, v = f32c(q), f32c(k), f32c(v)
+    N, H, Dh = q.shape
+    ss = np.ascontiguousarray(seg_start, dtype=np.int32)
+    se = np.ascontiguousarray(seg_end, dtype=np.int32)
+    out = np.empty_like(q)
+    lib().orc_window_attention(_f(q), _f(k), _f(v), _f(out), _i(ss), _i(se), N, H, Dh, scale)
     return out
 
 

@@ -565,3 +565,42 @@ def test_decoder_zero_layers_is_embedding_head():
     n = last / np.sqrt(np.mean(last * last) + cfg["rms_norm_eps"]) * d.final_norm
     want = orc.from_bf16(d.lm_head).astype(np.float64) @ orc.from_bf16(orc.to_bf16(n))
     assert np.max(np.abs(d.logits - want)) < 1e-4 * np.max(np.abs(want))
+
+
+# ------------------------------------------------------------- window attention ----
+
+
+def _windows(N, width):
+    """Consecutive windows of `width` (the last one ragged), as the audio tower's
+    cu_seqlens segments (src/model/asr_audio_tower.cu:509-533)."""
+    ss, se = np.zeros(N, np.int32), np.zeros(N, np.int32)
+    for s0 in range(0, N, width):
+        ss[s0:s0 + width], se[s0:s0 + width] = s0, min(N, s0 + width)
+    return ss, se
+
+
+def test_window_attention_full_is_noncausal_gqa_and_fp64():
+    r = SplitMix64(61)
+    N, H, Dh = 45, 4, 64
+    q, k, v = r.normal((N, H, Dh)), r.normal((N, H, Dh)), r.normal((N, H, Dh))
+    ss, se = np.zeros(N, np.int32), np.full(N, N, np.int32)
+    got = orc.window_attention(q, k, v, ss, se, 0.125)
+    assert rel_err(got, orc.gqa_attention(q, k, v, 0.125, False), 0.05) < 1e-6
+    assert rel_err(got, orc.attention_f64(q, k, v, 0.125, False), 0.05) < 1e-5
+
+
+def test_window_attention_block_diagonal_and_empty():
+    """Windows of 13 (ragged last) equal attention within each segment; an empty window
+    (seg_start == seg_end) gives zeros."""
+    r = SplitMix64(62)
+    N, H, Dh = 40, 2, 64
+    q, k, v = r.normal((N, H, Dh)), r.normal((N, H, Dh)), r.normal((N, H, Dh))
+    ss, se = _windows(N, 13)
+    se[5] = ss[5]
+    got = orc.window_attention(q, k, v, ss, se, 0.2)
+    for s0 in range(0, N, 13):
+        s1 = min(N, s0 + 13)
+        want = orc.attention_f64(q[s0:s1], k[s0:s1], v[s0:s1], 0.2, False)
+        rows = [i for i in range(s0, s1) if i != 5]
+        assert rel_err(got[rows], want[[i - s0 for i in rows]], 0.05) < 1e-5
+    assert np.all(got[5] == 0)
