@@ -163,6 +163,15 @@ int orator_window_attention(const float* q, const float* k, const float* v, floa
                             const int* d_seg_start, const int* d_seg_end, int N, int H, int Dh,
                             float scale, void* stream);
 
+/* The Sortformer decoder's self-attention (src/model/sortformer_decoder.cu:280-298: head-major
+ * gathers, QK^T batched SGEMM, ScaleMaskScoresKernel :114-123, AttnSoftmaxKernel :126-160, PV
+ * batched SGEMM, scatter :163-174) in one launch: q/k/v/out fp32 [T, H, Dk], Dk in
+ * {24, 32, 64}; scores (q.k) * scale, keys >= valid_len scored -1e30, row softmax, out the
+ * context fed to the out projection.  The sequence has no reference launcher: the parameters
+ * mirror the decomposition's. */
+int orator_masked_mha(const float* q, const float* k, const float* v, float* out, int T, int H,
+                      int Dk, int valid_len, float scale, void* stream);
+
 /* ----------------------------------------------------- bf16-weight linear ---- */
 /* asr_gemm::LinearPre (include/model/asr_gemm.h:33-38, src/model/asr_gemm.cu:175-208):
  * out[M,N] fp32 = act(in[M,K] W[N,K]^T + bias), in and W bf16, fp32 accumulation; act 0 none,

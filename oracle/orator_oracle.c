@@ -28,6 +28,8 @@
  *   orc_argmax_banned       numpy argmax with bans; the reference tie rule on planted ties
  *   orc_linear_bf16         fp64 numpy matmul of the bf16-decoded operands; GELU against
  *                           math.erf; ReLU; bias
+ *   orc_masked_mha          torch SDPA with a key-padding mask; == orc_relpos_attention with
+ *                           u = v = 0 and P = 0; valid_len 0 -> mean of V
  *   orc_window_attention    full windows == orc_gqa_attention non-causal (torch SDPA pinned);
  *                           block-diagonal windows == per-segment SDPA; empty window -> 0;
  *                           fp64 softmax brute force
@@ -653,6 +655,42 @@ void orc_window_attention(const float* q, const float* k, const float* v, float*
       for (int d = 0; d < Dh; ++d) o[d] = acc[d] * invl;
     }
   free(acc);
+}
+
+/* Sortformer decoder MHA as the reference decomposes it (src/model/sortformer_decoder.cu:
+ * 280-298): raw[h,i,j] = sum_d q.k in d order (the batched SGEMM), s = j >= valid ? -1e30 :
+ * raw * scale (:114-123), row max, e = exp(s - max), sum in j order, p = e * (1 / sum)
+ * (:126-160), ctx[i,h,d] = sum_j p v in j order (the PV SGEMM).  The reference's __expf is
+ * the fast exponential; this restatement uses expf. */
+void orc_masked_mha(const float* q, const float* k, const float* v, float* out, int T, int H,
+                    int Dk, int valid, float scale) {
+  float* s = (float*)malloc(sizeof(float) * (size_t)T);
+  for (int h = 0; h < H; ++h)
+    for (int i = 0; i < T; ++i) {
+      const float* qr = q + ((size_t)i * H + h) * Dk;
+      float mx = -1e30f;
+      for (int j = 0; j < T; ++j) {
+        const float* kr = k + ((size_t)j * H + h) * Dk;
+        float raw = 0.0f;
+        for (int d = 0; d < Dk; ++d) raw += qr[d] * kr[d];
+        s[j] = j >= valid ? -1e30f : raw * scale;
+        if (s[j] > mx) mx = s[j];
+      }
+      float sum = 0.0f;
+      for (int j = 0; j < T; ++j) {
+        s[j] = expf(s[j] - mx);
+        sum += s[j];
+      }
+      const float inv = 1.0f / sum;
+      for (int j = 0; j < T; ++j) s[j] *= inv;
+      float* o = out + ((size_t)i * H + h) * Dk;
+      for (int d = 0; d < Dk; ++d) {
+        float acc = 0.0f;
+        for (int j = 0; j < T; ++j) acc += s[j] * v[((size_t)j * H + h) * Dk + d];
+        o[d] = acc;
+      }
+    }
+  free(s);
 }
 
 /* asr_gemm::LinearPre (src/model/asr_gemm.cu:175-208; kernels :62-155): out[m,n] =

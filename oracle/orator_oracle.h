@@ -107,6 +107,10 @@ void orc_sgemm(const float* in, const float* W, const float* bias, float* out, i
 void orc_sgemm_batched(const float* in, const float* W, float* out, int M, int K, int N, int act,
                        int batch, long stride_in, long stride_w, long stride_out);
 
+/* ---- Sortformer decoder MHA (src/model/sortformer_decoder.cu:280-298) ---- */
+void orc_masked_mha(const float* q, const float* k, const float* v, float* out, int T, int H,
+                    int Dk, int valid, float scale);
+
 /* ---- WindowAttnKernel (src/model/asr_audio_tower.cu:204-258) ---- */
 void orc_window_attention(const float* q, const float* k, const float* v, float* out,
                           const int* seg_start, const int* seg_end, int N, int H, int Dh,

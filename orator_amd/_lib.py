@@ -107,6 +107,7 @@ SIGNATURES: dict[str, list] = {
     "orator_kv_write_paged": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p],
     "orator_gqa_decode": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+    "orator_masked_mha": [_p, _p, _p, _p, _i, _i, _i, _i, _f, _p],
     "orator_window_attention": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _f, _p],
     "orator_gqa_decode_append": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_decode_append_paged": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _i, _i, _i,

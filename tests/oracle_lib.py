@@ -60,6 +60,7 @@ def lib() -> C.CDLL:
             "orc_argmax_banned": ([_F, i, i, i], i),
             "orc_linear_bf16": ([_U16, _U16, _F, _F, i, i, i, i], None),
             "orc_window_attention": ([_F, _F, _F, _F, _I, _I, i, i, i, f], None),
+            "orc_masked_mha": ([_F, _F, _F, _F, i, i, i, i, f], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -286,6 +287,14 @@ def window_attention(q, k, v, seg_start, seg_end, scale) -> np.ndarray:
     se = np.ascontiguousarray(seg_end, dtype=np.int32)
     out = np.empty_like(q)
     lib().orc_window_attention(_f(q), _f(k), _f(v), _f(out), _i(ss), _i(se), N, H, Dh, scale)
+    return out
+
+
+def masked_mha(q, k, v, valid, scale) -> np.ndarray:
+    q, k, v = f32c(q), f32c(k), f32c(v)
+    T, H, Dk = q.shape
+    out = np.empty_like(q)
+    lib().orc_masked_mha(_f(q), _f(k), _f(v), _f(out), T, H, Dk, valid, scale)
     return out
 
 

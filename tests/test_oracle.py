@@ -604,3 +604,32 @@ def test_window_attention_block_diagonal_and_empty():
         rows = [i for i in range(s0, s1) if i != 5]
         assert rel_err(got[rows], want[[i - s0 for i in rows]], 0.05) < 1e-5
     assert np.all(got[5] == 0)
+
+
+# ------------------------------------------------------------------ masked MHA ----
+
+
+@pytest.mark.parametrize("valid", [41, 25, 0])
+def test_masked_mha_vs_sdpa_and_relpos(valid):
+    """The Sortformer decomposition against torch SDPA with a key mask (fp64), against the
+    rel-pos oracle with u = v = 0 and P = 0 (the same softmax over AC), and valid_len 0 giving
+    the mean of V (every score -1e30, uniform softmax)."""
+    torch, F = _torch()
+    r = SplitMix64(70 + valid)
+    T, H, Dk = 41, 8, 24
+    q, k, v = r.normal((T, H, Dk)), r.normal((T, H, Dk)), r.normal((T, H, Dk))
+    scale = 1.0 / math.sqrt(Dk)
+    got = orc.masked_mha(q, k, v, valid, scale)
+    if valid == 0:
+        want = np.broadcast_to(v.astype(np.float64).mean(axis=0), v.shape)
+        assert rel_err(got, want, 0.05) < 1e-5
+        return
+    qt, kt, vt = (torch.from_numpy(a).double().permute(1, 0, 2) for a in (q, k, v))
+    mask = torch.zeros(T, T, dtype=torch.bool)
+    mask[:, :valid] = True
+    ref = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask, scale=scale)
+    assert rel_err(got, ref.permute(1, 0, 2).numpy(), 0.05) < 1e-5
+    z = np.zeros
+    rp = orc.relpos_attention(q, k, v, z((2 * T - 1, H, Dk), np.float32), z((H, Dk), np.float32),
+                              z((H, Dk), np.float32), valid, scale)
+    assert rel_err(got, rp, 0.05) < 1e-5
