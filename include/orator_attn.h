@@ -261,6 +261,30 @@ int orator_decoder_decode_greedy(void* handle, int start_pos, int max_new, int e
 int orator_decoder_truncate(void* handle, int len);
 int orator_decoder_cache_len(void* handle, int* len);
 
+/* -------------------------------------------------------- Conformer layer ---- */
+/* ConformerLayer (include/model/conformer_layer.h:31-65) over caller-owned fp32 device
+ * weights, in the checkpoint order of src/model/conformer_layer.cu:270-308. */
+typedef struct OratorConformerWeights {
+  const float *norm_ff1_w, *norm_ff1_b, *ff1_w1, *ff1_b1, *ff1_w2, *ff1_b2;
+  const float *norm_att_w, *norm_att_b, *q_w, *q_b, *k_w, *k_b, *v_w, *v_b, *out_w, *out_b;
+  const float *pos_w, *pos_bias_u, *pos_bias_v;
+  const float *norm_conv_w, *norm_conv_b, *pw1_w, *pw1_b, *dw_w, *dw_b;
+  const float *bn_w, *bn_b, *bn_mean, *bn_var, *pw2_w, *pw2_b;
+  const float *norm_ff2_w, *norm_ff2_b, *ff2_w1, *ff2_b1, *ff2_w2, *ff2_b2;
+  const float *norm_out_w, *norm_out_b;
+} OratorConformerWeights;
+/* ConformerLayer(d_model, n_heads, d_ff, conv_kernel) + LoadWeights (conformer_layer.h:33-37);
+ * the weights stay owned by the caller. */
+int orator_conformer_create(int d_model, int n_heads, int d_ff, int conv_kernel,
+                            const OratorConformerWeights* weights, void** handle);
+int orator_conformer_destroy(void* handle);
+/* ConformerLayer::Forward (conformer_layer.h:39-43, .cu:364-488): x [T, d_model] in place,
+ * pos_emb [2T-1, d_model] (BuildPosEmb), frames >= valid_len masked.  attn_mode 0 runs the
+ * attention core in fp32 in the reference's decomposition, 1 the fused fp16 MFMA kernel
+ * (d_model / n_heads = 64). */
+int orator_conformer_forward(void* handle, float* x, int T, int valid_len, const float* pos_emb,
+                             int attn_mode, void* stream);
+
 /* ----------------------------------------------------------------- GEMM ---- */
 /* gemm::LaunchSgemm (include/model/gemm.cuh:160-174): out[M,N] = act(in[M,K] W[N,K]^T + bias),
  * act 0 none, 1 SiLU, 2 ReLU, 3 sigmoid (gemm.cuh:38-45); bias may be NULL. */

@@ -28,6 +28,9 @@
  *   orc_argmax_banned       numpy argmax with bans; the reference tie rule on planted ties
  *   orc_linear_bf16         fp64 numpy matmul of the bf16-decoded operands; GELU against
  *                           math.erf; ReLU; bias
+ *   orc_layer_norm,         torch F.layer_norm / F.glu / F.conv1d(groups=C) + F.batch_norm
+ *   orc_glu_mask,           (eval) + F.silu in fp64; the composed Conformer layer against the
+ *   orc_dwconv_bn_silu      same torch routines with the rel-pos core from orc_relpos_attention
  *   orc_masked_mha          torch SDPA with a key-padding mask; == orc_relpos_attention with
  *                           u = v = 0 and P = 0; valid_len 0 -> mean of V
  *   orc_window_attention    full windows == orc_gqa_attention non-causal (torch SDPA pinned);
@@ -691,6 +694,50 @@ void orc_masked_mha(const float* q, const float* k, const float* v, float* out, 
       }
     }
   free(s);
+}
+
+/* LayerNormKernel (src/model/conformer_layer.cu:28-66): mean, mean square deviation,
+ * inv = 1 / sqrt(var + eps), y = (x - mean) inv g + b, per row of C. */
+void orc_layer_norm(const float* x, const float* g, const float* b, float* y, int T, int C,
+                    float eps) {
+  for (int t = 0; t < T; ++t) {
+    const float* xr = x + (size_t)t * C;
+    float* yr = y + (size_t)t * C;
+    float s = 0.0f;
+    for (int c = 0; c < C; ++c) s += xr[c];
+    const float mean = s / (float)C;
+    float sq = 0.0f;
+    for (int c = 0; c < C; ++c) sq += (xr[c] - mean) * (xr[c] - mean);
+    const float inv = 1.0f / sqrtf(sq / (float)C + eps);
+    for (int c = 0; c < C; ++c) yr[c] = (xr[c] - mean) * inv * g[c] + b[c];
+  }
+}
+
+/* GluKernel (:207-215) + MaskRowsKernel (:78-83): out[t,c] = a sigmoid(b) for t < valid,
+ * else 0; in [T, 2C] = a | b. */
+void orc_glu_mask(const float* in, float* out, int T, int C, int valid) {
+  for (int t = 0; t < T; ++t)
+    for (int c = 0; c < C; ++c) {
+      const float a = in[(size_t)t * 2 * C + c], b = in[(size_t)t * 2 * C + C + c];
+      out[(size_t)t * C + c] = t < valid ? a * (1.0f / (1.0f + expf(-b))) : 0.0f;
+    }
+}
+
+/* DepthwiseConvKernel (:218-233) + BatchNormSiluKernel (:236-246). */
+void orc_dwconv_bn_silu(const float* in, const float* w, const float* bias, const float* mean,
+                        const float* var, const float* gamma, const float* beta, float* out,
+                        int T, int C, int K, float eps) {
+  const int pad = (K - 1) / 2;
+  for (int t = 0; t < T; ++t)
+    for (int c = 0; c < C; ++c) {
+      float acc = bias ? bias[c] : 0.0f;
+      for (int k = 0; k < K; ++k) {
+        const int ti = t + k - pad;
+        if (ti >= 0 && ti < T) acc += in[(size_t)ti * C + c] * w[(size_t)c * K + k];
+      }
+      const float y = (acc - mean[c]) * (1.0f / sqrtf(var[c] + eps)) * gamma[c] + beta[c];
+      out[(size_t)t * C + c] = y / (1.0f + expf(-y));
+    }
 }
 
 /* asr_gemm::LinearPre (src/model/asr_gemm.cu:175-208; kernels :62-155): out[m,n] =

@@ -107,6 +107,14 @@ void orc_sgemm(const float* in, const float* W, const float* bias, float* out, i
 void orc_sgemm_batched(const float* in, const float* W, float* out, int M, int K, int N, int act,
                        int batch, long stride_in, long stride_w, long stride_out);
 
+/* ---- Conformer non-attention passes (src/model/conformer_layer.cu:28-83,207-246) ---- */
+void orc_layer_norm(const float* x, const float* g, const float* b, float* y, int T, int C,
+                    float eps);
+void orc_glu_mask(const float* in, float* out, int T, int C, int valid);
+void orc_dwconv_bn_silu(const float* in, const float* w, const float* bias, const float* mean,
+                        const float* var, const float* gamma, const float* beta, float* out,
+                        int T, int C, int K, float eps);
+
 /* ---- Sortformer decoder MHA (src/model/sortformer_decoder.cu:280-298) ---- */
 void orc_masked_mha(const float* q, const float* k, const float* v, float* out, int T, int H,
                     int Dk, int valid, float scale);

@@ -46,6 +46,19 @@ class DecoderLayer(C.Structure):
                 ("qkv_w", _p), ("o_w", _p), ("gateup_w", _p), ("down_w", _p)]
 
 
+class ConformerWeights(C.Structure):
+    """OratorConformerWeights: the 39 fp32 tensors of one ConformerLayer, checkpoint order
+    (src/model/conformer_layer.cu:270-308)."""
+    _fields_ = [(n, _p) for n in (
+        "norm_ff1_w", "norm_ff1_b", "ff1_w1", "ff1_b1", "ff1_w2", "ff1_b2",
+        "norm_att_w", "norm_att_b", "q_w", "q_b", "k_w", "k_b", "v_w", "v_b", "out_w", "out_b",
+        "pos_w", "pos_bias_u", "pos_bias_v",
+        "norm_conv_w", "norm_conv_b", "pw1_w", "pw1_b", "dw_w", "dw_b",
+        "bn_w", "bn_b", "bn_mean", "bn_var", "pw2_w", "pw2_b",
+        "norm_ff2_w", "norm_ff2_b", "ff2_w1", "ff2_b1", "ff2_w2", "ff2_b2",
+        "norm_out_w", "norm_out_b")]
+
+
 # name -> argument types (all return int status)
 SIGNATURES: dict[str, list] = {
     # bf16-weight linear and decode-step glue
@@ -107,6 +120,9 @@ SIGNATURES: dict[str, list] = {
     "orator_kv_write_paged": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p],
     "orator_gqa_decode": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+    "orator_conformer_create": [_i, _i, _i, _i, C.POINTER(ConformerWeights), C.POINTER(_p)],
+    "orator_conformer_destroy": [_p],
+    "orator_conformer_forward": [_p, _p, _i, _i, _p, _i, _p],
     "orator_masked_mha": [_p, _p, _p, _p, _i, _i, _i, _i, _f, _p],
     "orator_window_attention": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _f, _p],
     "orator_gqa_decode_append": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],

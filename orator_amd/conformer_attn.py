@@ -36,3 +36,41 @@ def BuildPosEmb(T: int, d_model: int) -> np.ndarray:
     pe = np.empty((max(2 * T - 1, 0), d_model), np.float32)
     call("orator_build_pos_emb", pe.ctypes.data, T, d_model)
     return pe
+
+
+class ConformerLayer:
+    """ConformerLayer (include/model/conformer_layer.h:31-65) over caller-owned fp32 device
+    weights: `weights` maps each OratorConformerWeights field name to a device buffer."""
+
+    def __init__(self, weights: dict, d_model: int = 512, n_heads: int = 8, d_ff: int = 2048,
+                 conv_kernel: int = 9):
+        from ._lib import ConformerWeights
+        import ctypes as C
+        w = ConformerWeights(*[ptr(weights[name]) for name, _ in ConformerWeights._fields_])
+        h = C.c_void_p()
+        call("orator_conformer_create", d_model, n_heads, d_ff, conv_kernel, C.byref(w),
+             C.byref(h))
+        self._h = h
+        self._keep = weights
+        self.d_model = d_model
+
+    def Forward(self, x, T: int, valid_len: int, pos_emb, stream=None, attn_mode: int = 0):
+        """x [T, d_model] device fp32 in place; pos_emb [2T-1, d_model] device fp32."""
+        call("orator_conformer_forward", self._h, ptr(x), T, valid_len, ptr(pos_emb), attn_mode,
+             _sh(stream))
+
+    @staticmethod
+    def BuildPosEmb(T: int, d_model: int):
+        return BuildPosEmb(T, d_model)
+
+    def close(self) -> None:
+        if self._h:
+            from ._lib import lib
+            lib().orator_conformer_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,166 @@
+// One FastConformer layer, the Sortformer encoder's (ConformerLayer::Forward,
+// src/model/conformer_layer.cu:364-488), composed from this library's operators:
+//   x += 0.5 FFN1(LN(x))                                   FFN: Linear+SiLU, Linear
+//   x += MHSA(LN(x))        linear_q/k/v, linear_pos(pos_emb), rel-pos attention, linear_out
+//   x += Conv(LN(x))        pointwise 2C, GLU (+ padding-row mask), depthwise K,
+//                           BatchNorm(eval)+SiLU, pointwise C
+//   x += 0.5 FFN2(LN(x));  x = LN_out(x)
+// The projections run on the fp32 MFMA SGEMM; the attention core is either the reference
+// decomposition in fp32 (attn_mode 0) or the fused fp16 MFMA kernel (attn_mode 1).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <new>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace orator_hip {
+
+int launch_layer_norm(const float* in, const float* g, const float* b, float* out, int T, int C,
+                      float eps, hipStream_t s);
+int launch_glu_mask(const float* in, float* out, int T, int C, int valid, hipStream_t s);
+int launch_dwconv_bn_silu(const float* in, const float* w, const float* bias, const float* mean,
+                          const float* var, const float* gamma, const float* beta, float* out,
+                          int T, int C, int K, float eps, hipStream_t s);
+int launch_add_scaled(float* r, const float* x, float scale, long n, hipStream_t s);
+
+namespace {
+
+constexpr float kEps = 1e-5f;  // conformer_layer.cu:368
+
+struct Conformer {
+  int D = 0, H = 0, Dff = 0, K = 0;
+  OratorConformerWeights w{};
+  int cap_t = 0;
+  float *ln = nullptr, *ff = nullptr, *tmp = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
+        *p = nullptr, *ctx = nullptr, *pw1 = nullptr, *glu = nullptr, *dw = nullptr;
+
+  ~Conformer() { release(); }
+
+  void release() {
+    for (float* b : {ln, ff, tmp, q, k, v, p, ctx, pw1, glu, dw})
+      if (b) (void)hipFree(b);
+    ln = ff = tmp = q = k = v = p = ctx = pw1 = glu = dw = nullptr;
+    cap_t = 0;
+  }
+
+  int grow(int T) {
+    if (T <= cap_t) return ORATOR_OK;
+    release();
+    const size_t t = T, P = 2 * t - 1;
+    const std::pair<float**, size_t> bufs[] = {
+        {&ln, t * D},  {&ff, t * Dff}, {&tmp, t * D},     {&q, t * D},     {&k, t * D},
+        {&v, t * D},   {&p, P * D},    {&ctx, t * D},     {&pw1, 2 * t * D}, {&glu, t * D},
+        {&dw, t * D}};
+    for (const auto& [ptr, n] : bufs)
+      if (int rc = check_hip(hipMalloc(reinterpret_cast<void**>(ptr), n * sizeof(float)),
+                             "conformer scratch"))
+        return rc;
+    cap_t = T;
+    return ORATOR_OK;
+  }
+
+  int linear(const float* in, const float* W, const float* b, float* out, int M, int Kd, int N,
+             int act, hipStream_t s) {
+    return orator_sgemm(in, W, b, out, M, Kd, N, act, s);
+  }
+
+  int ffn(float* x, int T, const float* nw, const float* nb, const float* w1, const float* b1,
+          const float* w2, const float* b2, hipStream_t s) {
+    int rc = 0;
+    (rc = launch_layer_norm(x, nw, nb, ln, T, D, kEps, s)) ||
+        (rc = linear(ln, w1, b1, ff, T, D, Dff, 1, s)) ||  // SiLU
+        (rc = linear(ff, w2, b2, tmp, T, Dff, D, 0, s)) ||
+        (rc = launch_add_scaled(x, tmp, 0.5f, static_cast<long>(T) * D, s));
+    return rc;
+  }
+
+  int forward(float* x, int T, int valid, const float* pos_emb, int attn_mode, hipStream_t s) {
+    if (int rc = grow(T)) return rc;
+    const int P = 2 * T - 1, Dk = D / H;
+    const long TD = static_cast<long>(T) * D;
+    const float scale = 1.0f / std::sqrt(static_cast<float>(Dk));
+    int rc = 0;
+    // FFN1
+    if ((rc = ffn(x, T, w.norm_ff1_w, w.norm_ff1_b, w.ff1_w1, w.ff1_b1, w.ff1_w2, w.ff1_b2, s)))
+      return rc;
+    // MHSA
+    (rc = launch_layer_norm(x, w.norm_att_w, w.norm_att_b, ln, T, D, kEps, s)) ||
+        (rc = linear(ln, w.q_w, w.q_b, q, T, D, D, 0, s)) ||
+        (rc = linear(ln, w.k_w, w.k_b, k, T, D, D, 0, s)) ||
+        (rc = linear(ln, w.v_w, w.v_b, v, T, D, D, 0, s)) ||
+        (rc = linear(pos_emb, w.pos_w, nullptr, p, P, D, D, 0, s));
+    if (rc) return rc;
+    rc = attn_mode == 1
+             ? orator_relpos_attention_fast(q, k, v, p, w.pos_bias_u, w.pos_bias_v, ctx, T, H, Dk,
+                                            valid, scale, 0, s)
+             : orator_relpos_attention(q, k, v, p, w.pos_bias_u, w.pos_bias_v, ctx, T, H, Dk,
+                                       valid, scale, s);
+    (rc) || (rc = linear(ctx, w.out_w, w.out_b, tmp, T, D, D, 0, s)) ||
+        (rc = launch_add_scaled(x, tmp, 1.0f, TD, s));
+    if (rc) return rc;
+    // Conv module
+    (rc = launch_layer_norm(x, w.norm_conv_w, w.norm_conv_b, ln, T, D, kEps, s)) ||
+        (rc = linear(ln, w.pw1_w, w.pw1_b, pw1, T, D, 2 * D, 0, s)) ||
+        (rc = launch_glu_mask(pw1, glu, T, D, valid, s)) ||
+        (rc = launch_dwconv_bn_silu(glu, w.dw_w, w.dw_b, w.bn_mean, w.bn_var, w.bn_w, w.bn_b, dw,
+                                    T, D, K, kEps, s)) ||
+        (rc = linear(dw, w.pw2_w, w.pw2_b, tmp, T, D, D, 0, s)) ||
+        (rc = launch_add_scaled(x, tmp, 1.0f, TD, s));
+    if (rc) return rc;
+    // FFN2, norm_out
+    (rc = ffn(x, T, w.norm_ff2_w, w.norm_ff2_b, w.ff2_w1, w.ff2_b1, w.ff2_w2, w.ff2_b2, s)) ||
+        (rc = launch_layer_norm(x, w.norm_out_w, w.norm_out_b, ln, T, D, kEps, s)) ||
+        (rc = check_hip(hipMemcpyAsync(x, ln, TD * sizeof(float), hipMemcpyDeviceToDevice, s),
+                        "conformer out"));
+    return rc;
+  }
+};
+
+}  // namespace
+}  // namespace orator_hip
+
+using namespace orator_hip;
+
+extern "C" {
+
+int orator_conformer_create(int d_model, int n_heads, int d_ff, int conv_kernel,
+                            const OratorConformerWeights* weights, void** handle) {
+  if (!handle) return fail(ORATOR_ERR_INVALID, "conformer_create: null handle");
+  *handle = nullptr;
+  if (!weights) return fail(ORATOR_ERR_INVALID, "conformer_create: null weights");
+  if (d_model <= 0 || n_heads <= 0 || d_ff <= 0 || conv_kernel <= 0 || d_model % n_heads)
+    return fail(ORATOR_ERR_INVALID, "conformer_create: bad sizes");
+  const float* const* wp = reinterpret_cast<const float* const*>(weights);
+  for (size_t i = 0; i < sizeof(OratorConformerWeights) / sizeof(float*); ++i)
+    if (!wp[i]) return fail(ORATOR_ERR_INVALID, "conformer_create: null weight");
+  Conformer* c = new (std::nothrow) Conformer();
+  if (!c) return fail(ORATOR_ERR_CAPACITY, "conformer_create: out of host memory");
+  c->D = d_model;
+  c->H = n_heads;
+  c->Dff = d_ff;
+  c->K = conv_kernel;
+  c->w = *weights;
+  *handle = c;
+  return ORATOR_OK;
+}
+
+int orator_conformer_destroy(void* handle) {
+  delete static_cast<Conformer*>(handle);
+  return ORATOR_OK;
+}
+
+int orator_conformer_forward(void* handle, float* x, int T, int valid_len, const float* pos_emb,
+                             int attn_mode, void* stream) {
+  Conformer* c = static_cast<Conformer*>(handle);
+  if (!c || !x || !pos_emb) return fail(ORATOR_ERR_INVALID, "conformer_forward: null pointer");
+  if (T <= 0) return ORATOR_OK;
+  if (attn_mode != 0 && attn_mode != 1)
+    return fail(ORATOR_ERR_INVALID, "conformer_forward: attn_mode 0 (fp32) or 1 (fused fp16)");
+  if (attn_mode == 1 && c->D / c->H != 64)
+    return fail(ORATOR_ERR_UNSUPPORTED, "conformer_forward: the fused attention needs Dk = 64");
+  return c->forward(x, T, valid_len, pos_emb, attn_mode, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -61,6 +61,9 @@ def lib() -> C.CDLL:
             "orc_linear_bf16": ([_U16, _U16, _F, _F, i, i, i, i], None),
             "orc_window_attention": ([_F, _F, _F, _F, _I, _I, i, i, i, f], None),
             "orc_masked_mha": ([_F, _F, _F, _F, i, i, i, i, f], None),
+            "orc_layer_norm": ([_F, _F, _F, _F, i, i, f], None),
+            "orc_glu_mask": ([_F, _F, i, i, i], None),
+            "orc_dwconv_bn_silu": ([_F, _F, _F, _F, _F, _F, _F, _F, i, i, i, f], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -296,6 +299,73 @@ def masked_mha(q, k, v, valid, scale) -> np.ndarray:
     out = np.empty_like(q)
     lib().orc_masked_mha(_f(q), _f(k), _f(v), _f(out), T, H, Dk, valid, scale)
     return out
+
+
+# -------------------------------------------------------------- Conformer ----
+CONFORMER_FIELDS = (
+    "norm_ff1_w", "norm_ff1_b", "ff1_w1", "ff1_b1", "ff1_w2", "ff1_b2",
+    "norm_att_w", "norm_att_b", "q_w", "q_b", "k_w", "k_b", "v_w", "v_b", "out_w", "out_b",
+    "pos_w", "pos_bias_u", "pos_bias_v",
+    "norm_conv_w", "norm_conv_b", "pw1_w", "pw1_b", "dw_w", "dw_b",
+    "bn_w", "bn_b", "bn_mean", "bn_var", "pw2_w", "pw2_b",
+    "norm_ff2_w", "norm_ff2_b", "ff2_w1", "ff2_b1", "ff2_w2", "ff2_b2",
+    "norm_out_w", "norm_out_b")
+
+
+def layer_norm(x, g, b, eps=1e-5) -> np.ndarray:
+    x, g, b = f32c(x), f32c(g), f32c(b)
+    T, C = x.shape
+    out = np.empty_like(x)
+    lib().orc_layer_norm(_f(x), _f(g), _f(b), _f(out), T, C, eps)
+    return out
+
+
+def glu_mask(x, valid) -> np.ndarray:
+    x = f32c(x)
+    T, C2 = x.shape
+    out = np.empty((T, C2 // 2), np.float32)
+    lib().orc_glu_mask(_f(x), _f(out), T, C2 // 2, valid)
+    return out
+
+
+def dwconv_bn_silu(x, w, bias, mean, var, gamma, beta, eps=1e-5) -> np.ndarray:
+    x, w, bias, mean, var, gamma, beta = map(f32c, (x, w, bias, mean, var, gamma, beta))
+    T, C = x.shape
+    K = w.shape[-1]
+    out = np.empty_like(x)
+    lib().orc_dwconv_bn_silu(_f(x), _f(w), _f(bias), _f(mean), _f(var), _f(gamma), _f(beta),
+                             _f(out), T, C, K, eps)
+    return out
+
+
+def conformer_layer(x, T, valid, pos_emb, W, H, eps=1e-5):
+    """ConformerLayer::Forward (src/model/conformer_layer.cu:364-488) on the oracle pieces:
+    LaunchLinear = orc_sgemm (act 1 SiLU), the rel-pos core = orc_relpos_attention."""
+    x = f32c(x).copy()
+    D = x.shape[1]
+    Dk = D // H
+
+    def ffn(x, p):
+        ln = layer_norm(x, W[f"norm_{p}_w"], W[f"norm_{p}_b"], eps)
+        h = sgemm(ln, W[f"{p}_w1"], W[f"{p}_b1"], act=1)
+        return x + np.float32(0.5) * sgemm(h, W[f"{p}_w2"], W[f"{p}_b2"])
+
+    x = ffn(x, "ff1")
+    ln = layer_norm(x, W["norm_att_w"], W["norm_att_b"], eps)
+    q = sgemm(ln, W["q_w"], W["q_b"]).reshape(T, H, Dk)
+    k = sgemm(ln, W["k_w"], W["k_b"]).reshape(T, H, Dk)
+    v = sgemm(ln, W["v_w"], W["v_b"]).reshape(T, H, Dk)
+    p = sgemm(pos_emb, W["pos_w"]).reshape(2 * T - 1, H, Dk)
+    ctx = relpos_attention(q, k, v, p, W["pos_bias_u"], W["pos_bias_v"], valid,
+                           float(1.0 / np.sqrt(np.float32(Dk))))
+    x = x + sgemm(ctx.reshape(T, D), W["out_w"], W["out_b"])
+    ln = layer_norm(x, W["norm_conv_w"], W["norm_conv_b"], eps)
+    g = glu_mask(sgemm(ln, W["pw1_w"], W["pw1_b"]), valid)
+    c = dwconv_bn_silu(g, W["dw_w"], W["dw_b"], W["bn_mean"], W["bn_var"], W["bn_w"],
+                       W["bn_b"], eps)
+    x = x + sgemm(c, W["pw2_w"], W["pw2_b"])
+    x = ffn(x, "ff2")
+    return layer_norm(x, W["norm_out_w"], W["norm_out_b"], eps)
 
 
 # ------------------------------------------------------------- bf16 linear ----

@@ -633,3 +633,65 @@ def test_masked_mha_vs_sdpa_and_relpos(valid):
     rp = orc.relpos_attention(q, k, v, z((2 * T - 1, H, Dk), np.float32), z((H, Dk), np.float32),
                               z((H, Dk), np.float32), valid, scale)
     assert rel_err(got, rp, 0.05) < 1e-5
+
+
+# ------------------------------------------------------------ Conformer layer ----
+
+
+from conformer_model import conformer_weights as _conformer_weights  # noqa: E402
+
+
+def test_conformer_passes_vs_torch():
+    torch, F = _torch()
+    r = SplitMix64(80)
+    T, C, K = 19, 24, 9
+    x = r.normal((T, C))
+    g, b = 1 + r.normal(C, 0.1), r.normal(C, 0.1)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.float64))
+    want = F.layer_norm(t(x), (C,), t(g), t(b), eps=1e-5).numpy()
+    assert rel_err(orc.layer_norm(x, g, b), want, 0.05) < 1e-5
+    x2 = r.normal((T, 2 * C))
+    want = F.glu(t(x2), dim=-1).numpy()
+    want[13:] = 0
+    assert rel_err(orc.glu_mask(x2, 13), want, 0.05) < 1e-6
+    w, bias = r.normal((C, K), 0.3), r.normal(C, 0.1)
+    mean, var = r.normal(C, 0.1), (0.5 + r.uniform(C)).astype(np.float32)
+    conv = F.conv1d(t(x).T[None], t(w)[:, None, :], t(bias), padding=(K - 1) // 2, groups=C)
+    y = F.silu(F.batch_norm(conv, t(mean), t(var), t(g), t(b), training=False, eps=1e-5))
+    got = orc.dwconv_bn_silu(x, w, bias, mean, var, g, b)
+    assert rel_err(got, y[0].T.numpy(), 0.05) < 1e-5
+
+
+def test_conformer_layer_vs_torch_composition():
+    """The composed layer against the same steps written with torch routines in fp64 (the
+    rel-pos core from the fp64 oracle), so a wrong residual weight, norm or order fails."""
+    torch, F = _torch()
+    r = SplitMix64(81)
+    T, D, H, Dff, K, valid = 21, 32, 2, 64, 9, 17
+    W = _conformer_weights(r, D, H, Dff, K)
+    x = r.normal((T, D))
+    pe = orc.build_pos_emb(T, D)
+    got = orc.conformer_layer(x, T, valid, pe, W, H)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.float64))
+    Tw = {k: t(v) for k, v in W.items()}
+    X = t(x)
+    ln = lambda z, n: F.layer_norm(z, (D,), Tw[f"norm_{n}_w"], Tw[f"norm_{n}_b"], eps=1e-5)
+    ffn = lambda z, p: F.linear(F.silu(F.linear(ln(z, p), Tw[f"{p}_w1"], Tw[f"{p}_b1"])),
+                                Tw[f"{p}_w2"], Tw[f"{p}_b2"])
+    X = X + 0.5 * ffn(X, "ff1")
+    a = ln(X, "att")
+    q, k, v = (F.linear(a, Tw[f"{n}_w"], Tw[f"{n}_b"]).numpy().reshape(T, H, D // H)
+               for n in ("q", "k", "v"))
+    p = F.linear(t(pe), Tw["pos_w"]).numpy().reshape(2 * T - 1, H, D // H)
+    ctx = orc.relpos_attention_f64(q, k, v, p, W["pos_bias_u"], W["pos_bias_v"], valid,
+                                   1.0 / math.sqrt(D // H))
+    X = X + F.linear(t(ctx).reshape(T, D), Tw["out_w"], Tw["out_b"])
+    c = F.glu(F.linear(ln(X, "conv"), Tw["pw1_w"], Tw["pw1_b"]), dim=-1)
+    c[valid:] = 0
+    c = F.conv1d(c.T[None], Tw["dw_w"][:, None, :], Tw["dw_b"], padding=(K - 1) // 2, groups=D)
+    c = F.silu(F.batch_norm(c, Tw["bn_mean"], Tw["bn_var"], Tw["bn_w"], Tw["bn_b"],
+                            training=False, eps=1e-5))[0].T
+    X = X + F.linear(c, Tw["pw2_w"], Tw["pw2_b"])
+    X = X + 0.5 * ffn(X, "ff2")
+    want = ln(X, "out").numpy()
+    assert rel_err(got, want, 0.05) < 1e-4
