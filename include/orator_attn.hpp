@@ -16,6 +16,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "orator_attn.h"
 
@@ -67,8 +68,18 @@ inline void ArgmaxBanned(const float* logits, int n, int ban0, int ban1, int* ou
 
 }  // namespace asr_ops
 
-namespace asr_gemm {  // include/model/asr_gemm.h:23-25 (the cast half of the interface)
+namespace asr_gemm {  // include/model/asr_gemm.h:23-41
 
+inline void Linear(const float* in_f32, const uint16_t* W_bf16, const float* bias_f32,
+                   float* out_f32, int M, int K, int N, int act, hipStream_t stream = 0) {
+  gpu::Check(orator_linear(in_f32, W_bf16, bias_f32, out_f32, M, K, N, act, stream));
+}
+inline void LinearPre(const uint16_t* in_bf16, const uint16_t* W_bf16, const float* bias_f32,
+                      float* out_f32, int M, int K, int N, int act, hipStream_t stream = 0) {
+  gpu::Check(orator_linear_pre(in_bf16, W_bf16, bias_f32, out_f32, M, K, N, act, stream));
+}
+// The library's workspace lives until the process ends; nothing to release early.
+inline void Shutdown() {}
 inline void F32ToBf16(const float* in, uint16_t* out, long n, hipStream_t stream = 0) {
   gpu::Check(orator_f32_to_bf16(in, out, n, stream));
 }
@@ -127,10 +138,142 @@ inline void RelPosAttention(const float* q, const float* k, const float* v, cons
                                      scale, stream));
 }
 
+// ConformerLayer (include/model/conformer_layer.h:31-65) over caller-owned fp32 device
+// weights (LoadWeights' tensors, as an OratorConformerWeights of device pointers).
+class ConformerLayer {
+ public:
+  ConformerLayer(const OratorConformerWeights& weights, int d_model = 512, int n_heads = 8,
+                 int d_ff = 2048, int conv_kernel = 9) {
+    gpu::Check(orator_conformer_create(d_model, n_heads, d_ff, conv_kernel, &weights, &h_));
+  }
+  ~ConformerLayer() { orator_conformer_destroy(h_); }
+  ConformerLayer(const ConformerLayer&) = delete;
+  ConformerLayer& operator=(const ConformerLayer&) = delete;
+  // attn_mode 0: fp32 attention core (the reference's semantics); 1: fused fp16 MFMA core.
+  void Forward(float* x, int T, int valid_len, const float* pos_emb, hipStream_t stream = nullptr,
+               int attn_mode = 0) {
+    gpu::Check(orator_conformer_forward(h_, x, T, valid_len, pos_emb, attn_mode, stream));
+  }
+
+ private:
+  void* h_ = nullptr;
+};
+
 }  // namespace conformer_attn
+
+// The audio tower's WindowAttnKernel (src/model/asr_audio_tower.cu:204-258) and the Sortformer
+// decoder's masked MHA (src/model/sortformer_decoder.cu:280-298), both file-static in the
+// reference.
+namespace aux_attn {
+
+inline void WindowAttention(const float* q, const float* k, const float* v, float* out,
+                            const int* seg_start, const int* seg_end, int N, int H, int Dh,
+                            float scale, hipStream_t stream = 0) {
+  gpu::Check(orator_window_attention(q, k, v, out, seg_start, seg_end, N, H, Dh, scale, stream));
+}
+inline void MaskedSelfAttention(const float* q, const float* k, const float* v, float* out, int T,
+                                int H, int Dk, int valid_len, float scale,
+                                hipStream_t stream = 0) {
+  gpu::Check(orator_masked_mha(q, k, v, out, T, H, Dk, valid_len, scale, stream));
+}
+
+}  // namespace aux_attn
+
+// AsrTextDecoder (include/model/asr_text_decoder.h:45-112) over caller-owned device weights.
+struct AsrTextConfig {  // include/model/asr_text_decoder.h:30-42
+  int hidden_size = 2048;
+  int num_layers = 28;
+  int num_q_heads = 16;
+  int num_kv_heads = 8;
+  int head_dim = 128;
+  int intermediate_size = 6144;
+  int vocab_size = 151936;
+  float rms_norm_eps = 1e-6f;
+  float rope_theta = 1000000.0f;
+  int max_seq_len = 2048;
+  bool cuda_graph_enabled = true;  // graph replay in DecodeGreedy
+};
+
+class AsrTextDecoder {
+ public:
+  // embed / lm_head bf16 [vocab, hidden] (lm_head nullptr: tied), final_norm fp32 [hidden],
+  // layers[num_layers] in the fused qkv / gate|up layout.
+  AsrTextDecoder(const AsrTextConfig& c, const uint16_t* embed, const float* final_norm,
+                 const uint16_t* lm_head, const OratorDecoderLayer* layers)
+      : config_(c) {
+    const OratorDecoderConfig oc{c.num_layers,  c.hidden_size,       c.num_q_heads,
+                                 c.num_kv_heads, c.head_dim,         c.intermediate_size,
+                                 c.vocab_size,  c.max_seq_len,       c.rms_norm_eps,
+                                 c.rope_theta};
+    gpu::Check(orator_decoder_create(&oc, embed, final_norm, lm_head, layers, &h_));
+  }
+  ~AsrTextDecoder() { orator_decoder_destroy(h_); }
+  AsrTextDecoder(const AsrTextDecoder&) = delete;
+  AsrTextDecoder& operator=(const AsrTextDecoder&) = delete;
+
+  void ResetCache() { gpu::Check(orator_decoder_reset(h_)); }
+  void Embed(int token_id, float* out) const { gpu::Check(orator_decoder_embed(h_, token_id, out)); }
+  int hidden_size() const { return config_.hidden_size; }
+  int vocab_size() const { return config_.vocab_size; }
+  void Prefill(const float* embeds, int T, hipStream_t stream = 0) {
+    PrefillAt(embeds, T, 0, stream);
+  }
+  void PrefillAt(const float* embeds, int T, int pos0, hipStream_t stream = 0) {
+    gpu::Check(orator_decoder_prefill_at(h_, embeds, T, pos0, stream));
+  }
+  void TruncateCache(int len) { gpu::Check(orator_decoder_truncate(h_, len)); }
+  int cache_len() const {
+    int n = 0;
+    gpu::Check(orator_decoder_cache_len(h_, &n));
+    return n;
+  }
+  void DecodeStep(const float* embed, int pos, hipStream_t stream = 0) {
+    gpu::Check(orator_decoder_decode_step(h_, embed, pos, stream));
+  }
+  void DecodeStepDevice(const int* d_token, int pos, hipStream_t stream = 0) {
+    gpu::Check(orator_decoder_decode_step_device(h_, d_token, pos, stream));
+  }
+  int Argmax(int ban0 = -1, int ban1 = -1, hipStream_t stream = 0) {
+    int t = 0;
+    gpu::Check(orator_decoder_argmax(h_, ban0, ban1, &t, stream));
+    return t;
+  }
+  void ArgmaxToDevice(int* d_out, int ban0 = -1, int ban1 = -1, hipStream_t stream = 0) {
+    gpu::Check(orator_decoder_argmax_to_device(h_, d_out, ban0, ban1, stream));
+  }
+  int ReadTokenId(const int* d_token, hipStream_t stream = 0) const {
+    int t = 0;
+    gpu::Check(orator_stream_synchronize(stream));
+    gpu::Check(orator_memcpy_dtoh(&t, d_token, sizeof(int)));
+    return t;
+  }
+  std::vector<int> DecodeGreedy(int start_pos, int max_new, int eos0, int eos1,
+                                int ban_steps = 3, int batch = 32, hipStream_t stream = 0) {
+    std::vector<int> out(max_new > 0 ? max_new : 0);
+    int n = 0;
+    gpu::Check(orator_decoder_decode_greedy(h_, start_pos, max_new, eos0, eos1, ban_steps, batch,
+                                            config_.cuda_graph_enabled ? 1 : 0, out.data(), &n,
+                                            stream));
+    out.resize(n);
+    return out;
+  }
+  std::vector<float> CopyLogits() const {
+    float* d = nullptr;
+    gpu::Check(orator_decoder_logits(h_, &d));
+    std::vector<float> out(config_.vocab_size);
+    gpu::Check(orator_device_synchronize());
+    gpu::Check(orator_memcpy_dtoh(out.data(), d, sizeof(float) * out.size()));
+    return out;
+  }
+
+ private:
+  AsrTextConfig config_;
+  void* h_ = nullptr;
+};
+
 }  // namespace model
 
-namespace gemm {  // include/model/gemm.cuh:160-174, 251-268
+namespace gemm {  // include/model/gemm.cuh:160-174, 251-268, 483-501
 
 inline void LaunchSgemm(const float* in, const float* W, const float* bias, float* out, int M,
                         int K, int N, int act) {
@@ -150,6 +293,11 @@ inline void LaunchSgemmBatched(const float* in, const float* W, float* out, int 
                                hipStream_t stream) {
   gpu::Check(orator_sgemm_batched(in, W, out, M, K, N, act, batch, strideIn, strideW, strideOut,
                                   stream));
+}
+
+inline void LaunchBf16Gemm(const uint16_t* in, const uint16_t* W, const float* bias, float* out,
+                           int M, int K, int N, int act, hipStream_t stream) {
+  gpu::Check(orator_bf16_gemm(in, W, bias, out, M, K, N, act, stream));
 }
 
 }  // namespace gemm

@@ -72,20 +72,25 @@ def build_hip(jobs: int | None = None) -> Path:
     return LIB
 
 
-CPP_TEST_SRC = ROOT / "tests" / "cpp" / "test_asr_ops.cc"
-CPP_TEST_BIN = ROOT / "tests" / "cpp" / "test_asr_ops"
+CPP_TESTS = ("test_asr_ops", "test_asr_decoder")
 
 
-def build_cpp_tests() -> Path:
-    """The C++ drop-in header exercised by a host program (g++, links the library)."""
-    cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__",
-           "-I", str(ROOT / "include"), "-I", "/opt/rocm/include", str(CPP_TEST_SRC),
-           "-o", str(CPP_TEST_BIN), f"-L{PKG}", "-lorator_attn", "-Wl,-rpath,$ORIGIN/../../orator_amd",
-           f"-L{ROCM_LIB}", "-lamdhip64", f"-Wl,-rpath,{ROCM_LIB}"]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"C++ test build failed:\n{proc.stdout}{proc.stderr}")
-    return CPP_TEST_BIN
+def build_cpp_tests() -> list[Path]:
+    """The C++ drop-in header exercised by host programs (g++, linking the library)."""
+    bins = []
+    for name in CPP_TESTS:
+        src = ROOT / "tests" / "cpp" / f"{name}.cc"
+        out = ROOT / "tests" / "cpp" / name
+        cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__",
+               "-I", str(ROOT / "include"), "-I", "/opt/rocm/include", str(src),
+               "-o", str(out), f"-L{PKG}", "-lorator_attn",
+               "-Wl,-rpath,$ORIGIN/../../orator_amd",
+               f"-L{ROCM_LIB}", "-lamdhip64", f"-Wl,-rpath,{ROCM_LIB}"]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"C++ test build failed:\n{proc.stdout}{proc.stderr}")
+        bins.append(out)
+    return bins
 
 
 def build_oracle() -> Path:

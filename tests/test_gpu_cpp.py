@@ -23,3 +23,15 @@ def test_cpp_dropin_asr_ops(golden, tmp_path):
     print(proc.stdout)
     assert proc.returncode == 0, proc.stdout + proc.stderr
     assert "PASSED" in proc.stdout
+
+
+def test_cpp_dropin_asr_decoder():
+    """tests/cpp/test_asr_decoder.cc: the reference decoder test's incremental-prefill and
+    truncate checks plus graph-replayed vs eager greedy decoding, through the C++ class."""
+    exe = BIN.parent / "test_asr_decoder"
+    assert exe.exists(), "build() compiles tests/cpp/test_asr_decoder"
+    print("[gpu-case] C++ drop-in decoder test", flush=True)
+    proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    print(proc.stdout)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "PASSED" in proc.stdout
