@@ -10,10 +10,11 @@ synthetic and resident in HBM before timing.
 
 `value` = decode-attention algorithmic bytes / wall time of the K timed steps, where the
 bytes per (stream, layer, step) are 2*S*Hkv*Dh*2 (K and V read once) + Hq*Dh*4 (q) +
-Hq*Dh*4 (out) + 4 B per page-table entry.  The roofline object divides the same bytes
-per launch by the decode kernel's average launch duration (HIP events around each launch
-on its stream).  The CPU baseline is the oracle's scalar decode on the host cores, over a
-bounded sample of the same workload.
+Hq*Dh*4 (out) + 4 B per page-table entry.  The roofline object divides the bytes of one
+decode operation (the split-K kernel and its merge, B = 16 streams of one layer) by the
+operation's average duration: the HIP events that bracket the timed region on the launch
+stream, over its K * 28 back-to-back operations.  The CPU baseline is the oracle's scalar
+decode on the host cores, over a bounded sample of the same workload.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -36,7 +37,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
 
 LAYERS, B, HQ, HKV, DH, L_BASE, PAGE = 28, 16, 16, 8, 128, 4096, 16
-HBM_TRAFFIC_PER_OP = 274.0e6  # bytes, measured with rocprofv3 --pmc (profiles/decode_b16_l4096_hbm_traffic.md)
+HBM_TRAFFIC_PER_OP = 277.4e6  # bytes, measured with rocprofv3 --pmc (profiles/decode_b16_l4096_hbm_traffic.md)
 
 
 def parse():
@@ -46,6 +47,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="decoder part: run the greedy steps eagerly (same kernels, no graph "
+                         "replay), e.g. for a per-kernel profile")
     ap.add_argument("--only", choices=["decode", "prefill", "conformer", "sweep", "decoder"],
                     default=None,
                     help="run one part (for profiling); prints that part's numbers only")
@@ -109,19 +113,14 @@ def run_decode(steps: int, warmup: int):
     dpos = DeviceBuffer.from_array(np.ascontiguousarray(pos_all))
     scale = 1.0 / math.sqrt(DH)
 
-    def step(t, evs=None):
+    def step(t):
         pos_ptr = dpos.ptr + t * B * 4
         v = t % n_var
         for l in range(LAYERS):
-            if evs is not None:  # the decode operation: split-K kernel + split merge kernel
-                evs[l][0].record(stream)
-                call("orator_time_next_decode", evs[l][2].handle, evs[l][3].handle)
             # KV append of the new token + attention over pos + 1 keys, one launch (+ merge)
             da.GqaDecodeAttnAppendPaged(qs[v], ks[v], vs[v], kpools[l], vpools[l], tables[l],
                                         max_pages, PAGE, n_pages, pos_ptr, outs, B, HQ, HKV, DH,
                                         scale, stream)
-            if evs is not None:
-                evs[l][1].record(stream)
 
     for t in range(warmup):
         step(t)
@@ -144,21 +143,13 @@ def run_decode(steps: int, warmup: int):
     elapsed_s = max(wall_s, gpu_ms / 1e3)
     value_gbs = step_bytes / elapsed_s / 1e9
 
-    # ---- decode kernel launch durations (events on the launch stream) ----
-    n_kstep = min(steps, 16)
-    evs = [(Event(), Event(), Event(), Event()) for _ in range(LAYERS)]
-    durs, sdurs, kbytes = [], [], []
-    for i in range(n_kstep):
-        t = warmup + steps - n_kstep + i
-        step(t, evs)
-        stream.synchronize()
-        S = L_BASE + t + 1
-        for l in range(LAYERS):
-            durs.append(evs[l][0].elapsed_ms(evs[l][1]))
-            sdurs.append(evs[l][2].elapsed_ms(evs[l][3]))
-            kbytes.append(B * decode_bytes(S, (S + PAGE - 1) // PAGE))
-    avg_ms = float(np.mean(durs))
-    achieved = float(np.mean(kbytes)) / (avg_ms / 1e3) / 1e9
+    # ---- the decode operation's average duration: the HIP events bracketing the timed
+    # region on the launch stream, over its steps * LAYERS back-to-back operations (each the
+    # split-K kernel and its merge; nothing else runs on the stream in between) ----
+    n_ops = steps * LAYERS
+    avg_ms = gpu_ms / n_ops
+    op_bytes = step_bytes / n_ops
+    achieved = op_bytes / (avg_ms / 1e3) / 1e9
 
     # ---- spot parity of the last launch against the oracle (stream 0..1, layer 27) ----
     parity = spot_check(kpools[-1], vpools[-1], tables[-1], max_pages, qs, outs,
@@ -166,8 +157,7 @@ def run_decode(steps: int, warmup: int):
     return {
         "gpu_ms": gpu_ms, "wall_s": wall_s, "ms_per_step": elapsed_s * 1e3 / steps,
         "value_gbs": value_gbs, "kernel_avg_us": avg_ms * 1e3,
-        "split_kernel_avg_us": float(np.mean(sdurs)) * 1e3,
-        "kernel_bytes": float(np.mean(kbytes)), "achieved_gbs": achieved,
+        "kernel_bytes": op_bytes, "achieved_gbs": achieved,
         "max_pages": max_pages, "parity": parity,
     }
 
@@ -258,7 +248,7 @@ def run_conformer(T: int = 717, layers: int = 17, H: int = 8, Dk: int = 64):
             "fp32_reference_order_us_per_layer": round(us_f32, 2)}
 
 
-def run_decoder_e2e(T: int = 2048, new: int = 256):
+def run_decoder_e2e(T: int = 2048, new: int = 256, use_graph: bool = True):
     """the full synthetic Qwen3-ASR text decoder (28 layers, hidden 2048,
     16/8 heads, head_dim 128, SwiGLU 6144, vocab 151936, lm_head tied to embed as
     asr_text_decoder.cu:255-257), random-init bf16 weights, a 2048-row prefill of N(0, 0.02)
@@ -305,12 +295,12 @@ def run_decoder_e2e(T: int = 2048, new: int = 256):
     emb = DeviceBuffer.from_array((0.02 * rng.standard_normal((T, H))).astype(np.float32))
     # warm-up: one prefill and a short greedy run (captures the step graphs)
     dec.Prefill(emb, T)
-    dec.DecodeGreedy(T, 8, -1, -1, ban_steps=3, batch=32)
+    dec.DecodeGreedy(T, 8, -1, -1, ban_steps=3, batch=32, use_graph=use_graph)
     t0 = time.perf_counter()
     dec.Prefill(emb, T)  # synchronises
     prefill_s = time.perf_counter() - t0
     t0 = time.perf_counter()
-    toks = dec.DecodeGreedy(T, new, -1, -1, ban_steps=3, batch=32, use_graph=True)
+    toks = dec.DecodeGreedy(T, new, -1, -1, ban_steps=3, batch=32, use_graph=use_graph)
     decode_s = time.perf_counter() - t0
     bodies = dec.cache_len() - T
     # eager bodies must give the same tokens as the replayed graphs
@@ -331,6 +321,7 @@ def run_decoder_e2e(T: int = 2048, new: int = 256):
             "decode_bytes_per_token": int(w_bytes + kv_bytes),
             "decode_achieved_gbs": round((w_bytes + kv_bytes) * tok_s / 1e9, 1),
             "decode_frac_of_hbm_peak": round((w_bytes + kv_bytes) * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+            "graph_replay": use_graph,
             "graph_equals_eager_first_tokens": [int(t) for t in eager] == [int(t) for t in toks[:n_chk]]}
 
 
@@ -470,11 +461,11 @@ def main():
                 "prefill": lambda: [run_prefill(503, da.PREFILL_BF16),
                                     run_prefill(2048, da.PREFILL_BF16)],
                 "conformer": run_conformer, "sweep": run_decode_sweep,
-                "decoder": run_decoder_e2e}[args.only]()
+                "decoder": lambda: run_decoder_e2e(use_graph=not args.no_graph)}[args.only]()
         print(json.dumps({"only": args.only, "result": part}, default=float))
         return
     dec = run_decode(args.steps, args.warmup)
-    log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value_gbs']:.1f} GB/s; kernel "
+    log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value_gbs']:.1f} GB/s; op "
         f"{dec['kernel_avg_us']:.1f} us avg -> {dec['achieved_gbs']:.1f} GB/s; parity {dec['parity']}")
     from orator_amd import decoder_attn as da
     pre = [run_prefill(503, da.PREFILL_BF16), run_prefill(503, da.PREFILL_FP32),
@@ -511,9 +502,10 @@ def main():
                      # (split + merge kernels) at this workload, S = 4102.
                      "traffic": HBM_TRAFFIC_PER_OP,
                      "traffic_over_algorithmic": round(HBM_TRAFFIC_PER_OP / dec["kernel_bytes"], 3),
-                     "kernel": "gqa_decode = gqa_decode_kernel (split-K) + gqa_decode_combine_kernel",
+                     "kernel": "decode op = gqa_decode_kernel (split-K, 128-key splits) + "
+                               "gqa_decode_combine_kernel (split merge); average over the "
+                               "timed region's back-to-back ops (HIP events on its stream)",
                      "kernel_avg_us": round(dec["kernel_avg_us"], 2),
-                     "split_kernel_avg_us": round(dec["split_kernel_avg_us"], 2),
                      "bytes_per_launch": int(dec["kernel_bytes"])},
         "cpu_baseline": cpu,
         "parity": dec["parity"],

@@ -68,9 +68,11 @@ int orator_event_elapsed_ms(float* ms, void* start, void* stop);
 /* Pre-sizes the library workspace of `stream` (split-K decode partials, rel-pos fp32
  * intermediates) so that later calls do not allocate, e.g. before hipGraph capture. */
 int orator_workspace_reserve(size_t bytes, void* stream);
-/* Measurement hook (this thread): the next decode call records `start` before and `stop`
- * after its split kernel on the launch stream, so that kernel alone can be timed. */
-int orator_time_next_decode(void* start, void* stop);
+/* Measurement hook (this thread; no reference counterpart): the next decode call records the
+ * HIP events `start` before its split kernel, `split_end` after it and `stop` after the split
+ * merge, on the launch stream, so the operation and its split kernel can be timed without
+ * host gaps.  Any event may be NULL. */
+int orator_time_next_decode(void* start, void* split_end, void* stop);
 
 /* ------------------------------------------------------- asr_ops family ---- */
 /* asr_ops::RmsNorm (include/model/asr_ops.cuh:21-25; src/model/asr_ops.cu:21-51,199-204).

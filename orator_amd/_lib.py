@@ -105,7 +105,7 @@ SIGNATURES: dict[str, list] = {
     "orator_event_record": [_p, _p],
     "orator_event_elapsed_ms": [C.POINTER(_f), _p, _p],
     "orator_workspace_reserve": [_sz, _p],
-    "orator_time_next_decode": [_p, _p],
+    "orator_time_next_decode": [_p, _p, _p],
     # asr_ops family
     "orator_rms_norm": [_p, _p, _p, _i, _i, _f, _p],
     "orator_rope_interleaved": [_p, _p, _i, _i, _i, _f],

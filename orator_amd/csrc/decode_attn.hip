@@ -272,11 +272,19 @@ __device__ __forceinline__ void append_key(const float* kn, const float* vn,
   }
 }
 
+// Waves per split workgroup: bf16 splits of 256 / 512 keys give every wave one 32-key
+// chunk (8 / 16 waves); otherwise 4 waves.
+template <int SPLIT, typename KV, int G>
+constexpr int decode_waves() {
+  return (sizeof(KV) == 2 && G <= 2 && SPLIT >= 256 && SPLIT <= 512) ? SPLIT / 32 : 4;
+}
+
 template <int DH, int G, int SPLIT, typename KV>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gqa_decode_kernel(
-    DecodeArgs a) {
+__global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__((
+    amdgpu_waves_per_eu(2))) void gqa_decode_kernel(DecodeArgs a) {
   using CK = Chunk<DH, KV>;
-  constexpr int NW = 4;
+  constexpr int NW = decode_waves<SPLIT, KV, G>();
+  constexpr int NT = 64 * NW;
   constexpr int TPW = SPLIT / NW;  // keys per wave
   constexpr int NG = SPLIT / 16;   // 16-key groups per split
   static_assert(TPW % CK::CH == 0, "a wave covers whole chunks");
@@ -293,7 +301,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   int S = stream_keys(a, b);
   if (S <= 0) {  // no keys: the reference's 1/sum guard yields zeros
     if (split == 0)
-      for (int idx = threadIdx.x; idx < G * DH; idx += 256)
+      for (int idx = threadIdx.x; idx < G * DH; idx += NT)
         a.out[(static_cast<long>(b) * a.Hkv * G + kvh * G) * DH + idx] = 0.0f;
     return;
   }
@@ -437,8 +445,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   }
   __syncthreads();
 
-  // ---- merge the 4 waves; write the split partial (or the output if it is the only split) ----
-  for (int idx = tid; idx < G * DH; idx += 256) {
+  // ---- merge the waves; write the split partial (or the output if it is the only split) ----
+  for (int idx = tid; idx < G * DH; idx += NT) {
     const int g = idx / DH;
     const int d = idx % DH;
     float mx = red_ml[0][g][0];
@@ -466,8 +474,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 }
 
 // Split merge: one workgroup per (stream, q head), after the split kernel; thread d owns
-// output dim d.  Up to 16 splits' maxima, sums and partial rows are loaded together and
-// folded in with an online max, so a stream of <= 16 splits costs one memory round trip.
+// output dim d.  Splits' maxima, sums and partial rows are loaded 16 at a time and folded in
+// with an online max; the next 16 are in flight while the current ones are folded, so the
+// merge costs about one memory round trip however many splits a stream has.
 template <int DH>
 __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, int split_len,
                                                                 int Hq) {
@@ -481,29 +490,46 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
   const long base = bh * a.max_splits;
   const int d = threadIdx.x;
   float M = -INFINITY, L = 0.0f, acc = 0.0f;
-  for (int s0 = 0; s0 < n_splits; s0 += kBatch) {
-    float ms[kBatch], ls[kBatch], os[kBatch];
+  struct Batch {
+    float m[kBatch], l[kBatch], o[kBatch];
+  };
+  auto load = [&](Batch& x, int s0) {
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       const long ps = base + min(s0 + i, n_splits - 1);  // in-range address for every i
-      ms[i] = a.part_ml[ps * 2];
-      ls[i] = a.part_ml[ps * 2 + 1];
-      os[i] = a.part_o[ps * DH + d];
+      x.m[i] = a.part_ml[ps * 2];
+      x.l[i] = a.part_ml[ps * 2 + 1];
+      x.o[i] = a.part_o[ps * DH + d];
     }
+  };
+  auto fold = [&](const Batch& x, int s0) {
     float mx = M;
 #pragma unroll
     for (int i = 0; i < kBatch; ++i)
-      if (s0 + i < n_splits) mx = fmaxf(mx, ms[i]);
+      if (s0 + i < n_splits) mx = fmaxf(mx, x.m[i]);
     const float c_old = M == mx ? 1.0f : fast_exp2(M - mx);
     acc *= c_old;
     L *= c_old;
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      const float w = s0 + i < n_splits ? fast_exp2(ms[i] - mx) : 0.0f;
-      acc = fmaf(w, os[i], acc);
-      L = fmaf(w, ls[i], L);
+      const float w = s0 + i < n_splits ? fast_exp2(x.m[i] - mx) : 0.0f;
+      acc = fmaf(w, x.o[i], acc);
+      L = fmaf(w, x.l[i], L);
     }
     M = mx;
+  };
+  // ping-pong: the next 16 splits' loads are issued before the current 16 are folded
+  Batch A, Bb;
+  load(A, 0);
+  for (int s0 = 0;;) {
+    if (s0 + kBatch < n_splits) load(Bb, s0 + kBatch);
+    fold(A, s0);
+    s0 += kBatch;
+    if (s0 >= n_splits) break;
+    if (s0 + kBatch < n_splits) load(A, s0 + kBatch);
+    fold(Bb, s0);
+    s0 += kBatch;
+    if (s0 >= n_splits) break;
   }
   a.out[bh * DH + d] = acc * (1.0f / L);
 }
@@ -511,16 +537,20 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
 template <int DH, int G, int SPLIT, typename KV>
 int launch_split(const DecodeArgs& args, int B, hipStream_t stream) {
   dim3 grid(args.Hkv, B, args.max_splits);
-  hipEvent_t ev0, ev1;
-  take_timing_events(&ev0, &ev1);
+  hipEvent_t ev0, ev_split, ev1;
+  take_timing_events(&ev0, &ev_split, &ev1);
   if (ev0) (void)hipEventRecord(ev0, stream);
-  hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV>), grid, dim3(256), 0, stream, args);
+  hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV>), grid,
+                     dim3(64 * decode_waves<SPLIT, KV, G>()), 0, stream, args);
   int rc = check_launch("gqa_decode_kernel");
+  if (ev_split) (void)hipEventRecord(ev_split, stream);
+  if (!rc && args.max_splits > 1) {
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(DH), 0,
+                       stream, args, SPLIT, args.Hkv * G);
+    rc = check_launch("gqa_decode_combine_kernel");
+  }
   if (ev1) (void)hipEventRecord(ev1, stream);
-  if (rc || args.max_splits <= 1) return rc;
-  hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(DH), 0, stream,
-                     args, SPLIT, args.Hkv * G);
-  return check_launch("gqa_decode_combine_kernel");
+  return rc;
 }
 
 template <int DH, int G, typename KV>
@@ -567,8 +597,9 @@ int split_override() {
 // ahead of 256 (2 waves/SIMD) on every configs[2] case: B = 16 at 1K/2K/4K keys by 4-5%, a
 // single stream by 6-23%.  G = 4 keeps 4 heads of state per lane and runs 256-key splits.
 int choose_split(int /*B*/, int /*Hkv*/, int G, int /*capacity*/) {
+  if (G == 4) return 256;  // the only G = 4 instantiation (launch_dh_g)
   if (split_override()) return split_override();
-  return G == 4 ? 256 : 128;
+  return 128;
 }
 
 size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity) {
@@ -605,9 +636,9 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   }
   const int split = choose_split(p.B, p.Hkv, G, p.capacity);
   const int max_splits = (p.capacity + split - 1) / split;
+  if (max_splits > 1024) return fail(ORATOR_ERR_CAPACITY, "gqa_decode: more than 1024 splits");
   const size_t part_o = static_cast<size_t>(p.B) * p.Hq * max_splits * p.Dh * sizeof(float);
   const size_t part_ml = static_cast<size_t>(p.B) * p.Hq * max_splits * 2 * sizeof(float);
-  if (max_splits > 1024) return fail(ORATOR_ERR_CAPACITY, "gqa_decode: more than 1024 splits");
   char* ws = static_cast<char*>(workspace(stream, part_o + part_ml, 0));
   if (!ws) return ORATOR_ERR_HIP;
 

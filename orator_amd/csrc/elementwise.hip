@@ -200,12 +200,22 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(const float* __restr
   __shared__ int sidx[256];
   float best = -1e30f;
   int bi = 0;
-  for (int g = 0; g < parts; ++g) {
-    const float v = pval[g * 256 + threadIdx.x];
-    if (v > best) {
-      best = v;
-      bi = pidx[g * 256 + threadIdx.x];
+  // 16 ranges' candidates are loaded together, then folded in range order
+  for (int g0 = 0; g0 < parts; g0 += 16) {
+    float v[16];
+    int ix[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int g = min(g0 + u, parts - 1);
+      v[u] = pval[g * 256 + threadIdx.x];
+      ix[u] = pidx[g * 256 + threadIdx.x];
     }
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (g0 + u < parts && v[u] > best) {
+        best = v[u];
+        bi = ix[u];
+      }
   }
   sval[threadIdx.x] = best;
   sidx[threadIdx.x] = bi;

@@ -50,8 +50,9 @@ int launch_argmax_banned(const float* logits, int n, int ban0, int ban1, int* ou
 int device_cu_count();
 
 // Optional measurement hook: when set, the next decode launch records `start` right before
-// and `stop` right after its split kernel (on the launch stream), then clears the hook.
-void take_timing_events(hipEvent_t* start, hipEvent_t* stop);
+// its split kernel, `split_end` right after it and `stop` after its split merge (on the
+// launch stream), then clears the hook.  Any of them may be null.
+void take_timing_events(hipEvent_t* start, hipEvent_t* split_end, hipEvent_t* stop);
 
 // ---- launchers (defined in the .hip files) ----
 struct DecodeProblem {

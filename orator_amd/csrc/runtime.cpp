@@ -22,13 +22,14 @@ struct Block {
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Block> g_ws;
-thread_local hipEvent_t g_ev_start = nullptr, g_ev_stop = nullptr;
+thread_local hipEvent_t g_ev_start = nullptr, g_ev_split = nullptr, g_ev_stop = nullptr;
 }  // namespace
 
-void take_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+void take_timing_events(hipEvent_t* start, hipEvent_t* split_end, hipEvent_t* stop) {
   *start = g_ev_start;
+  *split_end = g_ev_split;
   *stop = g_ev_stop;
-  g_ev_start = g_ev_stop = nullptr;
+  g_ev_start = g_ev_split = g_ev_stop = nullptr;
 }
 
 int fail(int code, const std::string& msg) {
@@ -201,8 +202,9 @@ int orator_build_pos_emb(float* pe, int T, int d_model) {
   return ORATOR_OK;
 }
 
-int orator_time_next_decode(void* start, void* stop) {
+int orator_time_next_decode(void* start, void* split_end, void* stop) {
   orator_hip::g_ev_start = static_cast<hipEvent_t>(start);
+  orator_hip::g_ev_split = static_cast<hipEvent_t>(split_end);
   orator_hip::g_ev_stop = static_cast<hipEvent_t>(stop);
   return ORATOR_OK;
 }
