@@ -37,7 +37,11 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
 
 LAYERS, B, HQ, HKV, DH, L_BASE, PAGE = 28, 16, 16, 8, 128, 4096, 16
-HBM_TRAFFIC_PER_OP = 277.4e6  # bytes, measured with rocprofv3 --pmc (profiles/decode_b16_l4096_hbm_traffic.md)
+# HBM bytes per decode op measured with rocprofv3 --pmc at S = 4102 (FETCH_SIZE x 1.994 KiB +
+# WRITE_SIZE KiB, profiles/decode_b16_l4096_hbm_traffic.md) and the algorithmic bytes of the
+# same op, for the traffic / algorithmic ratio
+HBM_TRAFFIC_PER_OP = 277.6e6
+ALGORITHMIC_AT_TRAFFIC = 269.1e6
 
 
 def parse():
@@ -501,7 +505,7 @@ def main():
                      # rocprofv3 FETCH_SIZE x 1.993 + WRITE_SIZE x 1.0 KiB per decode op
                      # (split + merge kernels) at this workload, S = 4102.
                      "traffic": HBM_TRAFFIC_PER_OP,
-                     "traffic_over_algorithmic": round(HBM_TRAFFIC_PER_OP / dec["kernel_bytes"], 3),
+                     "traffic_over_algorithmic": round(HBM_TRAFFIC_PER_OP / ALGORITHMIC_AT_TRAFFIC, 3),
                      "kernel": "decode op = gqa_decode_kernel (split-K, 128-key splits) + "
                                "gqa_decode_combine_kernel (split merge); average over the "
                                "timed region's back-to-back ops (HIP events on its stream)",
