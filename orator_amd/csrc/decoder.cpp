@@ -181,8 +181,9 @@ struct Decoder {
 
   // One-token forward of sx at the device position spos (asr_text_decoder.cu:360-455).
   // Each projection is one fused GEMV that builds its bf16 input row from the fp32 producer
-  // (RmsNorm -> cast, cast, SwiGLU -> cast) and the o / down projections add into the
-  // residual stream in their store: per layer 6 launches instead of the reference's 16.
+  // (RmsNorm -> cast, or cast); gate|up stores silu(gate) * up directly, and the o / down
+  // projections add into the residual stream in their store: per layer 6 launches instead
+  // of the reference's 16.
   int decode_forward(hipStream_t s) {
     const int H = c.hidden_size, I = c.intermediate_size, Hq = c.num_q_heads,
               Hkv = c.num_kv_heads, Dh = c.head_dim;
@@ -201,10 +202,10 @@ struct Decoder {
           (rc = orator_gqa_decode(dq, kc[li], vc[li], sattn, Hq, Hkv, Dh, spos, c.max_seq_len,
                                   scale(), s)) ||
           (rc = launch_gemv_fused(kGemvInF32, sattn, nullptr, 0.0f, L.o_w, sx, Qd(), H, true, s)) ||
-          (rc = launch_gemv_fused(kGemvInRmsNorm, sx, L.post_ln, eps, L.gateup_w, sgateup, H,
-                                  2 * I, false, s)) ||
-          (rc = launch_gemv_fused(kGemvInSwiglu, sgateup, sgateup + I, 0.0f, L.down_w, sx, I, H,
-                                  true, s));
+          (rc = launch_gemv_fused(kGemvInRmsNorm, sx, L.post_ln, eps, L.gateup_w, sgateup, H, I,
+                                  false, s, /*pair=*/true)) ||
+          (rc = launch_gemv_fused(kGemvInF32, sgateup, nullptr, 0.0f, L.down_w, sx, I, H, true,
+                                  s));
     }
     if (rc) return rc;
     return launch_gemv_fused(kGemvInRmsNorm, sx, final_norm, eps, lm_head, logits, H,

@@ -34,11 +34,13 @@ inline int ilog2_exact(int v) {
 }
 
 // Decode-step GEMV over an fp32 producer (linear.hip): mode selects how the bf16 input row is
-// built (cast, RMSNorm with gain `aux`, SwiGLU with up = `aux`); accumulate adds into out.
+// built (cast, RMSNorm with gain `aux`, SwiGLU with up = `aux`); accumulate adds into out;
+// pair reads 2N weight rows (gate | up) and stores silu(gate) * up for N outputs.
 enum { kGemvInF32 = 1, kGemvInRmsNorm = 2, kGemvInSwiglu = 3 };
 constexpr int kFusedMaxK = 8192;
 int launch_gemv_fused(int mode, const float* x, const float* aux, float eps, const uint16_t* W,
-                      float* out, int K, int N, bool accumulate, hipStream_t s);
+                      float* out, int K, int N, bool accumulate, hipStream_t s,
+                      bool pair = false);
 
 // ArgmaxBanned with caller-provided scratch of argmax_scratch_bytes(n) bytes (0: none
 // needed, one workgroup does it).

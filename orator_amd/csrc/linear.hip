@@ -96,33 +96,39 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_bf16_kernel(
 //   kGemvInRmsNorm  xb = bf16(x * rsqrt(mean(x^2) + eps) * w)     (RmsNorm + F32ToBf16)
 //   kGemvInSwiglu   xb = bf16(silu(g) * u), g = x, u = aux        (SwiGLU + F32ToBf16)
 // so one launch replaces three of asr_text_decoder.cu:398-429; ACC folds the residual add
-// (AddResidualKernel) into the store.  The per-element arithmetic is the standalone
-// kernels'; only the order of the RMSNorm sum of squares differs.  The first batch of weight
-// loads is issued before the row is built so the prologue hides under the HBM latency; the
-// k loop then ping-pongs two register batches of kFusedU 16-byte chunks per row.
-constexpr int kFusedU = 4;
-
-template <int MODE, int R, bool ACC>
+// (AddResidualKernel) into the store.  PAIR computes the fused gate|up projection's rows n and
+// N + n in the same wave and stores silu(gate) * up (the SwiGLU that follows it, :424), N
+// outputs from 2N weight rows.  The per-element arithmetic is the standalone kernels'; only
+// the order of the RMSNorm sum of squares differs.  The first batch of weight loads (U
+// 16-byte chunks per lane and row: U = 4 holds a 2048-wide row, 12 a 6144-wide one) is
+// issued before the row is built, so the prologue hides under the HBM latency; longer rows
+// ping-pong two batches.
+template <int MODE, int R, bool ACC, int U, bool PAIR>
 __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict__ x,
                                                          const float* __restrict__ aux, float eps,
                                                          const uint16_t* __restrict__ W,
                                                          float* __restrict__ out, int K, int N) {
 #pragma clang fp contract(off)
+  constexpr int RO = PAIR ? R / 2 : R;  // outputs per wave
+  static_assert(!PAIR || R % 2 == 0, "paired rows");
   __shared__ __align__(16) uint16_t xs[kFusedMaxK];
   __shared__ float red[4];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int row0 = (blockIdx.x * 4 + wave) * R;
+  const int row0 = (blockIdx.x * 4 + wave) * RO;
   const int nchunk = K >> 3;
   const u32x4_t* wr[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-    wr[r] = reinterpret_cast<const u32x4_t*>(W + static_cast<long>(min(row0 + r, N - 1)) * K);
-  u32x4_t A[kFusedU][R], Bb[kFusedU][R];
-  auto load = [&](u32x4_t(&dst)[kFusedU][R], int base) {
+  for (int r = 0; r < R; ++r) {
+    const int o = min(row0 + (r % RO), N - 1);
+    const long row = PAIR && r >= RO ? static_cast<long>(N) + o : o;
+    wr[r] = reinterpret_cast<const u32x4_t*>(W + row * K);
+  }
+  u32x4_t A[U][R], Bb[U][R];
+  auto load = [&](u32x4_t(&dst)[U][R], int base) {
 #pragma unroll
-    for (int u = 0; u < kFusedU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int c = base + 64 * u + lane;
 #pragma unroll
       for (int r = 0; r < R; ++r)
@@ -174,9 +180,9 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict
 
   float acc[R] = {};
   const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(xs);
-  auto comp = [&](const u32x4_t(&src)[kFusedU][R], int base) {
+  auto comp = [&](const u32x4_t(&src)[U][R], int base) {
 #pragma unroll
-    for (int u = 0; u < kFusedU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int c = base + 64 * u + lane;
       if (c < nchunk) {
         const u32x4_t xx = xv[c];
@@ -185,7 +191,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict
       }
     }
   };
-  constexpr int kStep = 64 * kFusedU;
+  constexpr int kStep = 64 * U;
   int base = 0;
   while (true) {
     if (base + kStep < nchunk) load(Bb, base + kStep);
@@ -199,33 +205,48 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-  if (lane < R && row0 + lane < N) {
-    float v = acc[0];
+  if (lane < RO && row0 + lane < N) {
+    float v = acc[0], up = PAIR ? acc[RO] : 0.0f;
 #pragma unroll
-    for (int r = 1; r < R; ++r)
-      if (lane == r) v = acc[r];
+    for (int r = 1; r < RO; ++r)
+      if (lane == r) {
+        v = acc[r];
+        if constexpr (PAIR) up = acc[RO + r];
+      }
+    if constexpr (PAIR) v = (v / (1.0f + expf(-v))) * up;
     float* o = out + row0 + lane;
     if constexpr (ACC) v = *o + v;
     *o = v;
   }
 }
 
-template <int MODE, bool ACC>
-int launch_fused_mode(const float* x, const float* aux, float eps, const uint16_t* W, float* out,
-                      int K, int N, hipStream_t s) {
+template <int MODE, bool ACC, int U>
+int launch_fused_u(const float* x, const float* aux, float eps, const uint16_t* W, float* out,
+                   int K, int N, bool pair, hipStream_t s) {
   // rows per wave: enough waves to cover the chip for small N, fewer input-row rebuilds
   // (one per workgroup) for the vocabulary-sized projection
-  if (N >= 32768) {
-    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 4, ACC>), dim3((N + 15) / 16), dim3(256), 0, s, x,
-                       aux, eps, W, out, K, N);
+  if (pair) {
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC, U, true>), dim3((N + 3) / 4), dim3(256),
+                       0, s, x, aux, eps, W, out, K, N);
+  } else if (N >= 32768) {
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 4, ACC, U, false>), dim3((N + 15) / 16),
+                       dim3(256), 0, s, x, aux, eps, W, out, K, N);
   } else if (N >= 8192) {
-    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC>), dim3((N + 7) / 8), dim3(256), 0, s, x,
-                       aux, eps, W, out, K, N);
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC, U, false>), dim3((N + 7) / 8), dim3(256),
+                       0, s, x, aux, eps, W, out, K, N);
   } else {
-    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 1, ACC>), dim3((N + 3) / 4), dim3(256), 0, s, x,
-                       aux, eps, W, out, K, N);
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 1, ACC, U, false>), dim3((N + 3) / 4), dim3(256),
+                       0, s, x, aux, eps, W, out, K, N);
   }
   return check_launch("gemv_fused_kernel");
+}
+
+template <int MODE, bool ACC>
+int launch_fused_mode(const float* x, const float* aux, float eps, const uint16_t* W, float* out,
+                      int K, int N, bool pair, hipStream_t s) {
+  // one batch per row where it fits: K <= 2048 -> 4 chunks per lane, else 12 (K <= 6144)
+  if (K > 2048) return launch_fused_u<MODE, ACC, 12>(x, aux, eps, W, out, K, N, pair, s);
+  return launch_fused_u<MODE, ACC, 4>(x, aux, eps, W, out, K, N, pair, s);
 }
 
 // ------------------------------------------------------------------- GEMM (M > 1) ----
@@ -337,7 +358,7 @@ int launch_bf16_gemm(const uint16_t* in, const uint16_t* W, const float* bias, f
 }
 
 int launch_gemv_fused(int mode, const float* x, const float* aux, float eps, const uint16_t* W,
-                      float* out, int K, int N, bool accumulate, hipStream_t s) {
+                      float* out, int K, int N, bool accumulate, hipStream_t s, bool pair) {
   if (K <= 0 || N <= 0) return ORATOR_OK;
   if (!x || !W || !out || (mode != kGemvInF32 && !aux))
     return fail(ORATOR_ERR_INVALID, "gemv_fused: null pointer");
@@ -348,14 +369,16 @@ int launch_gemv_fused(int mode, const float* x, const float* aux, float eps, con
     return fail(ORATOR_ERR_INVALID, "gemv_fused: x, aux and W must be 16-byte aligned");
   switch (mode) {
     case kGemvInF32:
-      return accumulate ? launch_fused_mode<kGemvInF32, true>(x, aux, eps, W, out, K, N, s)
-                        : launch_fused_mode<kGemvInF32, false>(x, aux, eps, W, out, K, N, s);
+      return accumulate ? launch_fused_mode<kGemvInF32, true>(x, aux, eps, W, out, K, N, pair, s)
+                        : launch_fused_mode<kGemvInF32, false>(x, aux, eps, W, out, K, N, pair, s);
     case kGemvInRmsNorm:
-      return accumulate ? launch_fused_mode<kGemvInRmsNorm, true>(x, aux, eps, W, out, K, N, s)
-                        : launch_fused_mode<kGemvInRmsNorm, false>(x, aux, eps, W, out, K, N, s);
+      return accumulate
+                 ? launch_fused_mode<kGemvInRmsNorm, true>(x, aux, eps, W, out, K, N, pair, s)
+                 : launch_fused_mode<kGemvInRmsNorm, false>(x, aux, eps, W, out, K, N, pair, s);
     case kGemvInSwiglu:
-      return accumulate ? launch_fused_mode<kGemvInSwiglu, true>(x, aux, eps, W, out, K, N, s)
-                        : launch_fused_mode<kGemvInSwiglu, false>(x, aux, eps, W, out, K, N, s);
+      return accumulate
+                 ? launch_fused_mode<kGemvInSwiglu, true>(x, aux, eps, W, out, K, N, pair, s)
+                 : launch_fused_mode<kGemvInSwiglu, false>(x, aux, eps, W, out, K, N, pair, s);
     default:
       return fail(ORATOR_ERR_INVALID, "gemv_fused: unknown input mode");
   }
