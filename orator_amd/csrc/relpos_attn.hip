@@ -175,9 +175,11 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kRpDk = 64;
-constexpr int kRpWaves = 4;
-constexpr int kVtRow = 32 + 8;   // V^T tile row (halves): 80 bytes
-constexpr int kRtRow = 64 + 1;   // R^T row (floats)
+constexpr int kRpWaves = 8;
+constexpr int kVRowH = 64 + 32;  // row-major V tile row (halves): 192 bytes, so the 4 rows
+                                 // of a half-wave's transposing read start 48 banks apart
+constexpr int kRtRow = 64 + 2;   // R^T row (floats): the diagonal band reads [c][jl - c + 31]
+                                 // then fall on distinct banks across the 32 columns
 
 __device__ __forceinline__ f16x8_t as_f16x8(uint4 u) { return __builtin_bit_cast(f16x8_t, u); }
 
@@ -216,6 +218,17 @@ __device__ __forceinline__ void load8_f(const IN* p, float (&x)[8]) {
   }
 }
 
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element (i & 3) of the
+// 8 bytes addressed by lane 4k + (i >> 2), k = 0..3; with lane s pointing at row r0 + (s >> 2),
+// columns c0 + 4 (s & 3) of a row-major 16-bit tile, lane i gets column c0 + i of rows
+// r0 .. r0 + 3.
+typedef short rp_s16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) rp_s16x4_t lds_s16x4_t;
+  const rp_s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
 struct RelPosArgs {
   const void *q, *k, *v, *p;
   const float *u, *vb;
@@ -225,11 +238,13 @@ struct RelPosArgs {
 };
 
 template <typename IN>
-__global__ __launch_bounds__(256) void relpos_fused_kernel(RelPosArgs a) {
-  __shared__ uint16_t vt_lds[kRpWaves][kRpDk][kVtRow];
+__global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs a) {
+  __shared__ __align__(16) uint16_t v_lds[kRpWaves][32][kVRowH];
+  // R^T during the key loop, then the waves' partial outputs [wave][dim][query] for the merge
   __shared__ float rt_lds[kRpWaves][32][kRtRow];
   __shared__ float mo_lds[kRpWaves][2][32];
-  __shared__ float o_lds[kRpWaves][kRpDk][33];
+  static_assert(kRpDk * 33 <= 32 * kRtRow, "the merge area fits a wave's R^T area");
+  auto o_lds = [&](int w, int d, int c) -> float& { return (&rt_lds[w][0][0])[d * 33 + c]; };
 
   const int h = blockIdx.x % a.H;
   const int i0 = (blockIdx.x / a.H) * 32;
@@ -272,40 +287,56 @@ __global__ __launch_bounds__(256) void relpos_fused_kernel(RelPosArgs a) {
   const int n_tiles = (a.valid + 31) / 32;
   const int P = 2 * T - 1;
 
-  for (int n = wave; n < n_tiles; n += kRpWaves) {
+  // One tile's global operands: V rows (for the V LDS copy), K and the two P windows in
+  // MFMA A layout (zeros outside [0, T) / [0, P)).  The next tile's operands are loaded
+  // before the current one is processed.
+  struct Tile {
+    uint4 v[4], k[4], p0[4], p1[4];
+  };
+  const int dcv = lane & 7, rv = lane >> 3;
+  auto load_tile = [&](Tile& t, int n) {
     const int j0 = 32 * n;
-    wave_lds_sync();  // the previous tile's LDS reads precede this tile's writes
-    // V^T tile -> wave-private LDS (8 b16 stores per 16-byte row piece)
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int key = 8 * it + (lane >> 3), dc = lane & 7;
-      const int j = j0 + key;
-      const uint4 w = j < T ? load8_h(vp + j * rs + h * kRpDk + 8 * dc) : make_uint4(0, 0, 0, 0);
-      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt_lds[wave][8 * dc + 2 * e][key] = static_cast<uint16_t>(ws[e] & 0xffffu);
-        vt_lds[wave][8 * dc + 2 * e + 1][key] = static_cast<uint16_t>(ws[e] >> 16);
-      }
+      const int j = j0 + 8 * it + rv;
+      t.v[it] = j < T ? load8_h(vp + j * rs + h * kRpDk + 8 * dcv) : make_uint4(0, 0, 0, 0);
     }
-    // AC^T and R = P_window (q + v)^T
-    f32x16_t s, r0, r1;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) s[e] = r0[e] = r1[e] = 0.0f;
     const int jk = j0 + col;
     const int base = T - 1 - (i0 + 31) + j0;
     const int pr0 = base + col, pr1 = base + 32 + col;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int d0 = 16 * ks + 8 * h2;
-      const uint4 ka = jk < T ? load8_h(kp + jk * rs + h * kRpDk + d0) : make_uint4(0, 0, 0, 0);
-      const uint4 pa0 = (pr0 >= 0 && pr0 < P) ? load8_h(pp + static_cast<long>(pr0) * rs + h * kRpDk + d0)
-                                             : make_uint4(0, 0, 0, 0);
-      const uint4 pa1 = (pr1 >= 0 && pr1 < P) ? load8_h(pp + static_cast<long>(pr1) * rs + h * kRpDk + d0)
-                                             : make_uint4(0, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(ka), as_f16x8(qu[ks]), s, 0, 0, 0);
-      r0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(pa0), as_f16x8(qv[ks]), r0, 0, 0, 0);
-      r1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(pa1), as_f16x8(qv[ks]), r1, 0, 0, 0);
+      t.k[ks] = jk < T ? load8_h(kp + jk * rs + h * kRpDk + d0) : make_uint4(0, 0, 0, 0);
+      t.p0[ks] = (pr0 >= 0 && pr0 < P) ? load8_h(pp + static_cast<long>(pr0) * rs + h * kRpDk + d0)
+                                      : make_uint4(0, 0, 0, 0);
+      t.p1[ks] = (pr1 >= 0 && pr1 < P) ? load8_h(pp + static_cast<long>(pr1) * rs + h * kRpDk + d0)
+                                      : make_uint4(0, 0, 0, 0);
+    }
+  };
+  const int tg = lane >> 4, ts = lane & 15;
+  const uint16_t* vsrc0 = &v_lds[wave][4 * (tg >> 1) + (ts >> 2)][16 * (tg & 1) + 4 * (ts & 3)];
+  // tile n + W's operands are in flight while tile n is processed
+  Tile cur, nxt;
+  if (wave < n_tiles) load_tile(cur, wave);
+  for (int n = wave; n < n_tiles; n += kRpWaves) {
+    if (n + kRpWaves < n_tiles) load_tile(nxt, n + kRpWaves);
+    const int j0 = 32 * n;
+    wave_lds_sync();  // the previous tile's LDS reads precede this tile's writes
+    // V tile -> wave-private LDS, row-major (one 16-byte store per row piece); the PV
+    // operand V^T is read back with transposing reads
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+      *reinterpret_cast<uint4*>(&v_lds[wave][8 * it + rv][8 * dcv]) = cur.v[it];
+    // AC^T and R = P_window (q + v)^T
+    f32x16_t s, r0, r1;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = r0[e] = r1[e] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(cur.k[ks]), as_f16x8(qu[ks]), s, 0, 0, 0);
+      r0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(cur.p0[ks]), as_f16x8(qv[ks]), r0, 0, 0, 0);
+      r1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(cur.p1[ks]), as_f16x8(qv[ks]), r1, 0, 0, 0);
     }
     // R^T -> LDS; the lane's accumulator rows are 8i + 4*h2 + j (+32 for r1), column = col
 #pragma unroll
@@ -314,7 +345,7 @@ __global__ __launch_bounds__(256) void relpos_fused_kernel(RelPosArgs a) {
       rt_lds[wave][col][rr] = r0[e];
       rt_lds[wave][col][32 + rr] = r1[e];
     }
-    wave_lds_sync();  // R^T and V^T written by all lanes before any lane reads them
+    wave_lds_sync();  // R^T and V written by all lanes before any lane reads them
     // scores: (AC + BD) * scale, key mask j >= valid, padding query columns masked
     float tmax = -INFINITY;
 #pragma unroll
@@ -348,16 +379,20 @@ __global__ __launch_bounds__(256) void relpos_fused_kernel(RelPosArgs a) {
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+    // A operand of O^T += V^T P^T: row = dim 32 dt + col, k = keys 16 st + 4 h2 + 8 (e / 4) +
+    // e % 4, by ds_read_b64_tr_b16 of the row-major tile (16-lane group g covers dims
+    // 16 (g & 1) .. of the 32-dim block and keys 4 (g >> 1) .., +8 for the second half)
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
-        const uint16_t* vr = &vt_lds[wave][32 * dt + col][16 * st + 4 * h2];
-        const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
-        const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
+        const uint16_t* vsrc = vsrc0 + 16 * st * kVRowH + 32 * dt;
+        const uint2 v0 = lds_read_tr16(vsrc);
+        const uint2 v1 = lds_read_tr16(vsrc + 8 * kVRowH);
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(make_uint4(v0.x, v0.y, v1.x, v1.y)),
                                                        as_f16x8(pk[st]), o[dt], 0, 0, 0);
       }
+    cur = nxt;
   }
 
   // ---- merge the waves' partial softmax states ----
@@ -370,9 +405,9 @@ __global__ __launch_bounds__(256) void relpos_fused_kernel(RelPosArgs a) {
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
     for (int e = 0; e < 16; ++e)
-      o_lds[wave][32 * dt + 8 * (e >> 2) + 4 * h2 + (e & 3)][col] = o[dt][e];
+      o_lds(wave, 32 * dt + 8 * (e >> 2) + 4 * h2 + (e & 3), col) = o[dt][e];
   __syncthreads();
-  for (int idx = tid; idx < 32 * kRpDk; idx += 256) {
+  for (int idx = tid; idx < 32 * kRpDk; idx += 64 * kRpWaves) {
     const int c = idx / kRpDk, d = idx % kRpDk;
     const int i = i0 + c;
     if (i >= T) continue;
@@ -384,7 +419,7 @@ __global__ __launch_bounds__(256) void relpos_fused_kernel(RelPosArgs a) {
 #pragma unroll
     for (int w = 0; w < kRpWaves; ++w) {
       const float wt = fast_exp2(mo_lds[w][0][c] - mr);
-      ov = fmaf(wt, o_lds[w][d][c], ov);
+      ov = fmaf(wt, o_lds(w, d, c), ov);
       lv = fmaf(wt, mo_lds[w][1][c], lv);
     }
     a.out[(static_cast<long>(i) * H + h) * kRpDk + d] = lv > 0.0f ? ov / lv : 0.0f;
@@ -409,10 +444,10 @@ int orator_relpos_attention_fast(const void* q, const void* k, const void* v, co
                   scale * 1.4426950408889634f};
   const dim3 grid(((T + 31) / 32) * H);
   if (in_f16)
-    hipLaunchKernelGGL(relpos_fused_kernel<_Float16>, grid, dim3(256), 0,
+    hipLaunchKernelGGL(relpos_fused_kernel<_Float16>, grid, dim3(64 * kRpWaves), 0,
                        static_cast<hipStream_t>(stream), args);
   else
-    hipLaunchKernelGGL(relpos_fused_kernel<float>, grid, dim3(256), 0,
+    hipLaunchKernelGGL(relpos_fused_kernel<float>, grid, dim3(64 * kRpWaves), 0,
                        static_cast<hipStream_t>(stream), args);
   return check_launch("relpos_fused_kernel");
 }
