@@ -474,13 +474,13 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
 }
 
 // Split merge: one workgroup per (stream, q head), after the split kernel; thread d owns
-// output dim d.  Splits' maxima, sums and partial rows are loaded 16 at a time and folded in
-// with an online max; the next 16 are in flight while the current ones are folded, so the
-// merge costs about one memory round trip however many splits a stream has.
+// output dim d.  Splits' maxima, sums and partial rows are loaded 17 at a time and folded in
+// with an online max; the next 17 are in flight while the current ones are folded, so up to
+// 34 splits (4352 keys at 128-key splits) cost one memory round trip.
 template <int DH>
 __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, int split_len,
                                                                 int Hq) {
-  constexpr int kBatch = 16;
+  constexpr int kBatch = 17;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int S = stream_keys(a, b);
