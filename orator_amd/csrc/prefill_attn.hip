@@ -7,9 +7,10 @@
 // Two precisions share the kernel:
 //  * bf16 mode: q (and the softmax weights fed to the PV product) rounded to bf16 -- one
 //    v_mfma_f32_32x32x16_bf16 per product;
-//  * fp32 mode: q carried as three bf16 terms (hi + mid + lo, exact to fp32 rounding) and
-//    the softmax weights as two (hi + lo, ~2^-17 relative); K/V are exact in bf16, so QK is
-//    fp32-exact and PV within ~1e-6 of the fp32 reference, at 2.5x the MFMA work.
+//  * fp32 mode: q and the softmax weights each carried as three bf16 terms (hi + mid + lo,
+//    exact to fp32 rounding for q, ~2^-26 relative for the weights); K/V are exact in bf16,
+//    so QK and PV are fp32-accurate, at 3x the MFMA work.  (Two weight terms, ~2^-17, put
+//    near-zero outputs of long rows at the edge of a 1e-4 relative bound.)
 //
 // Work split.  A workgroup is 8 wave64s: RW query-row waves (32 query columns each) times
 // KG = 8/RW key groups.  Key group g takes the 32-key tiles g, g+KG, g+2KG, ... of the
@@ -41,6 +42,14 @@
 //    loads.
 //  * workgroups are ordered heaviest (latest tokens, most keys) first, and the kv head is
 //    the fastest-varying index, so each kv head's workgroups share an XCD (blockIdx % 8).
+//    With at least two token blocks per CU, workgroup i runs block n-1-i and then block i
+//    (equal key counts per workgroup, one workgroup per CU).
+//  * a contiguous cache's tile rows are plain arithmetic: the loads of a round never wait
+//    on an LDS page-row lookup (which would also drain that round's LDS stores).  Paged
+//    caches look the rows up in LDS.
+//
+// Measured alternative, not kept: feeding the tiles by LDS DMA (global_load_lds_dwordx4
+// into swizzled 3-stage rings, no staging registers) was 7-20% slower at 503-4096 tokens.
 #include <cstdlib>
 
 #include "common.hpp"
@@ -75,6 +84,7 @@ struct PrefillArgs {
   int Tq, Hq, Hkv;
   int capacity;
   int n_tblocks;
+  int paired;             // 1: workgroup i runs token blocks n_tblocks-1-i, then i
   float scale_log2e;      // > 0
 };
 
@@ -158,7 +168,7 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   __shared__ int row_lds[kMaxRowGroups];
 
   const int kvh = blockIdx.x % a.Hkv;
-  const int tblock = a.n_tblocks - 1 - static_cast<int>(blockIdx.x / a.Hkv);
+  const int wi = static_cast<int>(blockIdx.x / a.Hkv);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -169,7 +179,11 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   const int col = lane & 31;  // this lane's query column
   const int pos0 = *a.pos0p;
   GroupTiles& tl = reinterpret_cast<GroupTiles*>(smem)[grp];
+  const bool contiguous = a.page_table == nullptr;  // row of key k is k
 
+  // One token block: keys, tiles, softmax state, output.  Returns after its output is
+  // stored; every thread runs every barrier of it.
+  auto run_block = [&](int tblock) {
   const int t_blk = tblock * BT;
   const int t_end = min(t_blk + BT, a.Tq);
   const int n_keys = min(pos0 + t_end, a.capacity);  // keys [0, n_keys) are needed
@@ -179,8 +193,8 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   // tiles with a key beyond this need the causal / capacity mask
   const int mask_from = min(pos0 + t_blk, n_keys - 1);
 
-  // ---- page rows of the needed keys (16-key groups) ----
-  const int n_rowgroups = (n_keys + 15) >> 4;
+  // ---- page rows of the needed keys (16-key groups; paged caches only) ----
+  const int n_rowgroups = contiguous ? 0 : (n_keys + 15) >> 4;
   for (int gi = tid; gi < n_rowgroups; gi += kThreads) {
     int row = gi << 4;
     if (a.page_table) {
@@ -231,14 +245,16 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   // Row of `key` (clamped to the last needed key, so every load stays in bounds).
   auto row_clamped = [&](int key) -> long {
     key = min(key, n_keys - 1);
-    return static_cast<long>(row_lds[key >> 4] + (key & 15));
+    return contiguous ? key : static_cast<long>(row_lds[key >> 4] + (key & 15));
   };
   auto load_rows = [&](const uint16_t* base, int j, u32x4_t (&r)[NP]) {
     const int k0 = (grp + KG * j) * kBN;  // uniform
     if (k0 + kBN <= n_keys) {
-      // whole tile valid: two 16-row groups with uniform bases
-      const long rg0 = __builtin_amdgcn_readfirstlane(row_lds[k0 >> 4]);
-      const long rg1 = __builtin_amdgcn_readfirstlane(row_lds[(k0 >> 4) + 1]);
+      // whole tile valid: two 16-row groups with uniform bases (no LDS lookup, and so no
+      // wait on this round's LDS stores, for a contiguous cache)
+      const long rg0 = contiguous ? k0 : __builtin_amdgcn_readfirstlane(row_lds[k0 >> 4]);
+      const long rg1 =
+          contiguous ? k0 + 16 : __builtin_amdgcn_readfirstlane(row_lds[(k0 >> 4) + 1]);
       const char* b0 = reinterpret_cast<const char*>(base + rg0 * rs) + lane_off;
       const char* b1 = reinterpret_cast<const char*>(base + rg1 * rs) + lane_off;
 #pragma unroll
@@ -350,31 +366,34 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   // Softmax of tile j (scores s) and O^T += V^T P^T from V buffer `buf` (fp32 mode).
   auto softmax_pv = [&](f32x16_t s, int j, int buf) {
     const float mref = mask_and_rescale(s, j);
-    uint4 phi[2], plo[2];  // B operand per 16-key k-step st: keys 16st + 8(e/4) + 4*h2 + e%4
+    // B operand per 16-key k-step st (keys 16st + 8(e/4) + 4*h2 + e%4), each weight as
+    // hi + mid + lo bf16 terms: both remainders are exact in fp32, so the three terms carry
+    // the fp32 weight to ~2^-26 relative.  One k-step at a time (register pressure).
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(fmaf(s[8 * st + e], c, -mref));
-      uint32_t hw[4], lw[4];
+      uint32_t hw[4], mw[4], lw[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         hw[e] = cvt_bf16x2(pv[2 * e], pv[2 * e + 1]);
-        lw[e] = cvt_bf16x2(pv[2 * e] - bf16_lo(hw[e]), pv[2 * e + 1] - bf16_hi(hw[e]));
+        const float r0 = pv[2 * e] - bf16_lo(hw[e]), r1 = pv[2 * e + 1] - bf16_hi(hw[e]);
+        mw[e] = cvt_bf16x2(r0, r1);
+        lw[e] = cvt_bf16x2(r0 - bf16_lo(mw[e]), r1 - bf16_hi(mw[e]));
         lsum += pv[2 * e] + pv[2 * e + 1];
       }
-      phi[st] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-      plo[st] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    }
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
+      const uint4 phi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      const uint4 pmid = make_uint4(mw[0], mw[1], mw[2], mw[3]);
+      const uint4 plo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
       uint4 vf[4];
       read_vf(buf, st, vf);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         const bf16x8_t va = as_bf16x8(vf[dt]);
-        o[dt] = mfma32(va, as_bf16x8(plo[st]), o[dt]);
-        o[dt] = mfma32(va, as_bf16x8(phi[st]), o[dt]);
+        o[dt] = mfma32(va, as_bf16x8(plo), o[dt]);
+        o[dt] = mfma32(va, as_bf16x8(pmid), o[dt]);
+        o[dt] = mfma32(va, as_bf16x8(phi), o[dt]);
       }
     }
   };
@@ -509,7 +528,7 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
     L += w[g] * mml[((g * RW + rw) * 2 + 1) * 64 + lane];
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  if (!q_valid) return;
+  if (q_valid) {
   float* orow = a.out + (static_cast<long>(tq) * a.Hq + hq) * kDh + 4 * h2;
 #pragma unroll
   for (int d = 0; d < D; ++d) {
@@ -540,11 +559,22 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
       *reinterpret_cast<float4*>(orow + 32 * dt + 8 * i) =
           make_float4(f[4 * i] * inv, f[4 * i + 1] * inv, f[4 * i + 2] * inv, f[4 * i + 3] * inv);
   }
+  }
+  };  // run_block
+
+  // Heaviest blocks first; paired: the heavy block n-1-i, then (after a barrier that frees
+  // the merge area) the light block i, so every workgroup has about the same key count.
+  run_block(a.n_tblocks - 1 - wi);
+  if (a.paired && wi < a.n_tblocks - 1 - wi) {
+    __syncthreads();
+    run_block(wi);
+  }
 }
 
 template <int G, bool PRECISE>
 int launch_rw(const PrefillArgs& args, int rw, hipStream_t stream) {
-  const dim3 grid(args.n_tblocks * args.Hkv);
+  const int n_work = args.paired ? (args.n_tblocks + 1) / 2 : args.n_tblocks;
+  const dim3 grid(n_work * args.Hkv);
   if (rw == 4)
     hipLaunchKernelGGL((gqa_prefill_kernel<G, PRECISE, 4>), grid, dim3(kThreads), 0, stream, args);
   else
@@ -569,6 +599,14 @@ int launch_g(PrefillArgs& args, bool precise, hipStream_t stream) {
   if (rw_override) rw = rw_override;
   const int BT = rw * (32 / G);
   args.n_tblocks = (args.Tq + BT - 1) / BT;
+  // Pairs of blocks (heavy n-1-i with light i) per workgroup once there are at least two
+  // blocks per CU: one workgroup per CU instead of two back to back, and one prologue less.
+  static const int pair_override = [] {
+    const char* e = std::getenv("ORATOR_PREFILL_PAIR");
+    return e ? std::atoi(e) : -1;
+  }();
+  args.paired = static_cast<long>(args.n_tblocks) * args.Hkv >= 2L * (cus > 0 ? cus : 256);
+  if (pair_override == 0 || pair_override == 1) args.paired = pair_override;
   return precise ? launch_rw<G, true>(args, rw, stream) : launch_rw<G, false>(args, rw, stream);
 }
 

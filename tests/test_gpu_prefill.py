@@ -84,30 +84,44 @@ def test_prefill_streaming_split_equals_full():
     assert rel_err(np.concatenate([a, b]), full, FLOOR) <= 2e-6
 
 
+def _check(got, ref, mode):
+    if mode == da.PREFILL_FP32:
+        assert rel_err(got, ref, FLOOR) <= TOL32
+    else:
+        assert np.max(np.abs(got - ref)) <= TOL16
+
+
+MODES = [da.PREFILL_FP32, da.PREFILL_BF16]
+
+
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("T,pos0,cap", [(1, 0, 64), (1, 700, 1024), (37, 1000, 2048),
-                                        (64, 0, 64), (65, 3, 128), (200, 1800, 2048)])
-def test_prefill_offsets_and_ragged(T, pos0, cap):
+                                        (64, 0, 64), (65, 3, 128), (200, 1800, 2048),
+                                        (129, 0, 160), (300, 77, 400)])
+def test_prefill_offsets_and_ragged(T, pos0, cap, mode):
     Hkv, Dh = 8, 128
     q, kc, vc = _layer_inputs(T + pos0, T, pos0, cap=cap)
     ref = orc.gqa_prefill(q, kc, vc, pos0, 1.0 / math.sqrt(Dh), threads=8)
-    say("prefill offsets", T, pos0, cap)
-    got = _run(q, kc, vc, pos0, cap, da.PREFILL_FP32, Hkv)
-    assert rel_err(got, ref, FLOOR) <= TOL32
+    say("prefill offsets", T, pos0, cap, mode)
+    got = _run(q, kc, vc, pos0, cap, mode, Hkv)
+    _check(got, ref, mode)
     if T == 1 and pos0 == 0:  # one key: the output is v0
         np.testing.assert_allclose(got[0], np.repeat(orc.from_bf16(vc[0]), 2, axis=0), atol=1e-6)
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 4)])
-def test_prefill_group_variants(Hq, Hkv):
+def test_prefill_group_variants(Hq, Hkv, mode):
     T, pos0, Dh = 150, 20, 128
     q, kc, vc = _layer_inputs(Hq * 10 + Hkv, T, pos0, Hq=Hq, Hkv=Hkv)
     ref = orc.gqa_prefill(q, kc, vc, pos0, 1.0 / math.sqrt(Dh), threads=8)
-    say("prefill groups", Hq, Hkv)
-    got = _run(q, kc, vc, pos0, pos0 + T, da.PREFILL_FP32, Hkv)
-    assert rel_err(got, ref, FLOOR) <= TOL32
+    say("prefill groups", Hq, Hkv, mode)
+    got = _run(q, kc, vc, pos0, pos0 + T, mode, Hkv)
+    _check(got, ref, mode)
 
 
-def test_prefill_paged_matches_contiguous():
+@pytest.mark.parametrize("mode", MODES)
+def test_prefill_paged_matches_contiguous(mode):
     T, pos0, Hkv, Dh, ps = 300, 100, 8, 128, 16
     q, kc, vc = _layer_inputs(11, T, pos0, cap=400)
     n_pages = 400 // ps
@@ -116,9 +130,9 @@ def test_prefill_paged_matches_contiguous():
     vp = np.empty_like(kp)
     kp[perm] = kc.reshape(n_pages, ps, Hkv, Dh)
     vp[perm] = vc.reshape(n_pages, ps, Hkv, Dh)
-    say("prefill paged")
-    a = _run(q, kc, vc, pos0, 400, da.PREFILL_FP32, Hkv)
-    b = _run(q, kc, vc, pos0, 400, da.PREFILL_FP32, Hkv, page=(kp, vp, perm, ps))
+    say("prefill paged", mode)
+    a = _run(q, kc, vc, pos0, 400, mode, Hkv)
+    b = _run(q, kc, vc, pos0, 400, mode, Hkv, page=(kp, vp, perm, ps))
     np.testing.assert_array_equal(a, b)
 
 
