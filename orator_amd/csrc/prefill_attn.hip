@@ -448,24 +448,25 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // MFMA
     };
-    // ---- prologue: K0, V0, K1 into LDS, S(0); the first DIST register sets in flight ----
+    // ---- prologue: K0, V0, K1 into LDS, S(0); the first DIST register sets are loaded in
+    // the same burst (one memory round trip before the first round, not two) ----
     {
-      u32x4_t k1[NP];
-      load_k(0, kr[0]);
-      load_v(0, vr[0]);
+      u32x4_t k0[NP], v0[NP], k1[NP];
+      load_k(0, k0);
+      load_v(0, v0);
       load_k(1, k1);
-      store_k(0, kr[0]);
-      store_v(0, vr[0], 0);
+#pragma unroll
+      for (int d = 0; d < DIST; ++d) {
+        load_k(2 + d, kr[d]);
+        load_v(1 + d, vr[d]);
+      }
+      store_k(0, k0);
+      store_v(0, v0, 0);
       store_k(1, k1);
     }
     lds_barrier();
     f32x16_t s0 = qk(0), s1;
-#pragma unroll
-    for (int d = 0; d < DIST; ++d) {
-      load_k(2 + d, kr[d]);
-      load_v(1 + d, vr[d]);
-    }
-    lds_barrier();
+    lds_barrier();  // K buffer 0 is refilled in round 0
     int j = 0;
     for (; j + 1 < n_rounds; j += 2) {
       round.template operator()<0>(j, s0, s1);
