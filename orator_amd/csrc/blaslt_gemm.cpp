@@ -1,0 +1,116 @@
+// Plain bf16 GEMMs of the prefill projections on hipBLASLt (M > 1).
+//
+// LaunchBf16Gemm (include/model/gemm.cuh:384-501) computes out[M][N] = act(in[M][K] W[N][K]^T
+// + bias) in fp32 from bf16 operands.  For prompts the product is a plain GEMM, so it runs on
+// the library's tuned MFMA kernels: the row-major problem is the column-major
+// D[N x M] = op_T(W: K x N, ld K) * op_N(in: K x M, ld K), fp32 compute and output.  The bias
+// and activation, when asked for, follow in one elementwise pass (launch_bias_act), so the
+// activation is this library's own erf GELU / ReLU, not the GEMM library's epilogue.
+//
+// Plans (descriptors + the heuristic's first algorithm) are cached per device and shape.  Only
+// algorithms that need no workspace are taken, so concurrent streams share nothing; a shape
+// with none returns ORATOR_ERR_UNSUPPORTED and the caller runs its own MFMA kernel.
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <cstdlib>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "internal.hpp"
+
+namespace orator_hip {
+namespace {
+
+struct Plan {
+  bool ok = false;
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+};
+
+struct DeviceLt {
+  hipblasLtHandle_t handle = nullptr;
+  bool failed = false;
+  std::map<std::tuple<int, int, int>, Plan> plans;
+};
+
+std::mutex g_lt_mu;
+std::map<int, DeviceLt> g_lt;
+
+bool lt_ok(hipblasStatus_t st) { return st == HIPBLAS_STATUS_SUCCESS; }
+
+// Builds (once) the plan of an M x K x N product; false when the library has none.
+bool make_plan(DeviceLt& d, int M, int K, int N, Plan& p) {
+  const int32_t op_t = HIPBLAS_OP_T, op_n = HIPBLAS_OP_N;
+  if (!lt_ok(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)) ||
+      !lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_t,
+                                             sizeof(op_t))) ||
+      !lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_n,
+                                             sizeof(op_n))) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, K)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, N)))
+    return false;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (!lt_ok(hipblasLtMatmulPreferenceCreate(&pref))) return false;
+  const uint64_t no_ws = 0;
+  hipblasLtMatmulHeuristicResult_t res[4];
+  int n = 0;
+  const bool got =
+      lt_ok(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                  &no_ws, sizeof(no_ws))) &&
+      lt_ok(hipblasLtMatmulAlgoGetHeuristic(d.handle, p.desc, p.la, p.lb, p.lc, p.lc, pref, 4, res,
+                                            &n));
+  (void)hipblasLtMatmulPreferenceDestroy(pref);
+  for (int i = 0; got && i < n; ++i)
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize == 0) {
+      p.algo = res[i].algo;
+      p.ok = true;
+      return true;
+    }
+  return false;
+}
+
+}  // namespace
+
+// Tuning override (read once): ORATOR_GEMM_LIB=0 keeps every M > 1 product on this library's
+// own MFMA GEMM.
+bool bf16_gemm_lib_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("ORATOR_GEMM_LIB");
+    return !(e && std::atoi(e) == 0);
+  }();
+  return on;
+}
+
+int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
+                         hipStream_t stream) {
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  std::lock_guard<std::mutex> lock(g_lt_mu);
+  DeviceLt& d = g_lt[dev];
+  if (d.failed) return ORATOR_ERR_UNSUPPORTED;
+  if (!d.handle && !lt_ok(hipblasLtCreate(&d.handle))) {
+    d.failed = true;
+    d.handle = nullptr;
+    return ORATOR_ERR_UNSUPPORTED;
+  }
+  auto key = std::make_tuple(M, K, N);
+  auto it = d.plans.find(key);
+  if (it == d.plans.end()) {
+    Plan p;
+    make_plan(d, M, K, N, p);
+    it = d.plans.emplace(key, p).first;
+  }
+  Plan& p = it->second;
+  if (!p.ok) return ORATOR_ERR_UNSUPPORTED;
+  const float alpha = 1.0f, beta = 0.0f;
+  const hipblasStatus_t st = hipblasLtMatmul(d.handle, p.desc, &alpha, W, p.la, in, p.lb, &beta,
+                                             out, p.lc, out, p.lc, &p.algo, nullptr, 0, stream);
+  if (!lt_ok(st)) return fail(ORATOR_ERR_HIP, "bf16_gemm: hipblasLtMatmul failed");
+  return ORATOR_OK;
+}
+
+}  // namespace orator_hip

@@ -85,6 +85,14 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
 // Workspace bytes a decode launch over B streams of `capacity` keys needs (split partials).
 size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity);
 
+// bf16 GEMM on hipBLASLt (blaslt_gemm.cpp): out[M][N] = in[M][K] W[N][K]^T, fp32 accumulate
+// and output, no epilogue.  ORATOR_ERR_UNSUPPORTED when the library has no workspace-free
+// plan for the shape (the caller then runs its own kernel).
+constexpr int kLibMinM = 32;  // smaller M stays on the MFMA kernel / GEMV
+bool bf16_gemm_lib_enabled();
+int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
+                         hipStream_t stream);
+
 int launch_sgemm(const float* in, const float* W, const float* bias, float* out, int M, int K,
                  int N, int act, int batch, long stride_in, long stride_w, long stride_out,
                  hipStream_t stream);

@@ -336,6 +336,14 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
   }
 }
 
+// out[m][n] = act(out[m][n] + bias[n]) after a library GEMM.
+__global__ __launch_bounds__(256) void bias_act_kernel(float* __restrict__ out,
+                                                       const float* __restrict__ bias, long n_all,
+                                                       int N, int act) {
+  const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n_all) out[i] = apply_act(out[i] + (bias ? bias[i % N] : 0.0f), act);
+}
+
 int check_linear(const void* in, const uint16_t* W, const float* out, int K, int act,
                  const char* who) {
   if (!in || !W || !out) return fail(ORATOR_ERR_INVALID, std::string(who) + ": null pointer");
@@ -352,6 +360,20 @@ int launch_bf16_gemm(const uint16_t* in, const uint16_t* W, const float* bias, f
                      int K, int N, int act, hipStream_t stream) {
   if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;  // reference no-op
   if (int rc = check_linear(in, W, out, K, act, "bf16_gemm")) return rc;
+  // Prompt-sized products go to the GEMM library (plain fp32-accumulated bf16 GEMM; bias and
+  // activation in one pass after it); small M, and shapes it has no plan for, run the MFMA
+  // kernel below.
+  if (M >= kLibMinM && bf16_gemm_lib_enabled()) {
+    const int rc = launch_bf16_gemm_lib(in, W, out, M, K, N, stream);
+    if (rc == ORATOR_OK) {
+      if (!bias && act == 0) return ORATOR_OK;
+      const long n_all = static_cast<long>(M) * N;
+      hipLaunchKernelGGL(bias_act_kernel, dim3(static_cast<unsigned>((n_all + 255) / 256)),
+                         dim3(256), 0, stream, out, bias, n_all, N, act);
+      return check_launch("bias_act_kernel");
+    }
+    if (rc != ORATOR_ERR_UNSUPPORTED) return rc;
+  }
   const dim3 grid((N + kTN - 1) / kTN, (M + kTM - 1) / kTM);
   hipLaunchKernelGGL(gemm_bf16_kernel, grid, dim3(256), 0, stream, in, W, bias, out, M, K, N, act);
   return check_launch("gemm_bf16_kernel");

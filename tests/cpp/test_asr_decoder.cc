@@ -6,8 +6,8 @@
 //   * Prefill, then PrefillAt in two parts (pos0 = split): cache_len == T, identical argmax,
 //     logits max abs diff <= 0.5 (test_asr_decoder.cc:76-112);
 //   * TruncateCache(split) + PrefillAt of the second part: identical argmax (:114-127);
-// and, for the greedy loop: DecodeGreedy with graph replay == DecodeGreedy eager, token for
-// token, and cache_len == start + tokens run.
+// and, for the greedy loop: DecodeGreedy with graph replay == DecodeGreedy eager after the same
+// single-call prefill, token for token, and cache_len == start + tokens run.
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
@@ -141,6 +141,10 @@ int main() {
                   our_am);
       ++failures;
     }
+    // Graph replay against eager launches from the same history: both decoders prefill the
+    // whole prompt in one call (a split prefill may round the cache differently, since the
+    // projection GEMM of a 60-row prompt and of two 30-row parts need not sum in one order).
+    dec.Prefill(embeds.data(), T);
     const std::vector<int> graph = dec.DecodeGreedy(T, 24, 151645, 151643, 3, 4);
     const int graph_len = dec.cache_len();
     std::printf("  greedy (graph): %zu tokens, cache_len %d\n", graph.size(), graph_len);
