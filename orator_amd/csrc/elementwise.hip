@@ -297,33 +297,28 @@ struct QkvArgs {
   int max_pages, page_shift, capacity;  // paged: capacity = number of pages in the pool
 };
 
-__global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(QkvArgs a) {
+// Row hh of token t (q heads first, then k heads): RmsNorm of the loaded halves x0 = x[lane],
+// x1 = x[lane + 64], RoPE with this lane's (c, s), store; a k row also writes its k and v
+// rows into the cache row of the token's position.
+__device__ __forceinline__ void qkv_row(const QkvArgs& a, int t, int hh, int lane, float c,
+                                        float s, float x0, float x1) {
 #pragma clang fp contract(off)
   constexpr int Dh = 128, half = 64;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int per_token = a.Hq + a.Hkv;
-  if (row >= a.n_tokens * per_token) return;
-  const int t = row / per_token;
-  const int hh = row % per_token;
   const bool is_q = hh < a.Hq;
   const int h = is_q ? hh : hh - a.Hq;
   float* x = is_q ? a.q + t * a.q_stride + static_cast<long>(h) * Dh
                   : a.k + t * a.kv_stride + static_cast<long>(h) * Dh;
   const float* w = is_q ? a.q_norm : a.k_norm;
-  const float x0 = x[lane], x1 = x[lane + half];
   const float ss = wave_sum(x0 * x0 + x1 * x1);
   const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss / Dh + a.eps)));
   const float n0 = x0 * inv * w[lane], n1 = x1 * inv * w[lane + half];
-  const int pos = a.positions[t];
-  float c, s;
-  rope_cs(static_cast<float>(pos), a.theta, lane, Dh, &c, &s);
   const float r0 = n0 * c - n1 * s;
   const float r1 = n1 * c + n0 * s;
   x[lane] = r0;
   x[lane + half] = r1;
   if (is_q) return;
   // cache row of this token's position
+  const int pos = a.positions[t];
   long crow;
   if (a.page_table) {
     const int b = t / a.tokens_per_stream;
@@ -342,6 +337,57 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(QkvArgs a) {
   a.kpool[dst + lane + half] = f32_to_bf16(r1);
   a.vpool[dst + lane] = f32_to_bf16(vr[lane]);
   a.vpool[dst + lane + half] = f32_to_bf16(vr[lane + half]);
+}
+
+__device__ __forceinline__ const float* qkv_row_ptr(const QkvArgs& a, int t, int hh) {
+  return hh < a.Hq ? a.q + t * a.q_stride + static_cast<long>(hh) * 128
+                   : a.k + t * a.kv_stride + static_cast<long>(hh - a.Hq) * 128;
+}
+
+// Decode-sized calls: one wave per (token, head) row, 4 rows per workgroup.
+__global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(QkvArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int per_token = a.Hq + a.Hkv;
+  if (row >= a.n_tokens * per_token) return;
+  const int t = row / per_token;
+  const int hh = row % per_token;
+  const float* x = qkv_row_ptr(a, t, hh);
+  const float x0 = x[lane], x1 = x[lane + 64];
+  float c, s;
+  rope_cs(static_cast<float>(a.positions[t]), a.theta, lane, 128, &c, &s);
+  qkv_row(a, t, hh, lane, c, s, x0, x1);
+}
+
+// Prompts: one workgroup per token; wave w takes rows w, w+4, ... of the token, forms this
+// lane's RoPE (cos, sin) once for all of them (the fp64 pow/sincos depend only on the
+// position and the lane) and loads kQkvBatch rows before processing them.  Same per-row
+// arithmetic as qk_norm_rope_kv_kernel.
+constexpr int kQkvBatch = 8;
+__global__ __launch_bounds__(256) void qk_norm_rope_kv_token_kernel(QkvArgs a) {
+  const int t = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int per_token = a.Hq + a.Hkv;
+  float c, s;
+  rope_cs(static_cast<float>(a.positions[t]), a.theta, lane, 128, &c, &s);
+  for (int hb = wave; hb < per_token; hb += 4 * kQkvBatch) {
+    float x0[kQkvBatch], x1[kQkvBatch];
+#pragma unroll
+    for (int i = 0; i < kQkvBatch; ++i) {
+      const int hh = hb + 4 * i;
+      if (hh < per_token) {
+        const float* x = qkv_row_ptr(a, t, hh);
+        x0[i] = x[lane];
+        x1[i] = x[lane + 64];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kQkvBatch; ++i) {
+      const int hh = hb + 4 * i;
+      if (hh < per_token) qkv_row(a, t, hh, lane, c, s, x0[i], x1[i]);
+    }
+  }
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -531,9 +577,16 @@ int orator_qk_norm_rope_kv_write(float* q, float* k, const float* v, long q_stri
       return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: page_size must be a power of two");
     a.max_pages = max_pages;
   }
-  const long rows = static_cast<long>(n_tokens) * (Hq + Hkv);
-  hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
+  // Prompts: a workgroup per token (RoPE angles formed once per token and wave); a few
+  // tokens (decode): a wave per row, which spreads the rows over more of the chip.
+  if (n_tokens >= 64) {
+    hipLaunchKernelGGL(qk_norm_rope_kv_token_kernel, dim3(n_tokens), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
+  } else {
+    const long rows = static_cast<long>(n_tokens) * (Hq + Hkv);
+    hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
+  }
   return check_launch("qk_norm_rope_kv_write");
 }
 

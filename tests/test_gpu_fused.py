@@ -86,3 +86,39 @@ def test_fused_decode_layout_paged_streams():
     np.testing.assert_array_equal(got[:, (Hq + Hkv) * Dh:], qkv[:, (Hq + Hkv) * Dh:])  # v untouched
     _bf16_close(down(dkp, kp_ref.shape, np.uint16), kp_ref)
     np.testing.assert_array_equal(down(dvp, vp_ref.shape, np.uint16), vp_ref)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_fused_token_kernel_matches_row_kernel(paged):
+    """Prompts (>= 64 tokens) run a workgroup per token, a few tokens a wave per row: the same
+    arithmetic per row, so a 96-token call equals three 32-token calls bit for bit."""
+    r = SplitMix64(33 + paged)
+    T, Hq, Hkv, Dh, pos0, ps = 96, 16, 8, 128, 10, 16
+    q, k, v = r.normal((T, Hq, Dh)), r.normal((T, Hkv, Dh)), r.normal((T, Hkv, Dh))
+    qw, kw = r.normal((Dh,), 0.5) + 1.0, r.normal((Dh,), 0.5) + 1.0
+    pos = np.arange(pos0, pos0 + T, dtype=np.int32)
+    cap = 128
+    n_pages = cap // ps
+    table = np.array(SplitMix64(6).uniform(n_pages).argsort(), np.int32) if paged else None
+    shape = (n_pages, ps, Hkv, Dh) if paged else (cap, Hkv, Dh)
+    outs = []
+    for chunks in ([(0, T)], [(0, 32), (32, 64), (64, 96)]):
+        dq, dk = up(q), up(k)
+        dkc, dvc = up(np.zeros(shape, np.uint16)), up(np.zeros(shape, np.uint16))
+        dt = up(table) if paged else None
+        dpos, dv = up(pos), up(v)
+        for a, b in chunks:
+            n = b - a
+            say("fused token/row", paged, a, b)
+            da.QkNormRopeKvWrite(dq.ptr + a * Hq * Dh * 4, dk.ptr + a * Hkv * Dh * 4,
+                                 dv.ptr + a * Hkv * Dh * 4, Hq * Dh, Hkv * Dh, up(qw), up(kw), EPS,
+                                 dpos.ptr + a * 4, THETA, n, n, Hq, Hkv, Dh, dkc, dvc, dt,
+                                 n_pages if paged else 0, ps if paged else 0,
+                                 n_pages if paged else cap)
+        outs.append([down(dq, q.shape), down(dk, k.shape), down(dkc, shape, np.uint16),
+                     down(dvc, shape, np.uint16)])
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    q_ref, k_ref = _oracle(q, k, v, qw, kw, pos)
+    assert np.max(np.abs(outs[0][0] - q_ref)) < 2e-6
+    assert np.max(np.abs(outs[0][1] - k_ref)) < 2e-6
