@@ -3,8 +3,9 @@
 // LaunchBf16Gemm (include/model/gemm.cuh:384-501) computes out[M][N] = act(in[M][K] W[N][K]^T
 // + bias) in fp32 from bf16 operands.  For prompts the product is a plain GEMM, so it runs on
 // the library's tuned MFMA kernels: the row-major problem is the column-major
-// D[N x M] = op_T(W: K x N, ld K) * op_N(in: K x M, ld K), fp32 compute and output.  The bias
-// and activation, when asked for, follow in one elementwise pass (launch_bias_act), so the
+// D[N x M] = op_T(W: K x N, ld K) * op_N(in: K x M, ld K), fp32 compute and output (beta = 1
+// with C = D folds a residual add into the product: one fp32 rounding, as the add).  The bias
+// and activation, when asked for, follow in one elementwise pass (bias_act_kernel), so the
 // activation is this library's own erf GELU / ReLU, not the GEMM library's epilogue.
 //
 // Plans (descriptors + the heuristic's first algorithm) are cached per device and shape.  Only
@@ -86,7 +87,7 @@ bool bf16_gemm_lib_enabled() {
 }
 
 int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
-                         hipStream_t stream) {
+                         float beta, hipStream_t stream) {
   int dev = 0;
   if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
   std::lock_guard<std::mutex> lock(g_lt_mu);
@@ -106,7 +107,7 @@ int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int 
   }
   Plan& p = it->second;
   if (!p.ok) return ORATOR_ERR_UNSUPPORTED;
-  const float alpha = 1.0f, beta = 0.0f;
+  const float alpha = 1.0f;  // D = alpha op(A) op(B) + beta C, C = D = out
   const hipblasStatus_t st = hipblasLtMatmul(d.handle, p.desc, &alpha, W, p.la, in, p.lb, &beta,
                                              out, p.lc, out, p.lc, &p.algo, nullptr, 0, stream);
   if (!lt_ok(st)) return fail(ORATOR_ERR_HIP, "bf16_gemm: hipblasLtMatmul failed");

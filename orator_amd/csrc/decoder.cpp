@@ -20,6 +20,7 @@
 //    without graphs the same bodies run eagerly.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -48,9 +49,9 @@ struct Decoder {
 
   // prefill scratch (grown to the prefill length)
   int cap_t = 0;
-  float *x = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr,
-        *proj = nullptr, *gate = nullptr, *up = nullptr;
-  uint16_t* norm_bf16 = nullptr;
+  float *x = nullptr, *q = nullptr, *kv = nullptr, *attn = nullptr, *proj = nullptr,
+        *gu = nullptr;
+  uint16_t *norm_bf16 = nullptr, *act_bf16 = nullptr;
   int* pos_dev = nullptr;  // [cap_t + 1]: positions, then pos0
   int* pos_host = nullptr; // pinned staging
   // decode-step scratch (fixed addresses: captured graphs bake them in)
@@ -82,12 +83,12 @@ struct Decoder {
   }
 
   void free_prefill() {
-    for (void* p : {(void*)x, (void*)norm, (void*)q, (void*)k, (void*)v, (void*)attn, (void*)proj,
-                    (void*)gate, (void*)up, (void*)norm_bf16, (void*)pos_dev})
+    for (void* p : {(void*)x, (void*)q, (void*)kv, (void*)attn, (void*)proj, (void*)gu,
+                    (void*)norm_bf16, (void*)act_bf16, (void*)pos_dev})
       if (p) (void)hipFree(p);
     if (pos_host) (void)hipHostFree(pos_host);
-    x = norm = q = k = v = attn = proj = gate = up = nullptr;
-    norm_bf16 = nullptr;
+    x = q = kv = attn = proj = gu = nullptr;
+    norm_bf16 = act_bf16 = nullptr;
     pos_dev = pos_host = nullptr;
     cap_t = 0;
   }
@@ -122,11 +123,12 @@ struct Decoder {
     free_prefill();
     const size_t H = c.hidden_size, I = c.intermediate_size, t = T;
     int rc = 0;
-    if ((rc = dalloc(&x, t * H)) || (rc = dalloc(&norm, t * H)) || (rc = dalloc(&q, t * Qd())) ||
-        (rc = dalloc(&k, t * KVd())) || (rc = dalloc(&v, t * KVd())) ||
-        (rc = dalloc(&attn, t * Qd())) || (rc = dalloc(&proj, t * H)) ||
-        (rc = dalloc(&gate, t * I)) || (rc = dalloc(&up, t * I)) ||
-        (rc = dalloc(&norm_bf16, t * H)) || (rc = dalloc(&pos_dev, t + 1)))
+    const size_t act = std::max<size_t>(Qd(), I);
+    if ((rc = dalloc(&x, t * H)) || (rc = dalloc(&q, t * Qd())) ||
+        (rc = dalloc(&kv, t * 2 * KVd())) || (rc = dalloc(&attn, t * Qd())) ||
+        (rc = dalloc(&proj, t * H)) || (rc = dalloc(&gu, t * 2 * I)) ||
+        (rc = dalloc(&norm_bf16, t * H)) || (rc = dalloc(&act_bf16, t * act)) ||
+        (rc = dalloc(&pos_dev, t + 1)))
       return rc;
     if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&pos_host), (t + 1) * sizeof(int)),
                         "decoder pinned positions")))
@@ -146,31 +148,29 @@ struct Decoder {
                                       hipMemcpyHostToDevice, s),
                        "decoder positions");
     const int* d_pos0 = pos_dev + T;
-    const long TH = static_cast<long>(T) * H;
+    // Per layer, the reference's passes with the casts and residual adds folded in (same
+    // fp32 values rounded once each): RmsNorm -> bf16, q and k|v projections (row slices of
+    // the fused qkv weight), QK-norm/RoPE/KV write, attention, bf16 cast, o projection += x,
+    // RmsNorm -> bf16, the fused gate|up projection, SwiGLU -> bf16, down projection += x.
+    const long TQ = static_cast<long>(T) * Qd();
     for (int li = 0; li < c.num_layers && !rc; ++li) {
       const OratorDecoderLayer& L = layers[li];
-      (rc = orator_rms_norm(x, L.in_ln, norm, T, H, eps, s)) ||
-          (rc = orator_f32_to_bf16(norm, norm_bf16, TH, s)) ||
+      (rc = launch_rms_norm_bf16(x, L.in_ln, norm_bf16, T, H, eps, s)) ||
           (rc = orator_linear_pre(norm_bf16, L.qkv_w, nullptr, q, T, H, Qd(), 0, s)) ||
-          (rc = orator_linear_pre(norm_bf16, L.qkv_w + static_cast<size_t>(Qd()) * H, nullptr, k,
-                                  T, H, KVd(), 0, s)) ||
-          (rc = orator_linear_pre(norm_bf16, L.qkv_w + static_cast<size_t>(Qd() + KVd()) * H,
-                                  nullptr, v, T, H, KVd(), 0, s)) ||
-          (rc = orator_qk_norm_rope_kv_write(q, k, v, Qd(), KVd(), L.q_norm, L.k_norm, eps,
-                                             pos_dev, c.rope_theta, T, T, Hq, Hkv, Dh, kc[li],
-                                             vc[li], nullptr, 0, 0, c.max_seq_len, s)) ||
+          (rc = orator_linear_pre(norm_bf16, L.qkv_w + static_cast<size_t>(Qd()) * H, nullptr,
+                                  kv, T, H, 2 * KVd(), 0, s)) ||
+          (rc = orator_qk_norm_rope_kv_write(q, kv, kv + KVd(), Qd(), 2 * KVd(), L.q_norm,
+                                             L.k_norm, eps, pos_dev, c.rope_theta, T, T, Hq, Hkv,
+                                             Dh, kc[li], vc[li], nullptr, 0, 0, c.max_seq_len,
+                                             s)) ||
           (rc = orator_gqa_prefill(q, kc[li], vc[li], attn, T, Hq, Hkv, Dh, d_pos0,
                                    c.max_seq_len, scale(), s)) ||
-          (rc = orator_linear(attn, L.o_w, nullptr, proj, T, Qd(), H, 0, s)) ||
-          (rc = orator_add_residual(x, proj, TH, s)) ||
-          (rc = orator_rms_norm(x, L.post_ln, norm, T, H, eps, s)) ||
-          (rc = orator_f32_to_bf16(norm, norm_bf16, TH, s)) ||
-          (rc = orator_linear_pre(norm_bf16, L.gateup_w, nullptr, gate, T, H, I, 0, s)) ||
-          (rc = orator_linear_pre(norm_bf16, L.gateup_w + static_cast<size_t>(I) * H, nullptr, up,
-                                  T, H, I, 0, s)) ||
-          (rc = orator_swiglu(gate, up, gate, T * I, s)) ||
-          (rc = orator_linear(gate, L.down_w, nullptr, proj, T, I, H, 0, s)) ||
-          (rc = orator_add_residual(x, proj, TH, s));
+          (rc = orator_f32_to_bf16(attn, act_bf16, TQ, s)) ||
+          (rc = launch_linear_pre_acc(act_bf16, L.o_w, x, T, Qd(), H, proj, s)) ||
+          (rc = launch_rms_norm_bf16(x, L.post_ln, norm_bf16, T, H, eps, s)) ||
+          (rc = orator_linear_pre(norm_bf16, L.gateup_w, nullptr, gu, T, H, 2 * I, 0, s)) ||
+          (rc = launch_swiglu_bf16(gu, act_bf16, T, I, s)) ||
+          (rc = launch_linear_pre_acc(act_bf16, L.down_w, x, T, I, H, proj, s));
     }
     if (rc) return rc;
     cache_len = pos0 + T;

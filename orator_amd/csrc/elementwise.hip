@@ -21,17 +21,19 @@ inline int blocks_for(long n, int per_block = kBlock) {
 }
 
 // ------------------------------------------------------------------ RmsNorm ----
-template <bool VEC>
+// OUT = float: the reference's RmsNorm; OUT = uint16_t: RmsNorm then F32ToBf16 (RNE) of the
+// same fp32 values, in one pass.
+template <bool VEC, typename OUT = float>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ w,
-                                                       float* out, int rows, int dim,
+                                                       OUT* out, int rows, int dim,
                                                        float eps) {
 #pragma clang fp contract(off)
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   const float* xr = x + static_cast<long>(row) * dim;
-  float* yr = out + static_cast<long>(row) * dim;
+  OUT* yr = out + static_cast<long>(row) * dim;
   float local = 0.0f;
   if (VEC) {
     for (int d = lane * 4; d < dim; d += 256) {
@@ -51,11 +53,21 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
     for (int d = lane * 4; d < dim; d += 256) {
       const float4 v = *reinterpret_cast<const float4*>(xr + d);
       const float4 g = *reinterpret_cast<const float4*>(w + d);
-      *reinterpret_cast<float4*>(yr + d) =
+      const float4 y =
           make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+      if constexpr (sizeof(OUT) == 4)
+        *reinterpret_cast<float4*>(yr + d) = y;
+      else
+        *reinterpret_cast<uint2*>(yr + d) = make_uint2(pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w));
     }
   } else {
-    for (int d = lane; d < dim; d += 64) yr[d] = xr[d] * inv * w[d];
+    for (int d = lane; d < dim; d += 64) {
+      const float y = xr[d] * inv * w[d];
+      if constexpr (sizeof(OUT) == 4)
+        yr[d] = y;
+      else
+        yr[d] = f32_to_bf16(y);
+    }
   }
 }
 
@@ -106,6 +118,23 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* g, const float
   if (i >= n) return;
   const float gv = g[i];
   o[i] = (gv / (1.0f + expf(-gv))) * u[i];
+}
+
+// SwiGLU of a fused gate|up row block gu [T][2I] (gate = columns [0, I), up = [I, 2I)) with
+// the bf16 cast of the down projection's input folded in: out[t][i] = bf16(silu(g) * u), the
+// same fp32 value as swiglu_kernel's.  4 columns per thread (I % 4 == 0).
+__global__ __launch_bounds__(256) void swiglu_bf16_kernel(const float* __restrict__ gu,
+                                                          uint16_t* __restrict__ out, int T,
+                                                          int I) {
+  const long i4 = 4 * (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x);
+  if (i4 >= static_cast<long>(T) * I) return;
+  const long t = i4 / I;
+  const int i = static_cast<int>(i4 - t * I);
+  const float4 g = *reinterpret_cast<const float4*>(gu + t * 2 * I + i);
+  const float4 u = *reinterpret_cast<const float4*>(gu + t * 2 * I + I + i);
+  const float y0 = (g.x / (1.0f + expf(-g.x))) * u.x, y1 = (g.y / (1.0f + expf(-g.y))) * u.y;
+  const float y2 = (g.z / (1.0f + expf(-g.z))) * u.z, y3 = (g.w / (1.0f + expf(-g.w))) * u.w;
+  *reinterpret_cast<uint2*>(out + i4) = make_uint2(pack_bf16x2(y0, y1), pack_bf16x2(y2, y3));
 }
 
 // -------------------------------------------------------------------- casts ----
@@ -396,6 +425,29 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 }  // namespace orator_hip
 
 namespace orator_hip {
+
+int launch_rms_norm_bf16(const float* x, const float* w, uint16_t* out, int rows, int dim,
+                         float eps, hipStream_t s) {
+  if (rows <= 0 || dim <= 0) return ORATOR_OK;
+  const dim3 grid(blocks_for(rows, 4));
+  if (dim % 4 == 0 && aligned16(x) && aligned16(w) && (reinterpret_cast<uintptr_t>(out) & 7u) == 0)
+    hipLaunchKernelGGL((rms_norm_kernel<true, uint16_t>), grid, dim3(256), 0, s, x, w, out, rows,
+                       dim, eps);
+  else
+    hipLaunchKernelGGL((rms_norm_kernel<false, uint16_t>), grid, dim3(256), 0, s, x, w, out, rows,
+                       dim, eps);
+  return check_launch("rms_norm_bf16");
+}
+
+int launch_swiglu_bf16(const float* gu, uint16_t* out, int T, int I, hipStream_t s) {
+  if (T <= 0 || I <= 0) return ORATOR_OK;
+  if (I % 4 || !aligned16(gu) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(ORATOR_ERR_UNSUPPORTED, "swiglu_bf16: I % 4 and 16/8-byte alignment");
+  const long threads = static_cast<long>(T) * I / 4;
+  hipLaunchKernelGGL(swiglu_bf16_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                     dim3(256), 0, s, gu, out, T, I);
+  return check_launch("swiglu_bf16");
+}
 
 size_t argmax_scratch_bytes(int n) {
   const int rows = (n + 255) / 256;

@@ -91,7 +91,16 @@ size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity);
 constexpr int kLibMinM = 32;  // smaller M stays on the MFMA kernel / GEMV
 bool bf16_gemm_lib_enabled();
 int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
-                         hipStream_t stream);
+                         float beta, hipStream_t stream);
+// out[M][N] += in[M][K] W[N][K]^T (the residual add folded into the library GEMM's beta = 1;
+// below its size, this library's GEMM into tmp [M][N] and an add).
+int launch_linear_pre_acc(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
+                          float* tmp, hipStream_t stream);
+// RmsNorm with the bf16 cast of its output folded in; SwiGLU of a fused gate|up block
+// [T][2I] with the bf16 cast folded in.
+int launch_rms_norm_bf16(const float* x, const float* w, uint16_t* out, int rows, int dim,
+                         float eps, hipStream_t s);
+int launch_swiglu_bf16(const float* gu, uint16_t* out, int T, int I, hipStream_t s);
 
 int launch_sgemm(const float* in, const float* W, const float* bias, float* out, int M, int K,
                  int N, int act, int batch, long stride_in, long stride_w, long stride_out,

@@ -364,7 +364,7 @@ int launch_bf16_gemm(const uint16_t* in, const uint16_t* W, const float* bias, f
   // activation in one pass after it); small M, and shapes it has no plan for, run the MFMA
   // kernel below.
   if (M >= kLibMinM && bf16_gemm_lib_enabled()) {
-    const int rc = launch_bf16_gemm_lib(in, W, out, M, K, N, stream);
+    const int rc = launch_bf16_gemm_lib(in, W, out, M, K, N, 0.0f, stream);
     if (rc == ORATOR_OK) {
       if (!bias && act == 0) return ORATOR_OK;
       const long n_all = static_cast<long>(M) * N;
@@ -417,6 +417,18 @@ int launch_linear_pre(const uint16_t* in, const uint16_t* W, const float* bias, 
     return check_launch("gemv_bf16_kernel");
   }
   return launch_bf16_gemm(in, W, bias, out, M, K, N, act, stream);
+}
+
+int launch_linear_pre_acc(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
+                          float* tmp, hipStream_t stream) {
+  if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;
+  if (int rc = check_linear(in, W, out, K, 0, "linear_acc")) return rc;
+  if (M >= kLibMinM && bf16_gemm_lib_enabled()) {
+    const int rc = launch_bf16_gemm_lib(in, W, out, M, K, N, 1.0f, stream);
+    if (rc != ORATOR_ERR_UNSUPPORTED) return rc;
+  }
+  if (int rc = launch_linear_pre(in, W, nullptr, tmp, M, K, N, 0, stream)) return rc;
+  return orator_add_residual(out, tmp, static_cast<long>(M) * N, stream);
 }
 
 }  // namespace orator_hip
