@@ -59,7 +59,36 @@ struct DecodeArgs {
   const float* k_new;
   const float* v_new;
   long pool_rows;  // rows the pools hold (paged writes past it are dropped)
+  // QK-norm + RoPE folded in (the QKN kernels): see DecodeProblem
+  const float* q_norm;
+  const float* k_norm;
+  const float* rope;
+  float eps;
 };
+
+// RmsNorm (weights w, eps) + rotate-half RoPE (cos, sin of pairs j = EPV * o + e at cs) of one
+// 128-dim head held in the octet layout: lane o of each 8-lane group owns dims 8o + e and
+// 64 + 8o + e (x[e], x[8 + e]), so every RoPE pair is lane-local; the sum of squares is
+// reduced over the octet.  Same operations as the fused QK-norm/RoPE kernel (no contraction).
+__device__ __forceinline__ void qk_norm_rope_octet(float (&x)[16], const float* w, float eps,
+                                                   const float* cs, int o) {
+#pragma clang fp contract(off)
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ss += x[i] * x[i];
+  ss += dpp<0xB1>(ss);
+  ss += dpp<0x4E>(ss);
+  ss += dpp<0x141>(ss);
+  const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss / 128.0f + eps)));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int j = 8 * o + e;
+    const float n0 = x[e] * inv * w[j], n1 = x[8 + e] * inv * w[j + 64];
+    const float c = cs[2 * j], s = cs[2 * j + 1];
+    x[e] = n0 * c - n1 * s;
+    x[8 + e] = n1 * c + n0 * s;
+  }
+}
 
 // Number of keys stream b attends, clamped to the capacity.
 __device__ __forceinline__ int stream_keys(const DecodeArgs& a, int b) {
@@ -224,21 +253,31 @@ __device__ __forceinline__ void process_chunk(const Chunk<DH, KV>& cur,
 // 64 lanes hold it after the reduction), one lane adds its weight to the row sum, the r == 0
 // lanes its weighted V row.  Returns this lane's bf16 K (octet layout) and V (row layout)
 // pieces for the cache write.
-template <int DH, int G>
+template <int DH, int G, bool QKN>
 __device__ __forceinline__ void append_key(const float* kn, const float* vn,
                                            const float (&qr)[G][Chunk<DH, uint16_t>::QPL],
                                            float (&m)[G], float (&lpart)[G], float (&acc)[G][8],
                                            int lane, float scale_log2e,
-                                           uint4 (&kw)[Chunk<DH, uint16_t>::NCQ], uint4& vw) {
+                                           uint4 (&kw)[Chunk<DH, uint16_t>::NCQ], uint4& vw,
+                                           const float* k_norm, float eps, const float* cs) {
   using CK = Chunk<DH, uint16_t>;
   const int o = lane & 7;
   float kf[CK::QPL];
+  float kx[CK::QPL];
 #pragma unroll
   for (int cc = 0; cc < CK::NCQ; ++cc) {
     const float4 x0 = *reinterpret_cast<const float4*>(kn + 8 * CK::EPV * cc + CK::EPV * o);
     const float4 x1 = *reinterpret_cast<const float4*>(kn + 8 * CK::EPV * cc + CK::EPV * o + 4);
-    kw[cc] = make_uint4(pack_bf16x2(x0.x, x0.y), pack_bf16x2(x0.z, x0.w), pack_bf16x2(x1.x, x1.y),
-                        pack_bf16x2(x1.z, x1.w));
+    kx[cc * 8 + 0] = x0.x; kx[cc * 8 + 1] = x0.y; kx[cc * 8 + 2] = x0.z; kx[cc * 8 + 3] = x0.w;
+    kx[cc * 8 + 4] = x1.x; kx[cc * 8 + 5] = x1.y; kx[cc * 8 + 6] = x1.z; kx[cc * 8 + 7] = x1.w;
+  }
+  if constexpr (QKN) qk_norm_rope_octet(kx, k_norm, eps, cs, o);
+#pragma unroll
+  for (int cc = 0; cc < CK::NCQ; ++cc) {
+    kw[cc] = make_uint4(pack_bf16x2(kx[cc * 8 + 0], kx[cc * 8 + 1]),
+                        pack_bf16x2(kx[cc * 8 + 2], kx[cc * 8 + 3]),
+                        pack_bf16x2(kx[cc * 8 + 4], kx[cc * 8 + 5]),
+                        pack_bf16x2(kx[cc * 8 + 6], kx[cc * 8 + 7]));
     const uint32_t w[4] = {kw[cc].x, kw[cc].y, kw[cc].z, kw[cc].w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) kf[cc * 8 + e] = (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
@@ -279,9 +318,10 @@ constexpr int decode_waves() {
   return (sizeof(KV) == 2 && G <= 2 && SPLIT >= 256 && SPLIT <= 512) ? SPLIT / 32 : 4;
 }
 
-template <int DH, int G, int SPLIT, typename KV>
+template <int DH, int G, int SPLIT, typename KV, bool QKN>
 __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__((
     amdgpu_waves_per_eu(2))) void gqa_decode_kernel(DecodeArgs a) {
+  static_assert(!QKN || (DH == 128 && sizeof(KV) == 2), "QK-norm folding: Dh 128, bf16 caches");
   using CK = Chunk<DH, KV>;
   constexpr int NW = decode_waves<SPLIT, KV, G>();
   constexpr int NT = 64 * NW;
@@ -341,6 +381,12 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
         qr[g][cc * CK::EPV + e4 + 2] = x.z;
         qr[g][cc * CK::EPV + e4 + 3] = x.w;
       }
+  }
+  const float* rope_cs = nullptr;  // (cos, sin) pairs of this stream's position (QKN)
+  if constexpr (QKN) {
+    rope_cs = a.rope + static_cast<long>(min(max(a.pos[b], 0), a.capacity - 1)) * DH;
+#pragma unroll
+    for (int g = 0; g < G; ++g) qk_norm_rope_octet(qr[g], a.q_norm, a.eps, rope_cs, o);
   }
   lds_barrier();  // row_lds ready (the q loads may still be in flight)
 
@@ -404,7 +450,8 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   if constexpr (sizeof(KV) == 2) {
     if (owns_new) {  // uniform over the wave
       uint4 kw[CK::NCQ], vw;
-      append_key<DH, G>(kn, vn, qr, m, lpart, acc, lane, a.scale_log2e, kw, vw);
+      append_key<DH, G, QKN>(kn, vn, qr, m, lpart, acc, lane, a.scale_log2e, kw, vw, a.k_norm,
+                             a.eps, rope_cs);
       // write the new row into the cache (dropped past the pool, as the KV write does)
       const long row = row_lds[(new_key - t0) >> 4] + (new_key & 15);
       if (row < a.pool_rows) {
@@ -540,8 +587,17 @@ int launch_split(const DecodeArgs& args, int B, hipStream_t stream) {
   hipEvent_t ev0, ev_split, ev1;
   take_timing_events(&ev0, &ev_split, &ev1);
   if (ev0) (void)hipEventRecord(ev0, stream);
-  hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV>), grid,
-                     dim3(64 * decode_waves<SPLIT, KV, G>()), 0, stream, args);
+  bool launched = false;
+  if constexpr (DH == 128 && sizeof(KV) == 2) {
+    if (args.q_norm) {
+      hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV, true>), grid,
+                         dim3(64 * decode_waves<SPLIT, KV, G>()), 0, stream, args);
+      launched = true;
+    }
+  }
+  if (!launched)
+    hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV, false>), grid,
+                       dim3(64 * decode_waves<SPLIT, KV, G>()), 0, stream, args);
   int rc = check_launch("gqa_decode_kernel");
   if (ev_split) (void)hipEventRecord(ev_split, stream);
   if (!rc && args.max_splits > 1) {
@@ -626,6 +682,9 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
     if ((reinterpret_cast<uintptr_t>(p.k_new) | reinterpret_cast<uintptr_t>(p.v_new)) & 15u)
       return fail(ORATOR_ERR_INVALID, "gqa_decode: appended k/v rows must be 16-byte aligned");
   }
+  if (p.q_norm && (!p.k_norm || !p.rope || !p.k_new || p.Dh != 128 || p.kv_f32))
+    return fail(ORATOR_ERR_INVALID,
+                "gqa_decode: QK-norm folding needs k_norm, the RoPE table, an appended row, Dh 128");
   int page_shift = 0;
   if (p.page_table) {
     page_shift = ilog2_exact(p.page_size);
@@ -664,6 +723,10 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   args.k_new = p.k_new;
   args.v_new = p.v_new;
   args.pool_rows = p.pool_rows;
+  args.q_norm = p.q_norm;
+  args.k_norm = p.k_norm;
+  args.rope = p.rope;
+  args.eps = p.eps;
 
   if (p.kv_f32) return launch_kv<float>(args, p.B, p.Dh, G, split, stream);
   return launch_kv<uint16_t>(args, p.B, p.Dh, G, split, stream);

@@ -56,6 +56,7 @@ struct Decoder {
   int* pos_host = nullptr; // pinned staging
   // decode-step scratch (fixed addresses: captured graphs bake them in)
   float *sx = nullptr, *sqkv = nullptr, *sattn = nullptr, *sgateup = nullptr, *logits = nullptr;
+  float* rope = nullptr;  // [max_seq_len][64][cos, sin]: the step's RoPE without fp64 trig
   void* argmax_scratch = nullptr;
   int *spos = nullptr, *stok = nullptr, *scount = nullptr, *sout = nullptr;
   int sout_cap = 0;
@@ -77,7 +78,8 @@ struct Decoder {
     for (auto* p : vc) (void)hipFree(p);
     free_prefill();
     for (void* p : {(void*)sx, (void*)sqkv, (void*)sattn, (void*)sgateup, (void*)logits,
-                    argmax_scratch, (void*)spos, (void*)stok, (void*)scount, (void*)sout})
+                    argmax_scratch, (void*)spos, (void*)stok, (void*)scount, (void*)sout,
+                    (void*)rope})
       if (p) (void)hipFree(p);
     if (host_int) (void)hipHostFree(host_int);
   }
@@ -108,7 +110,10 @@ struct Decoder {
     if ((rc = dalloc(&sx, H)) || (rc = dalloc(&sqkv, Qd() + 2 * KVd())) ||
         (rc = dalloc(&sattn, Qd())) || (rc = dalloc(&sgateup, 2 * I)) ||
         (rc = dalloc(&logits, c.vocab_size)) || (rc = dalloc(&spos, 1)) ||
-        (rc = dalloc(&stok, 1)) || (rc = dalloc(&scount, 1)))
+        (rc = dalloc(&stok, 1)) || (rc = dalloc(&scount, 1)) ||
+        (rc = dalloc(&rope, static_cast<size_t>(c.max_seq_len) * 128)) ||
+        (rc = launch_rope_table(rope, c.max_seq_len, c.rope_theta, nullptr)) ||
+        (rc = check_hip(hipDeviceSynchronize(), "decoder rope table")))
       return rc;
     if (const size_t n = argmax_scratch_bytes(c.vocab_size))
       if ((rc = dalloc(reinterpret_cast<char**>(&argmax_scratch), n))) return rc;
@@ -159,10 +164,10 @@ struct Decoder {
           (rc = orator_linear_pre(norm_bf16, L.qkv_w, nullptr, q, T, H, Qd(), 0, s)) ||
           (rc = orator_linear_pre(norm_bf16, L.qkv_w + static_cast<size_t>(Qd()) * H, nullptr,
                                   kv, T, H, 2 * KVd(), 0, s)) ||
-          (rc = orator_qk_norm_rope_kv_write(q, kv, kv + KVd(), Qd(), 2 * KVd(), L.q_norm,
-                                             L.k_norm, eps, pos_dev, c.rope_theta, T, T, Hq, Hkv,
-                                             Dh, kc[li], vc[li], nullptr, 0, 0, c.max_seq_len,
-                                             s)) ||
+          (rc = launch_qk_norm_rope_kv(q, kv, kv + KVd(), Qd(), 2 * KVd(), L.q_norm, L.k_norm,
+                                       eps, pos_dev, c.rope_theta, rope, c.max_seq_len, T, T,
+                                       Hq, Hkv, Dh, kc[li], vc[li], nullptr, 0, 0, c.max_seq_len,
+                                       s)) ||
           (rc = orator_gqa_prefill(q, kc[li], vc[li], attn, T, Hq, Hkv, Dh, d_pos0,
                                    c.max_seq_len, scale(), s)) ||
           (rc = orator_f32_to_bf16(attn, act_bf16, TQ, s)) ||
@@ -194,13 +199,30 @@ struct Decoder {
     int rc = 0;
     for (int li = 0; li < c.num_layers && !rc; ++li) {
       const OratorDecoderLayer& L = layers[li];
+      // attention of the step: QK-norm, RoPE (the position's table row), the KV write of the
+      // new row and the split-K attention in one launch, plus the split merge
+      DecodeProblem p{};
+      p.q = dq;
+      p.kpool = kc[li];
+      p.vpool = vc[li];
+      p.pos = spos;
+      p.out = sattn;
+      p.B = 1;
+      p.Hq = Hq;
+      p.Hkv = Hkv;
+      p.Dh = Dh;
+      p.capacity = c.max_seq_len;
+      p.scale = scale();
+      p.k_new = dk;
+      p.v_new = dv;
+      p.pool_rows = c.max_seq_len;
+      p.q_norm = L.q_norm;
+      p.k_norm = L.k_norm;
+      p.rope = rope;
+      p.eps = eps;
       (rc = launch_gemv_fused(kGemvInRmsNorm, sx, L.in_ln, eps, L.qkv_w, sqkv, H,
                               Qd() + 2 * KVd(), false, s)) ||
-          (rc = orator_qk_norm_rope_kv_write(dq, dk, dv, 0, 0, L.q_norm, L.k_norm, eps, spos,
-                                             c.rope_theta, 1, 1, Hq, Hkv, Dh, kc[li], vc[li],
-                                             nullptr, 0, 0, c.max_seq_len, s)) ||
-          (rc = orator_gqa_decode(dq, kc[li], vc[li], sattn, Hq, Hkv, Dh, spos, c.max_seq_len,
-                                  scale(), s)) ||
+          (rc = launch_gqa_decode(p, s)) ||
           (rc = launch_gemv_fused(kGemvInF32, sattn, nullptr, 0.0f, L.o_w, sx, Qd(), H, true, s)) ||
           (rc = launch_gemv_fused(kGemvInRmsNorm, sx, L.post_ln, eps, L.gateup_w, sgateup, H, I,
                                   false, s, /*pair=*/true)) ||

@@ -111,6 +111,17 @@ __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x,
   }
 }
 
+// (cos, sin) of RoPE pair j (head_dim 128) at position p: out[(p * 64 + j) * 2 + {0, 1}].
+__global__ __launch_bounds__(256) void rope_table_kernel(float* __restrict__ out, int n_pos,
+                                                         float theta) {
+  const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<long>(n_pos) * 64) return;
+  float c, s;
+  rope_cs(static_cast<float>(i / 64), theta, static_cast<int>(i % 64), 128, &c, &s);
+  out[2 * i] = c;
+  out[2 * i + 1] = s;
+}
+
 // ------------------------------------------------------------------- SwiGLU ----
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* g, const float* u, float* o,
                                                      int n) {
@@ -324,7 +335,22 @@ struct QkvArgs {
   uint16_t* vpool;
   const int* page_table;  // nullptr => contiguous cache of `capacity` rows
   int max_pages, page_shift, capacity;  // paged: capacity = number of pages in the pool
+  const float* rope;  // optional (cos, sin) table of rope_table_kernel, instead of rope_cs
+  int rope_rows;      // positions the table holds
 };
+
+// (cos, sin) of RoPE pair `lane` at position pos: the table row when it holds pos (the same
+// values rope_cs forms), else formed here.
+__device__ __forceinline__ void qkv_rope_cs(const QkvArgs& a, int pos, int lane, float* c,
+                                            float* s) {
+  if (a.rope && pos >= 0 && pos < a.rope_rows) {
+    const float* cs = a.rope + (static_cast<long>(pos) * 64 + lane) * 2;
+    *c = cs[0];
+    *s = cs[1];
+  } else {
+    rope_cs(static_cast<float>(pos), a.theta, lane, 128, c, s);
+  }
+}
 
 // Row hh of token t (q heads first, then k heads): RmsNorm of the loaded halves x0 = x[lane],
 // x1 = x[lane + 64], RoPE with this lane's (c, s), store; a k row also writes its k and v
@@ -384,7 +410,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(QkvArgs a) {
   const float* x = qkv_row_ptr(a, t, hh);
   const float x0 = x[lane], x1 = x[lane + 64];
   float c, s;
-  rope_cs(static_cast<float>(a.positions[t]), a.theta, lane, 128, &c, &s);
+  qkv_rope_cs(a, a.positions[t], lane, &c, &s);
   qkv_row(a, t, hh, lane, c, s, x0, x1);
 }
 
@@ -399,7 +425,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_token_kernel(QkvArgs a) {
   const int lane = threadIdx.x & 63;
   const int per_token = a.Hq + a.Hkv;
   float c, s;
-  rope_cs(static_cast<float>(a.positions[t]), a.theta, lane, 128, &c, &s);
+  qkv_rope_cs(a, a.positions[t], lane, &c, &s);
   for (int hb = wave; hb < per_token; hb += 4 * kQkvBatch) {
     float x0[kQkvBatch], x1[kQkvBatch];
 #pragma unroll
@@ -437,6 +463,66 @@ int launch_rms_norm_bf16(const float* x, const float* w, uint16_t* out, int rows
     hipLaunchKernelGGL((rms_norm_kernel<false, uint16_t>), grid, dim3(256), 0, s, x, w, out, rows,
                        dim, eps);
   return check_launch("rms_norm_bf16");
+}
+
+int launch_qk_norm_rope_kv(float* q, float* k, const float* v, long q_stride, long kv_stride,
+                           const float* q_norm, const float* k_norm, float eps,
+                           const int* positions, float theta, const float* rope,
+                           int rope_rows, int n_tokens, int tokens_per_stream, int Hq, int Hkv,
+                           int Dh, uint16_t* kpool, uint16_t* vpool, const int* page_table,
+                           int max_pages, int page_size, int capacity, hipStream_t stream) {
+  if (n_tokens <= 0 || Hq <= 0 || Hkv <= 0 || Dh <= 0) return ORATOR_OK;
+  if (!q || !k || !v || !q_norm || !k_norm || !positions || !kpool || !vpool)
+    return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: null pointer");
+  if (Dh != 128) return fail(ORATOR_ERR_UNSUPPORTED, "qk_norm_rope_kv_write: Dh must be 128");
+  if (capacity <= 0) return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: capacity must be > 0");
+  QkvArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.q_stride = q_stride;
+  a.kv_stride = kv_stride;
+  a.q_norm = q_norm;
+  a.k_norm = k_norm;
+  a.eps = eps;
+  a.positions = positions;
+  a.theta = theta;
+  a.n_tokens = n_tokens;
+  a.tokens_per_stream = tokens_per_stream > 0 ? tokens_per_stream : n_tokens;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.kpool = kpool;
+  a.vpool = vpool;
+  a.page_table = page_table;
+  a.capacity = capacity;
+  a.rope = rope;
+  a.rope_rows = rope ? rope_rows : 0;
+  if (page_table) {
+    a.page_shift = ilog2_exact(page_size);
+    if (a.page_shift < 0 || max_pages <= 0)
+      return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: page_size must be a power of two");
+    a.max_pages = max_pages;
+  }
+  // Prompts: a workgroup per token (RoPE angles formed once per token and wave); a few
+  // tokens (decode): a wave per row, which spreads the rows over more of the chip.
+  if (n_tokens >= 64) {
+    hipLaunchKernelGGL(qk_norm_rope_kv_token_kernel, dim3(n_tokens), dim3(256), 0,
+                       stream, a);
+  } else {
+    const long rows = static_cast<long>(n_tokens) * (Hq + Hkv);
+    hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0,
+                       stream, a);
+  }
+  return check_launch("qk_norm_rope_kv_write");
+}
+
+
+int launch_rope_table(float* out, int n_pos, float theta, hipStream_t s) {
+  if (n_pos <= 0) return ORATOR_OK;
+  const long n = static_cast<long>(n_pos) * 64;
+  hipLaunchKernelGGL(rope_table_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
+                     0, s, out, n_pos, theta);
+  return check_launch("rope_table");
 }
 
 int launch_swiglu_bf16(const float* gu, uint16_t* out, int T, int I, hipStream_t s) {
@@ -599,47 +685,11 @@ int orator_qk_norm_rope_kv_write(float* q, float* k, const float* v, long q_stri
                                  int tokens_per_stream, int Hq, int Hkv, int Dh, uint16_t* kpool,
                                  uint16_t* vpool, const int* page_table, int max_pages,
                                  int page_size, int capacity, void* stream) {
-  if (n_tokens <= 0 || Hq <= 0 || Hkv <= 0 || Dh <= 0) return ORATOR_OK;
-  if (!q || !k || !v || !q_norm || !k_norm || !positions || !kpool || !vpool)
-    return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: null pointer");
-  if (Dh != 128) return fail(ORATOR_ERR_UNSUPPORTED, "qk_norm_rope_kv_write: Dh must be 128");
-  if (capacity <= 0) return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: capacity must be > 0");
-  QkvArgs a{};
-  a.q = q;
-  a.k = k;
-  a.v = v;
-  a.q_stride = q_stride;
-  a.kv_stride = kv_stride;
-  a.q_norm = q_norm;
-  a.k_norm = k_norm;
-  a.eps = eps;
-  a.positions = positions;
-  a.theta = theta;
-  a.n_tokens = n_tokens;
-  a.tokens_per_stream = tokens_per_stream > 0 ? tokens_per_stream : n_tokens;
-  a.Hq = Hq;
-  a.Hkv = Hkv;
-  a.kpool = kpool;
-  a.vpool = vpool;
-  a.page_table = page_table;
-  a.capacity = capacity;
-  if (page_table) {
-    a.page_shift = ilog2_exact(page_size);
-    if (a.page_shift < 0 || max_pages <= 0)
-      return fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write: page_size must be a power of two");
-    a.max_pages = max_pages;
-  }
-  // Prompts: a workgroup per token (RoPE angles formed once per token and wave); a few
-  // tokens (decode): a wave per row, which spreads the rows over more of the chip.
-  if (n_tokens >= 64) {
-    hipLaunchKernelGGL(qk_norm_rope_kv_token_kernel, dim3(n_tokens), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
-  } else {
-    const long rows = static_cast<long>(n_tokens) * (Hq + Hkv);
-    hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
-  }
-  return check_launch("qk_norm_rope_kv_write");
+  return orator_hip::launch_qk_norm_rope_kv(q, k, v, q_stride, kv_stride, q_norm, k_norm, eps,
+                                            positions, theta, nullptr, 0, n_tokens,
+                                            tokens_per_stream, Hq, Hkv, Dh, kpool, vpool,
+                                            page_table, max_pages, page_size, capacity,
+                                            static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

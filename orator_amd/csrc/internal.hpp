@@ -80,8 +80,30 @@ struct DecodeProblem {
   const float* k_new;
   const float* v_new;
   long pool_rows;
+  // Optional (append, Dh 128, bf16 caches): q and k_new are raw projections; the launch
+  // applies the per-head RmsNorm (weights q_norm / k_norm, eps) and the rotate-half RoPE of
+  // position pos[b], with (cos, sin) of pair j at rope[(pos * 64 + j) * 2 ..] (the values
+  // rope_cs forms; the table holds `capacity` positions, and a position past it -- whose KV
+  // write is dropped -- uses the last row), before attending: the step's QK-norm/RoPE kernel
+  // folded in.
+  const float* q_norm = nullptr;
+  const float* k_norm = nullptr;
+  const float* rope = nullptr;
+  float eps = 0.0f;
 };
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
+// (cos, sin) of RoPE pair j (head_dim 128, base theta) for positions [0, n_pos): out[(p * 64 +
+// j) * 2 + {0, 1}], the values the fused QK-norm/RoPE kernels form.
+int launch_rope_table(float* out, int n_pos, float theta, hipStream_t s);
+// orator_qk_norm_rope_kv_write with an optional (cos, sin) table of launch_rope_table holding
+// positions [0, rope_rows) (the same values, without the per-call fp64 pow/sincos); other
+// positions, or rope == nullptr, form them per call.
+int launch_qk_norm_rope_kv(float* q, float* k, const float* v, long q_stride, long kv_stride,
+                           const float* q_norm, const float* k_norm, float eps,
+                           const int* positions, float theta, const float* rope,
+                           int rope_rows, int n_tokens, int tokens_per_stream, int Hq, int Hkv,
+                           int Dh, uint16_t* kpool, uint16_t* vpool, const int* page_table,
+                           int max_pages, int page_size, int capacity, hipStream_t stream);
 // Workspace bytes a decode launch over B streams of `capacity` keys needs (split partials).
 size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity);
 
