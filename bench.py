@@ -16,7 +16,11 @@ operation's average duration: the HIP events that bracket the timed region on th
 stream, over its K * 28 back-to-back operations.  The CPU baseline is the oracle's scalar
 decode on the host cores, over a bounded sample of the same workload.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1]
+Secondary fields: prefill attention (T = 503, 2048; bf16 and fp32 modes), the 17-layer
+Conformer rel-pos stack, the decode sweep, the 28-layer decoder end to end, and `aux`: the
+windowed attention, the Sortformer MHA and a whole Conformer layer at their reference shapes.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--only PART]
 """
 from __future__ import annotations
 
@@ -54,7 +58,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true",
                     help="decoder part: run the greedy steps eagerly (same kernels, no graph "
                          "replay), e.g. for a per-kernel profile")
-    ap.add_argument("--only", choices=["decode", "prefill", "conformer", "sweep", "decoder"],
+    ap.add_argument("--only", choices=["decode", "prefill", "conformer", "sweep", "decoder",
+                                       "aux"],
                     default=None,
                     help="run one part (for profiling); prints that part's numbers only")
     return ap.parse_args()
@@ -250,6 +255,91 @@ def run_conformer(T: int = 717, layers: int = 17, H: int = 8, Dk: int = 64):
             "fused_f16_tflops": round(tf, 2), "frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
             "stack_ms": round(us_f16 * layers / 1e3, 4),
             "fp32_reference_order_us_per_layer": round(us_f32, 2)}
+
+
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 (the VALU-bound aux kernels are quoted against it)
+
+
+def run_aux(reps: int = 20):
+    """The path's sibling operators at their reference shapes:
+    * the audio tower's windowed self-attention (asr_audio_tower.cu:204-258): 390 frames (30 s
+      of audio after the CNN), 104-frame windows (:510), 16 heads x Dh 64, fp32;
+    * the Sortformer decoder's masked MHA (sortformer_decoder.cu:280-298): T = 717, 8 heads x
+      Dk 24 (d_model 192), fp32;
+    * one whole FastConformer layer (conformer_layer.cu:364-488): T = 717, d_model 512, 8 heads,
+      d_ff 2048, conv kernel 9, both attention modes.
+    Algorithmic flops: attention 4*H*Dh*(attended pairs); the layer's GEMMs 2*rows*in*out each
+    plus its rel-pos core 6*H*T^2*Dk."""
+    from orator_amd import audio_attn, conformer_attn as ca, sortformer_attn
+    from orator_amd.runtime import DeviceBuffer, Event, Stream
+
+    rng = np.random.default_rng(9)
+    st = Stream()
+    f32 = lambda shape, s=1.0: DeviceBuffer.from_array(
+        (s * rng.standard_normal(shape)).astype(np.float32))
+
+    def timed(fn):
+        fn()
+        st.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(st)
+        for _ in range(reps):
+            fn()
+        e1.record(st)
+        st.synchronize()
+        return e0.elapsed_ms(e1) * 1e3 / reps
+
+    out = {}
+    # windowed attention
+    N, H, Dh, W = 390, 16, 64, 104
+    bounds = list(range(0, N, W)) + [N]
+    seg_s = np.concatenate([[a] * (b - a) for a, b in zip(bounds[:-1], bounds[1:])]).astype(np.int32)
+    seg_e = np.concatenate([[b] * (b - a) for a, b in zip(bounds[:-1], bounds[1:])]).astype(np.int32)
+    q, k, v, o = f32((N, H, Dh)), f32((N, H, Dh)), f32((N, H, Dh)), DeviceBuffer(N * H * Dh * 4)
+    ds, de = DeviceBuffer.from_array(seg_s), DeviceBuffer.from_array(seg_e)
+    us = timed(lambda: audio_attn.WindowAttention(q, k, v, o, ds, de, N, H, Dh, 0.125, st))
+    pairs = sum((b - a) ** 2 for a, b in zip(bounds[:-1], bounds[1:]))
+    fl = 4.0 * H * Dh * pairs
+    out["window_attention"] = {"N": N, "H": H, "Dh": Dh, "window": W, "us": round(us, 2),
+                               "tflops": round(fl / us / 1e6, 3),
+                               "GBs": round(4 * N * H * Dh * 4 / us / 1e3, 1)}
+    # Sortformer masked MHA
+    T, H, Dk = 717, 8, 24
+    q, k, v, o = f32((T, H, Dk)), f32((T, H, Dk)), f32((T, H, Dk)), DeviceBuffer(T * H * Dk * 4)
+    us = timed(lambda: sortformer_attn.MaskedSelfAttention(q, k, v, o, T, H, Dk, T,
+                                                          1.0 / math.sqrt(Dk), st))
+    fl = 4.0 * H * Dk * T * T
+    out["sortformer_mha"] = {"T": T, "H": H, "Dk": Dk, "us": round(us, 2),
+                             "tflops": round(fl / us / 1e6, 3),
+                             "frac_fp32": round(fl / us / 1e6 / FP32_PEAK_TFLOPS, 4)}
+    # whole Conformer layer
+    T, D, H, Dff, K = 717, 512, 8, 2048, 9
+    lin = lambda n_out, n_in: f32((n_out, n_in), 1.0 / math.sqrt(n_in))
+    vec = lambda n, s=0.1: f32((n,), s)
+    w = {}
+    for p in ("ff1", "ff2"):
+        w[f"norm_{p}_w"], w[f"norm_{p}_b"] = vec(D), vec(D)
+        w[f"{p}_w1"], w[f"{p}_b1"], w[f"{p}_w2"], w[f"{p}_b2"] = lin(Dff, D), vec(Dff), lin(D, Dff), vec(D)
+    for n in ("att", "conv", "out"):
+        w[f"norm_{n}_w"], w[f"norm_{n}_b"] = vec(D), vec(D)
+    for n in ("q", "k", "v", "out"):
+        w[f"{n}_w"], w[f"{n}_b"] = lin(D, D), vec(D)
+    w["pos_w"], w["pos_bias_u"], w["pos_bias_v"] = lin(D, D), vec(D), vec(D)
+    w["pw1_w"], w["pw1_b"], w["pw2_w"], w["pw2_b"] = lin(2 * D, D), vec(2 * D), lin(D, D), vec(D)
+    w["dw_w"], w["dw_b"] = f32((D, K), 1.0 / math.sqrt(K)), vec(D)
+    w["bn_w"], w["bn_b"], w["bn_mean"] = vec(D), vec(D), vec(D)
+    w["bn_var"] = DeviceBuffer.from_array((0.5 + rng.uniform(size=D)).astype(np.float32))
+    layer = ca.ConformerLayer(w, D, H, Dff, K)
+    pe = DeviceBuffer.from_array(ca.BuildPosEmb(T, D))
+    x = f32((T, D))
+    gemm = 2.0 * (T * D * Dff * 4 + T * D * D * 5 + (2 * T - 1) * D * D + T * D * 2 * D)
+    att = 6.0 * H * T * T * (D // H)
+    for mode, name in ((1, "fused_f16"), (0, "fp32")):
+        us = timed(lambda: layer.Forward(x, T, T, pe, st, attn_mode=mode))
+        out[f"conformer_layer_{name}"] = {"T": T, "d_model": D, "us": round(us, 2),
+                                          "tflops": round((gemm + att) / us / 1e6, 2)}
+    layer.close()
+    return out
 
 
 def run_decoder_e2e(T: int = 2048, new: int = 256, use_graph: bool = True):
@@ -465,7 +555,8 @@ def main():
                 "prefill": lambda: [run_prefill(503, da.PREFILL_BF16),
                                     run_prefill(2048, da.PREFILL_BF16)],
                 "conformer": run_conformer, "sweep": run_decode_sweep,
-                "decoder": lambda: run_decoder_e2e(use_graph=not args.no_graph)}[args.only]()
+                "decoder": lambda: run_decoder_e2e(use_graph=not args.no_graph),
+                "aux": run_aux}[args.only]()
         print(json.dumps({"only": args.only, "result": part}, default=float))
         return
     dec = run_decode(args.steps, args.warmup)
@@ -481,6 +572,8 @@ def main():
     log("decode sweep:", sweep)
     e2e = run_decoder_e2e()
     log("decoder e2e:", e2e)
+    aux = run_aux()
+    log("aux:", aux)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": "GQA decode-attn HBM GB/s (% peak); prefill-attn TFLOP/s (% MFMA peak)",
@@ -517,6 +610,7 @@ def main():
         "conformer_relpos": conf,
         "decode_sweep": sweep,
         "decoder_e2e": e2e,
+        "aux": aux,
     }
     print(json.dumps(line))
 

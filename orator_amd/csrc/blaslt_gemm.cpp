@@ -1,12 +1,16 @@
-// Plain bf16 GEMMs of the prefill projections on hipBLASLt (M > 1).
+// Plain GEMMs on hipBLASLt: the bf16 prompt projections (M > 1) and the fp32 nn.Linear
+// products of the Conformer.
 //
 // LaunchBf16Gemm (include/model/gemm.cuh:384-501) computes out[M][N] = act(in[M][K] W[N][K]^T
-// + bias) in fp32 from bf16 operands.  For prompts the product is a plain GEMM, so it runs on
-// the library's tuned MFMA kernels: the row-major problem is the column-major
-// D[N x M] = op_T(W: K x N, ld K) * op_N(in: K x M, ld K), fp32 compute and output (beta = 1
-// with C = D folds a residual add into the product: one fp32 rounding, as the add).  The bias
-// and activation, when asked for, follow in one elementwise pass (bias_act_kernel), so the
-// activation is this library's own erf GELU / ReLU, not the GEMM library's epilogue.
+// + bias) in fp32 from bf16 operands, LaunchSgemm[Batched] (:47-268) the same from fp32
+// operands.  Where the product is a plain GEMM it runs on the library's tuned MFMA kernels:
+// the row-major problem is the column-major D[N x M] = op_T(W: K x N, ld K) * op_N(in: K x M,
+// ld K), fp32 compute (exact fp32 products for fp32 operands, not a reduced-precision mode)
+// and fp32 output; strided batches map onto the layouts' batch strides.  beta = 1 with C = D
+// folds a residual add into the product (one fp32 rounding, as the add).  Bias and
+// activation, when asked for, follow in one elementwise pass of the caller, so the
+// activations are this library's own (erf GELU / ReLU, SiLU / ReLU / sigmoid), not the GEMM
+// library's epilogue.
 //
 // Plans (descriptors + the heuristic's first algorithm) are cached per device and shape.  Only
 // algorithms that need no workspace are taken, so concurrent streams share nothing; a shape
@@ -34,7 +38,8 @@ struct Plan {
 struct DeviceLt {
   hipblasLtHandle_t handle = nullptr;
   bool failed = false;
-  std::map<std::tuple<int, int, int>, Plan> plans;
+  // (M, K, N, fp32 operands, batch, batch strides of in, W, out)
+  std::map<std::tuple<int, int, int, bool, int, long, long, long>, Plan> plans;
 };
 
 std::mutex g_lt_mu;
@@ -42,17 +47,31 @@ std::map<int, DeviceLt> g_lt;
 
 bool lt_ok(hipblasStatus_t st) { return st == HIPBLAS_STATUS_SUCCESS; }
 
-// Builds (once) the plan of an M x K x N product; false when the library has none.
-bool make_plan(DeviceLt& d, int M, int K, int N, Plan& p) {
+bool set_batch(hipblasLtMatrixLayout_t l, int batch, long stride) {
+  const int32_t n = batch;
+  const int64_t st = stride;
+  return batch == 1 ||
+         (lt_ok(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &n,
+                                                  sizeof(n))) &&
+          lt_ok(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET,
+                                                  &st, sizeof(st))));
+}
+
+// Builds (once) the plan of a (batched) M x K x N product; false when the library has none.
+bool make_plan(DeviceLt& d, int M, int K, int N, bool f32, int batch, long s_in, long s_w,
+               long s_out, Plan& p) {
   const int32_t op_t = HIPBLAS_OP_T, op_n = HIPBLAS_OP_N;
+  const hipDataType ab = f32 ? HIP_R_32F : HIP_R_16BF;
   if (!lt_ok(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)) ||
       !lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_t,
                                              sizeof(op_t))) ||
       !lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_n,
                                              sizeof(op_n))) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K)) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, K)) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, N)))
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p.la, ab, K, N, K)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p.lb, ab, K, M, K)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, N)) ||
+      !set_batch(p.la, batch, s_w) || !set_batch(p.lb, batch, s_in) ||
+      !set_batch(p.lc, batch, s_out))
     return false;
   hipblasLtMatmulPreference_t pref = nullptr;
   if (!lt_ok(hipblasLtMatmulPreferenceCreate(&pref))) return false;
@@ -86,8 +105,10 @@ bool bf16_gemm_lib_enabled() {
   return on;
 }
 
-int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
-                         float beta, hipStream_t stream) {
+namespace {
+
+int gemm_lib(const void* in, const void* W, float* out, int M, int K, int N, bool f32, int batch,
+             long s_in, long s_w, long s_out, float beta, hipStream_t stream) {
   int dev = 0;
   if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
   std::lock_guard<std::mutex> lock(g_lt_mu);
@@ -98,11 +119,11 @@ int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int 
     d.handle = nullptr;
     return ORATOR_ERR_UNSUPPORTED;
   }
-  auto key = std::make_tuple(M, K, N);
+  auto key = std::make_tuple(M, K, N, f32, batch, s_in, s_w, s_out);
   auto it = d.plans.find(key);
   if (it == d.plans.end()) {
     Plan p;
-    make_plan(d, M, K, N, p);
+    make_plan(d, M, K, N, f32, batch, s_in, s_w, s_out, p);
     it = d.plans.emplace(key, p).first;
   }
   Plan& p = it->second;
@@ -110,8 +131,22 @@ int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int 
   const float alpha = 1.0f;  // D = alpha op(A) op(B) + beta C, C = D = out
   const hipblasStatus_t st = hipblasLtMatmul(d.handle, p.desc, &alpha, W, p.la, in, p.lb, &beta,
                                              out, p.lc, out, p.lc, &p.algo, nullptr, 0, stream);
-  if (!lt_ok(st)) return fail(ORATOR_ERR_HIP, "bf16_gemm: hipblasLtMatmul failed");
+  if (!lt_ok(st)) return fail(ORATOR_ERR_HIP, "gemm: hipblasLtMatmul failed");
   return ORATOR_OK;
+}
+
+}  // namespace
+
+int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
+                         float beta, hipStream_t stream) {
+  return gemm_lib(in, W, out, M, K, N, false, 1, 0, 0, 0, beta, stream);
+}
+
+int launch_f32_gemm_lib(const float* in, const float* W, float* out, int M, int K, int N,
+                        int batch, long stride_in, long stride_w, long stride_out,
+                        hipStream_t stream) {
+  return gemm_lib(in, W, out, M, K, N, true, batch, stride_in, stride_w, stride_out, 0.0f,
+                  stream);
 }
 
 }  // namespace orator_hip

@@ -114,6 +114,11 @@ constexpr int kLibMinM = 32;  // smaller M stays on the MFMA kernel / GEMV
 bool bf16_gemm_lib_enabled();
 int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
                          float beta, hipStream_t stream);
+// fp32 (strided-batched) GEMM on hipBLASLt: out_b[M][N] = in_b[M][K] W_b[N][K]^T, exact fp32
+// products, fp32 accumulate; ORATOR_ERR_UNSUPPORTED without a workspace-free plan.
+int launch_f32_gemm_lib(const float* in, const float* W, float* out, int M, int K, int N,
+                        int batch, long stride_in, long stride_w, long stride_out,
+                        hipStream_t stream);
 // out[M][N] += in[M][K] W[N][K]^T (the residual add folded into the library GEMM's beta = 1;
 // below its size, this library's GEMM into tmp [M][N] and an add).
 int launch_linear_pre_acc(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,

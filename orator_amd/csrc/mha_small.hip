@@ -5,9 +5,10 @@
 // gathers, QK^T batched SGEMM, ScaleMaskScoresKernel, AttnSoftmaxKernel, PV batched SGEMM,
 // scatter): scores = (q_i . k_j) * scale, keys j >= valid_len scored -1e30, row softmax, then
 // ctx = P . V, written back in the [T, H, Dk] layout linear_out reads.  No [H, T, T] score
-// matrix: one workgroup owns 64 queries of one head, one query per lane; its four waves split
-// the keys, each keeps an online softmax (a running max per 8-key block), and the four
-// partials are merged in LDS.  K and V rows are wave-uniform, so they arrive through scalar
+// matrix: one workgroup owns 64 queries of one head, one query per lane; its waves (16 for
+// Dk <= 32, 8 above: 717 queries x 8 heads is only 96 workgroups, so the keys are split
+// finely to occupy the SIMDs) split the keys, each keeps an online softmax (a running max per
+// 8-key block), and the partials are merged in LDS.  K and V rows are wave-uniform, so they arrive through scalar
 // loads and feed the FMAs as scalar operands: the kernel is VALU-bound at ~2 Dk FMAs per
 // (query, key), with no LDS traffic in the key loop.
 #include "common.hpp"
@@ -17,10 +18,15 @@ namespace orator_hip {
 namespace {
 
 constexpr int kQ = 64;       // queries per workgroup (one per lane)
-constexpr int kWaves = 4;    // key ranges per workgroup
 constexpr int kKB = 8;       // keys per softmax block
 
+// key ranges (waves) per workgroup; the merge area [waves][64][DK + 2] floats fits the LDS
 template <int DK>
+constexpr int mha_waves() {
+  return DK <= 32 ? 16 : 8;
+}
+
+template <int DK, int kWaves = mha_waves<DK>()>
 __global__ __launch_bounds__(kQ * kWaves) void mha_small_kernel(const float* __restrict__ q,
                                                                 const float* __restrict__ k,
                                                                 const float* __restrict__ v,
@@ -94,7 +100,7 @@ __global__ __launch_bounds__(kQ * kWaves) void mha_small_kernel(const float* __r
     m = mn;
   }
 
-  // ---- merge the four key ranges ----
+  // ---- merge the key ranges ----
   float* mine = part[wave][lane];
   mine[0] = m;
   mine[1] = l;
@@ -128,8 +134,8 @@ __global__ __launch_bounds__(kQ * kWaves) void mha_small_kernel(const float* __r
 template <int DK>
 void launch(const float* q, const float* k, const float* v, float* out, int T, int H, int valid,
             float scale, hipStream_t s) {
-  hipLaunchKernelGGL(mha_small_kernel<DK>, dim3((T + kQ - 1) / kQ, H), dim3(kQ * kWaves), 0, s,
-                     q, k, v, out, T, H, valid, scale);
+  hipLaunchKernelGGL(mha_small_kernel<DK>, dim3((T + kQ - 1) / kQ, H), dim3(kQ * mha_waves<DK>()),
+                     0, s, q, k, v, out, T, H, valid, scale);
 }
 
 }  // namespace

@@ -7,6 +7,10 @@
 // on v_mfma_f32_32x32x2_f32, so results stay within fp32 rounding of the reference's
 // k-sequential FMA chains.
 //
+// Products of at least 32 rows run on hipBLASLt (blaslt_gemm.cpp; fp32 compute, bias and
+// activation in one pass after it); the kernel below serves smaller products and shapes the
+// library has no plan for.
+//
 // Tiling: a workgroup of 4 wave64s computes a 64x64 output tile (2x2 waves of 32x32);
 // 64x16 slices of both operands are staged through padded LDS (row stride 17 floats, so
 // the 32 rows an MFMA operand load touches fall in distinct banks).
@@ -102,6 +106,19 @@ __global__ __launch_bounds__(256) void sgemm_nt_kernel(const float* __restrict__
     }
 }
 
+// out_b[m][n] = act(out_b[m][n] + bias[n]) after a library GEMM.
+__global__ __launch_bounds__(256) void sgemm_bias_act_kernel(float* __restrict__ out,
+                                                             const float* __restrict__ bias,
+                                                             int M, int N, int act, long per,
+                                                             long stride_out, long total) {
+  const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const long b = i / per, r = i - b * per;
+  float* o = out + b * stride_out + r;
+  const float v = *o + (bias ? bias[r % N] : 0.0f);
+  *o = apply_act(v, act);
+}
+
 }  // namespace
 
 int launch_sgemm(const float* in, const float* W, const float* bias, float* out, int M, int K,
@@ -110,6 +127,22 @@ int launch_sgemm(const float* in, const float* W, const float* bias, float* out,
   if (M <= 0 || N <= 0 || K <= 0 || batch <= 0) return ORATOR_OK;
   if (!in || !W || !out) return fail(ORATOR_ERR_INVALID, "sgemm: null pointer");
   if (act < 0 || act > 3) return fail(ORATOR_ERR_INVALID, "sgemm: act must be 0..3");
+  // Products of at least kLibMinM rows: the GEMM library (exact fp32 products), then bias and
+  // activation in one pass; shapes it has no plan for run the kernel above.
+  if (M >= kLibMinM && bf16_gemm_lib_enabled()) {
+    const long s_in = batch > 1 ? stride_in : 0, s_w = batch > 1 ? stride_w : 0,
+               s_out = batch > 1 ? stride_out : 0;
+    const int rc = launch_f32_gemm_lib(in, W, out, M, K, N, batch, s_in, s_w, s_out, stream);
+    if (rc == ORATOR_OK) {
+      if (!bias && act == 0) return ORATOR_OK;
+      const long per = static_cast<long>(M) * N, total = per * batch;
+      hipLaunchKernelGGL(sgemm_bias_act_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
+                         dim3(256), 0, stream, out, bias, M, N, act, per,
+                         batch > 1 ? stride_out : per, total);
+      return check_launch("sgemm_bias_act");
+    }
+    if (rc != ORATOR_ERR_UNSUPPORTED) return rc;
+  }
   const dim3 grid((N + kTile - 1) / kTile, (M + kTile - 1) / kTile, batch);
   hipLaunchKernelGGL(sgemm_nt_kernel, grid, dim3(256), 0, stream, in, W, bias, out, M, K, N, act,
                      stride_in, stride_w, stride_out);
