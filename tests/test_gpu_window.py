@@ -26,6 +26,7 @@ def windows(N, width):
 @pytest.mark.parametrize("N,H,Dh,kind", [(1, 16, 64, "full"), (37, 16, 64, "full"),
                                           (390, 16, 64, "full"), (390, 16, 64, "w104"),
                                           (1500, 16, 64, "w104"), (300, 8, 128, "ragged"),
+                                          (300, 8, 64, "ragged"), (150, 4, 64, "clamp"),
                                           (257, 16, 64, "empty")])
 def test_window_attention_vs_oracle(N, H, Dh, kind):
     r = SplitMix64(N * 3 + H + Dh)
@@ -38,11 +39,17 @@ def test_window_attention_vs_oracle(N, H, Dh, kind):
         a = (r.uniform(N) * N).astype(np.int32)
         b = (r.uniform(N) * N).astype(np.int32)
         ss, se = np.minimum(a, b), np.maximum(a, b) + 1
+    elif kind == "clamp":  # ranges reaching outside [0, N) are clamped into it
+        ss = (r.uniform(N) * 2 * N).astype(np.int32) - N
+        se = ss + (r.uniform(N) * 2 * N).astype(np.int32)
     else:  # every 7th query has an empty window
         ss, se = windows(N, 50)
         se[::7] = ss[::7]
     scale = 1.0 / np.sqrt(Dh)
-    ref = orc.window_attention(q, k, v, ss, se, scale)
+    # the device clamps each range into [0, N) (the reference reads outside it); the oracle
+    # gets the clamped ranges
+    cs = np.clip(ss, 0, N).astype(np.int32)
+    ref = orc.window_attention(q, k, v, cs, np.clip(se, cs, N).astype(np.int32), scale)
     out = empty((N, H, Dh), np.float32)
     say("window attention", N, H, Dh, kind)
     WindowAttention(up(q), up(k), up(v), out, up(ss), up(se), N, H, Dh, scale)
