@@ -135,7 +135,9 @@ struct Chunk {
 };
 
 // Loads one 32-key chunk starting at absolute key c (rows resolved through row_lds).
-// Octet layout: lane o of a key's 8 lanes reads bytes 128*cc + 16*o of the row.
+// Octet layout: lane o of a key's 8 lanes reads bytes 128*cc + 16*o of the row.  Keys at or
+// past `end` load the row of key end-1 instead (branch-free, always in bounds): their scores
+// are masked to -inf, so their weights are exactly 0 and the finite row adds nothing.
 template <int DH, typename KV>
 __device__ __forceinline__ void load_chunk(Chunk<DH, KV>& ch, const KV* kbase, const KV* vbase,
                                            const int* row_lds, long rs, int c, int t0, int end,
@@ -146,29 +148,24 @@ __device__ __forceinline__ void load_chunk(Chunk<DH, KV>& ch, const KV* kbase, c
   const long rb0 = row_lds[g0];
   const long rb1 = CK::CH > 16 ? row_lds[g0 + 1] : rb0;
   const int o = lane & 7;
+  const int last = end - 1 - c;  // last valid key within the chunk (>= 0)
 #pragma unroll
   for (int i = 0; i < CK::NIQ; ++i) {
-    const int kk = 8 * i + (lane >> 3);  // key within the chunk
+    const int kk = min(8 * i + (lane >> 3), last);  // key within the chunk
     const long row = (kk < 16 ? rb0 : rb1) + (kk & 15);
     const KV* src = kbase + row * rs + EPV * o;
-    if (c + kk < end) {
 #pragma unroll
-      for (int cc = 0; cc < CK::NCQ; ++cc) ch.k[i][cc] = load_nt(src + 8 * EPV * cc);
-    } else {
-#pragma unroll
-      for (int cc = 0; cc < CK::NCQ; ++cc) ch.k[i][cc] = make_uint4(0, 0, 0, 0);
-    }
+    for (int cc = 0; cc < CK::NCQ; ++cc) ch.k[i][cc] = load_nt(src + 8 * EPV * cc);
   }
   const int dg = lane % CK::LPT;
   const int r = lane / CK::LPT;
 #pragma unroll
   for (int i = 0; i < CK::NIV; ++i) {
-    const int kk = CK::TPI * i + r;
+    const int kk = min(CK::TPI * i + r, last);
     const long row = (kk < 16 ? rb0 : rb1) + (kk & 15);
     const KV* src = vbase + row * rs + 8 * dg;
 #pragma unroll
-    for (int u = 0; u < CK::NV; ++u)
-      ch.v[i][u] = c + kk < end ? load_nt(src + EPV * u) : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < CK::NV; ++u) ch.v[i][u] = load_nt(src + EPV * u);
   }
 }
 
@@ -351,7 +348,7 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: wave-level branches
   const int Hq = a.Hkv * G;
 
   // ---- first pool row of every 16-key group of the split (pages hold >= 16 aligned keys) ----
