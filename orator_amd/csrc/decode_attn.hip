@@ -9,9 +9,10 @@
 // Design (HBM-bound, ~2 flop/byte):
 //  * one workgroup = (split of SPLIT keys, kv head, stream), 4 wave64s; each wave streams
 //    a contiguous quarter of the split in 32-key chunks.  All G q heads of the GQA group
-//    consume every K/V row the wave loads, so K/V leave HBM exactly once.
-//  * software pipeline: the K and V loads of chunk c+1 are issued before chunk c is
-//    computed, so every wave keeps 16 KB in flight while it does arithmetic.
+//    consume every K/V row the wave loads, so K/V leave HBM exactly once.  At the default
+//    128-key splits every wave issues its whole chunk (16 KB of K and V) at once.
+//  * longer splits: software pipeline, the K and V loads of chunk c+1 are issued before
+//    chunk c is computed (two chunk buffers).
 //  * QK, "octet" layout: 8 lanes per key, each lane 2 x 16-byte loads (one contiguous
 //    128-byte half row per instruction and octet); dot reduced with 3 DPP steps.
 //  * online softmax per wave (running max / sum, accumulator rescale once per chunk);
@@ -22,8 +23,10 @@
 //    round trip for up to 16 splits: all loads issued together, online max).  (A
 //    last-workgroup merge in the same launch needs a device-scope release fence per
 //    workgroup -- an L2 write-back on gfx950 -- and measured 7-10x slower.)
-//  * paged KV: the split's page rows are resolved once into LDS, so no K/V load waits
-//    on a page-table load.
+//  * paged KV: each wave reads the two page-table entries of its chunk with uniform loads
+//    at entry, together with the stream's position; no workgroup-wide table and no barrier
+//    stand between the entry and the K/V loads.  Keys past the range load the last valid
+//    row (branch-free; their weights are 0).
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -90,19 +93,41 @@ __device__ __forceinline__ void qk_norm_rope_octet(float (&x)[16], const float* 
   }
 }
 
-// Number of keys stream b attends, clamped to the capacity.
-__device__ __forceinline__ int stream_keys(const DecodeArgs& a, int b) {
+// Number of keys stream b attends, clamped to the capacity; pos_b = pos[b] (pos_mode 0).
+__device__ __forceinline__ int stream_keys(const DecodeArgs& a, int b, int pos_b) {
   if (a.pos_mode == 3) {  // window [seg_start, seg_end) clamped into [0, capacity)
     const int j0 = min(max(a.seg_start[b], 0), a.capacity);
     return min(max(a.seg_end[b], j0), a.capacity) - j0;
   }
-  const int S = a.pos_mode == 0 ? a.pos[b] + 1 : (a.pos_mode == 1 ? b + 1 : a.capacity);
+  const int S = a.pos_mode == 0 ? pos_b + 1 : (a.pos_mode == 1 ? b + 1 : a.capacity);
   return S > a.capacity ? a.capacity : S;
 }
 
 // First key row of stream b's range (non-zero only for windows).
 __device__ __forceinline__ int stream_key0(const DecodeArgs& a, int b) {
   return a.pos_mode == 3 ? min(max(a.seg_start[b], 0), a.capacity) : 0;
+}
+
+// Pool rows of keys c and c + 16 (c a multiple of 16) of stream b, whose range starts at pool
+// key key0 (windows; 0 otherwise): through the page table for paged caches (pages hold >= 16
+// aligned keys), else the key offset by key0.  Both table indices are clamped into the table
+// (capacity - 1 at most) and depend on nothing loaded, so the two reads go out together at
+// entry; a row past the stream's keys is never dereferenced (the chunk loads clamp to the
+// last valid key).  Called with wave-uniform arguments: no workgroup-wide table, no barrier.
+__device__ __forceinline__ void chunk_rows(const DecodeArgs& a, int b, int key0, int c, long& r0,
+                                           long& r1) {
+  const int lim = a.capacity - 1;
+  const int j0 = min(c, lim) & ~15, j1 = min(c + 16, lim) & ~15;
+  if (a.page_table) {
+    const int* pt = a.page_table + static_cast<long>(b) * a.max_pages;
+    const int p0 = pt[j0 >> a.page_shift], p1 = pt[j1 >> a.page_shift];
+    const int msk = (1 << a.page_shift) - 1;
+    r0 = static_cast<long>((p0 << a.page_shift) | (j0 & msk));
+    r1 = static_cast<long>((p1 << a.page_shift) | (j1 & msk));
+  } else {
+    r0 = j0 + key0;
+    r1 = j1 + key0;
+  }
 }
 
 // Element helpers: K/V rows are bf16 (cache) or fp32 (self-attention over fp32 K/V).
@@ -134,19 +159,17 @@ struct Chunk {
   uint4 v[NIV][NV];
 };
 
-// Loads one 32-key chunk starting at absolute key c (rows resolved through row_lds).
+// Loads one 32-key chunk starting at absolute key c; rb0 / rb1 are the pool rows of keys c and
+// c + 16.
 // Octet layout: lane o of a key's 8 lanes reads bytes 128*cc + 16*o of the row.  Keys at or
 // past `end` load the row of key end-1 instead (branch-free, always in bounds): their scores
 // are masked to -inf, so their weights are exactly 0 and the finite row adds nothing.
 template <int DH, typename KV>
 __device__ __forceinline__ void load_chunk(Chunk<DH, KV>& ch, const KV* kbase, const KV* vbase,
-                                           const int* row_lds, long rs, int c, int t0, int end,
+                                           long rb0, long rb1, long rs, int c, int end,
                                            int lane) {
   using CK = Chunk<DH, KV>;
   constexpr int EPV = CK::EPV;
-  const int g0 = (c - t0) >> 4;
-  const long rb0 = row_lds[g0];
-  const long rb1 = CK::CH > 16 ? row_lds[g0 + 1] : rb0;
   const int o = lane & 7;
   const int last = end - 1 - c;  // last valid key within the chunk (>= 0)
 #pragma unroll
@@ -323,44 +346,36 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   constexpr int NW = decode_waves<SPLIT, KV, G>();
   constexpr int NT = 64 * NW;
   constexpr int TPW = SPLIT / NW;  // keys per wave
-  constexpr int NG = SPLIT / 16;   // 16-key groups per split
   static_assert(TPW % CK::CH == 0, "a wave covers whole chunks");
 
   __shared__ float red_o[NW][G][DH];
   __shared__ float red_ml[NW][G][2];
-  __shared__ int row_lds[NG];
 
   // split index slowest: the short last splits of the streams are dispatched last, where
   // they fill the drain of the final round instead of lengthening it
   const int kvh = blockIdx.x;
   const int b = blockIdx.y;
   const int split = blockIdx.z;
-  int S = stream_keys(a, b);
+  const int t0 = split * SPLIT;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: wave-level branches
+  // the stream's position and the pool rows of the wave's first chunk (keys w0, w0 + 16):
+  // independent uniform loads, issued together before anything else
+  const int pos_b = a.pos_mode == 0 ? a.pos[b] : 0;
+  const int key0 = stream_key0(a, b);
+  long wr0, wr1;
+  chunk_rows(a, b, key0, t0 + wave * TPW, wr0, wr1);
+  int S = stream_keys(a, b, pos_b);
   if (S <= 0) {  // no keys: the reference's 1/sum guard yields zeros
     if (split == 0)
       for (int idx = threadIdx.x; idx < G * DH; idx += NT)
         a.out[(static_cast<long>(b) * a.Hkv * G + kvh * G) * DH + idx] = 0.0f;
     return;
   }
-  const int t0 = split * SPLIT;
   if (t0 >= S) return;
   const int n_splits = (S + SPLIT - 1) / SPLIT;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: wave-level branches
   const int Hq = a.Hkv * G;
-
-  // ---- first pool row of every 16-key group of the split (pages hold >= 16 aligned keys) ----
-  if (tid < NG) {
-    const int j0 = t0 + 16 * tid;
-    int row = j0 + stream_key0(a, b);
-    if (a.page_table && j0 < S) {
-      const int page = a.page_table[static_cast<long>(b) * a.max_pages + (j0 >> a.page_shift)];
-      row = (page << a.page_shift) | (j0 & ((1 << a.page_shift) - 1));
-    }
-    row_lds[tid] = row;
-  }
 
   // ---- q of the G heads, octet layout: lane owns dims 8*EPV*cc + EPV*o + e ----
   const int o = lane & 7;
@@ -381,11 +396,10 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   }
   const float* rope_cs = nullptr;  // (cos, sin) pairs of this stream's position (QKN)
   if constexpr (QKN) {
-    rope_cs = a.rope + static_cast<long>(min(max(a.pos[b], 0), a.capacity - 1)) * DH;
+    rope_cs = a.rope + static_cast<long>(min(max(pos_b, 0), a.capacity - 1)) * DH;
 #pragma unroll
     for (int g = 0; g < G; ++g) qk_norm_rope_octet(qr[g], a.q_norm, a.eps, rope_cs, o);
   }
-  lds_barrier();  // row_lds ready (the q loads may still be in flight)
 
   const long kv_base = (a.page_table ? 0 : static_cast<long>(b) * a.stream_stride) +
                        static_cast<long>(kvh) * DH;
@@ -397,7 +411,7 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   // wave whose range would hold the new key folds it in afterwards.
   int new_key = -1;
   if constexpr (sizeof(KV) == 2)
-    if (a.k_new && S == a.pos[b] + 1) new_key = S - 1;
+    if (a.k_new && S == pos_b + 1) new_key = S - 1;
   const int S_cache = new_key >= 0 ? S - 1 : S;
   const int w0 = t0 + wave * TPW;
   const int w_end = min(w0 + TPW, S_cache);
@@ -423,22 +437,28 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
     // one chunk per wave (128-key splits): no second buffer
     if (w0 < w_end) {
       CK A;
-      load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, w0, t0, w_end, lane);
+      load_chunk<DH, KV>(A, kbase, vbase, wr0, wr1, rs, w0, w_end, lane);
       process_chunk<DH, G, KV>(A, qr, m, lpart, acc, w0, w_end, lane, a.scale_log2e);
     }
   } else if (w0 < w_end) {
     // Ping-pong buffers: the loads of one chunk are in flight while the other is computed.
     CK A, Bb;
-    load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, w0, t0, w_end, lane);
+    load_chunk<DH, KV>(A, kbase, vbase, wr0, wr1, rs, w0, w_end, lane);
     int c = w0;
     while (true) {
-      if (c + CK::CH < w_end)
-        load_chunk<DH, KV>(Bb, kbase, vbase, row_lds, rs, c + CK::CH, t0, w_end, lane);
+      if (c + CK::CH < w_end) {
+        long r0, r1;
+        chunk_rows(a, b, key0, c + CK::CH, r0, r1);
+        load_chunk<DH, KV>(Bb, kbase, vbase, r0, r1, rs, c + CK::CH, w_end, lane);
+      }
       process_chunk<DH, G, KV>(A, qr, m, lpart, acc, c, w_end, lane, a.scale_log2e);
       c += CK::CH;
       if (c >= w_end) break;
-      if (c + CK::CH < w_end)
-        load_chunk<DH, KV>(A, kbase, vbase, row_lds, rs, c + CK::CH, t0, w_end, lane);
+      if (c + CK::CH < w_end) {
+        long r0, r1;
+        chunk_rows(a, b, key0, c + CK::CH, r0, r1);
+        load_chunk<DH, KV>(A, kbase, vbase, r0, r1, rs, c + CK::CH, w_end, lane);
+      }
       process_chunk<DH, G, KV>(Bb, qr, m, lpart, acc, c, w_end, lane, a.scale_log2e);
       c += CK::CH;
       if (c >= w_end) break;
@@ -450,7 +470,9 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
       append_key<DH, G, QKN>(kn, vn, qr, m, lpart, acc, lane, a.scale_log2e, kw, vw, a.k_norm,
                              a.eps, rope_cs);
       // write the new row into the cache (dropped past the pool, as the KV write does)
-      const long row = row_lds[(new_key - t0) >> 4] + (new_key & 15);
+      long row, row_unused;
+      chunk_rows(a, b, key0, new_key & ~15, row, row_unused);
+      row += new_key & 15;
       if (row < a.pool_rows) {
         uint16_t* kdst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(kbase)) + row * rs;
         uint16_t* vdst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(vbase)) + row * rs;
@@ -527,7 +549,7 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
   constexpr int kBatch = 17;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int S = stream_keys(a, b);
+  const int S = stream_keys(a, b, a.pos_mode == 0 ? a.pos[b] : 0);
   const int n_splits = (S + split_len - 1) / split_len;
   if (n_splits <= 1) return;  // written directly by the split kernel
   const long bh = static_cast<long>(b) * Hq + h;
