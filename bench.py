@@ -44,7 +44,7 @@ LAYERS, B, HQ, HKV, DH, L_BASE, PAGE = 28, 16, 16, 8, 128, 4096, 16
 # HBM bytes per decode op measured with rocprofv3 --pmc at S = 4102 (FETCH_SIZE x 1.994 KiB +
 # WRITE_SIZE KiB, profiles/decode_b16_l4096_hbm_traffic.md) and the algorithmic bytes of the
 # same op, for the traffic / algorithmic ratio
-HBM_TRAFFIC_PER_OP = 277.6e6
+HBM_TRAFFIC_PER_OP = 277.8e6
 ALGORITHMIC_AT_TRAFFIC = 269.1e6
 
 
