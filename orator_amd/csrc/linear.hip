@@ -225,7 +225,13 @@ int launch_fused_u(const float* x, const float* aux, float eps, const uint16_t* 
                    int K, int N, bool pair, hipStream_t s) {
   // rows per wave: enough waves to cover the chip for small N, fewer input-row rebuilds
   // (one per workgroup) for the vocabulary-sized projection
-  if (pair) {
+  if (pair && U == 4) {
+    // two gate|up output pairs per wave (4 weight rows): the 6144-pair projection is 768
+    // workgroups, one round at 3 per CU (one pair per wave needed 1536, a 5-per-CU round
+    // plus a sparse tail)
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 4, ACC, U, true>), dim3((N + 7) / 8), dim3(256),
+                       0, s, x, aux, eps, W, out, K, N);
+  } else if (pair) {
     hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC, U, true>), dim3((N + 3) / 4), dim3(256),
                        0, s, x, aux, eps, W, out, K, N);
   } else if (N >= 32768) {
