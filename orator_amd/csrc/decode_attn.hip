@@ -549,9 +549,6 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
   constexpr int kBatch = 17;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int S = stream_keys(a, b, a.pos_mode == 0 ? a.pos[b] : 0);
-  const int n_splits = (S + split_len - 1) / split_len;
-  if (n_splits <= 1) return;  // written directly by the split kernel
   const long bh = static_cast<long>(b) * Hq + h;
   const long base = bh * a.max_splits;
   const int d = threadIdx.x;
@@ -559,15 +556,23 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
   struct Batch {
     float m[kBatch], l[kBatch], o[kBatch];
   };
+  // Addresses use the launch's split count, not the stream's, so the first batch goes out
+  // together with the read of the stream's position instead of after it; slots past the
+  // stream's splits hold stale data and are excluded by selects (no arithmetic on them).
   auto load = [&](Batch& x, int s0) {
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      const long ps = base + min(s0 + i, n_splits - 1);  // in-range address for every i
+      const long ps = base + min(s0 + i, a.max_splits - 1);  // in-range address for every i
       x.m[i] = a.part_ml[ps * 2];
       x.l[i] = a.part_ml[ps * 2 + 1];
       x.o[i] = a.part_o[ps * DH + d];
     }
   };
+  Batch A, Bb;
+  load(A, 0);
+  const int S = stream_keys(a, b, a.pos_mode == 0 ? a.pos[b] : 0);
+  const int n_splits = (S + split_len - 1) / split_len;
+  if (n_splits <= 1) return;  // written directly by the split kernel
   auto fold = [&](const Batch& x, int s0) {
     float mx = M;
 #pragma unroll
@@ -578,15 +583,15 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
     L *= c_old;
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      const float w = s0 + i < n_splits ? fast_exp2(x.m[i] - mx) : 0.0f;
-      acc = fmaf(w, x.o[i], acc);
-      L = fmaf(w, x.l[i], L);
+      if (s0 + i < n_splits) {
+        const float w = fast_exp2(x.m[i] - mx);
+        acc = fmaf(w, x.o[i], acc);
+        L = fmaf(w, x.l[i], L);
+      }
     }
     M = mx;
   };
-  // ping-pong: the next 16 splits' loads are issued before the current 16 are folded
-  Batch A, Bb;
-  load(A, 0);
+  // ping-pong: the next batch's loads are issued before the current one is folded
   for (int s0 = 0;;) {
     if (s0 + kBatch < n_splits) load(Bb, s0 + kBatch);
     fold(A, s0);
