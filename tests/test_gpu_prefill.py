@@ -156,3 +156,25 @@ def test_prefill_2048_bf16():
     say("prefill 2048 bf16")
     got = _run(q, kc, vc, 0, T, da.PREFILL_BF16, Hkv)
     assert np.max(np.abs(got - ref)) <= TOL16
+
+
+@pytest.mark.parametrize("S", [513, 4097])
+def test_decode_equals_last_prefill_row(S):
+    """A size-independent invariant at the decode target size: decode at position p attends
+    the same keys [0, p] as the last row of a causal prefill ending at p, so the two kernels
+    (split-K decode, MFMA prefill in fp32 mode) agree to the sum of their tolerances; each is
+    also checked against the oracle's decode."""
+    T, Hq, Hkv, Dh = 4, 16, 8, 128
+    pos0 = S - T
+    q, kc, vc = _layer_inputs(S, T, pos0)
+    scale = 1.0 / math.sqrt(Dh)
+    say("decode vs prefill last row", S)
+    pre = _run(q, kc, vc, pos0, S, da.PREFILL_FP32, Hkv)[T - 1]
+    dout = empty((Hq, Dh), np.float32)
+    da.GqaDecodeAttn(up(np.ascontiguousarray(q[T - 1])), up(kc), up(vc), dout, Hq, Hkv, Dh,
+                     up(np.array([S - 1], np.int32)), S, scale)
+    dec = down(dout, (Hq, Dh))
+    ref = orc.gqa_decode(q[T - 1], kc, vc, S - 1, scale)
+    assert rel_err(dec, ref, FLOOR) <= TOL32
+    assert rel_err(pre, ref, FLOOR) <= TOL32
+    assert rel_err(pre, dec, FLOOR) <= 2 * TOL32
