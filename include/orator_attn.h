@@ -148,8 +148,9 @@ int orator_gqa_decode_append(const float* q, const float* k_new, const float* v_
                              uint16_t* kc, uint16_t* vc, float* out, int Hq, int Hkv, int Dh,
                              const int* d_pos, int capacity, float scale, void* stream);
 /* Batched paged form: stream b appends k_new/v_new [B, Hkv, Dh] at d_pos[b] through page-table
- * row b and attends d_pos[b] + 1 keys.  Rows of pages >= n_pages are not written (as
- * orator_kv_write_paged). */
+ * row b and attends d_pos[b] + 1 keys.  A new row whose page-table entry is unmapped (< 0) or
+ * >= n_pages is not written (as orator_kv_write_paged), but is still attended; every earlier
+ * position's page must be mapped. */
 int orator_gqa_decode_append_paged(const float* q, const float* k_new, const float* v_new,
                                    uint16_t* kpool, uint16_t* vpool, const int* page_table,
                                    int max_pages, int page_size, int n_pages, const int* d_pos,

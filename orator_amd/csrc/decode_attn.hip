@@ -122,8 +122,9 @@ __device__ __forceinline__ void chunk_rows(const DecodeArgs& a, int b, int key0,
     const int* pt = a.page_table + static_cast<long>(b) * a.max_pages;
     const int p0 = pt[j0 >> a.page_shift], p1 = pt[j1 >> a.page_shift];
     const int msk = (1 << a.page_shift) - 1;
-    r0 = static_cast<long>((p0 << a.page_shift) | (j0 & msk));
-    r1 = static_cast<long>((p1 << a.page_shift) | (j1 & msk));
+    // long arithmetic: an unmapped page (< 0) yields a negative row, never a wrapped one
+    r0 = static_cast<long>(p0) * (1L << a.page_shift) + (j0 & msk);
+    r1 = static_cast<long>(p1) * (1L << a.page_shift) + (j1 & msk);
   } else {
     r0 = j0 + key0;
     r1 = j1 + key0;
@@ -469,11 +470,12 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
       uint4 kw[CK::NCQ], vw;
       append_key<DH, G, QKN>(kn, vn, qr, m, lpart, acc, lane, a.scale_log2e, kw, vw, a.k_norm,
                              a.eps, rope_cs);
-      // write the new row into the cache (dropped past the pool, as the KV write does)
+      // write the new row into the cache; a row outside the pool (an unmapped page, < 0, or
+      // a page past the pool) is dropped, as the KV write does
       long row, row_unused;
       chunk_rows(a, b, key0, new_key & ~15, row, row_unused);
       row += new_key & 15;
-      if (row < a.pool_rows) {
+      if (row >= 0 && row < a.pool_rows) {
         uint16_t* kdst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(kbase)) + row * rs;
         uint16_t* vdst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(vbase)) + row * rs;
         if (lane < 8)
@@ -722,7 +724,7 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (max_splits > 1024) return fail(ORATOR_ERR_CAPACITY, "gqa_decode: more than 1024 splits");
   const size_t part_o = static_cast<size_t>(p.B) * p.Hq * max_splits * p.Dh * sizeof(float);
   const size_t part_ml = static_cast<size_t>(p.B) * p.Hq * max_splits * 2 * sizeof(float);
-  char* ws = static_cast<char*>(workspace(stream, part_o + part_ml, 0));
+  char* ws = static_cast<char*>(workspace(stream, part_o + part_ml));
   if (!ws) return ORATOR_ERR_HIP;
 
   DecodeArgs args;

@@ -31,6 +31,9 @@
 namespace orator_hip {
 namespace {
 
+// Longest context a decoder accepts: the decode split merge covers 1024 splits of 128 keys.
+constexpr int kDecoderMaxSeq = 131072;
+
 template <typename T>
 int dalloc(T** p, size_t n) {
   *p = nullptr;
@@ -73,7 +76,11 @@ struct Decoder {
   ~Decoder() {
     if (graph) (void)hipGraphExecDestroy(graph);
     if (graph_banned) (void)hipGraphExecDestroy(graph_banned);
-    if (capture_stream) (void)hipStreamDestroy(capture_stream);
+    if (capture_stream) {
+      // the graphs are gone: the capture stream's workspace (decode partials) goes too
+      (void)workspace_release(capture_stream);
+      (void)hipStreamDestroy(capture_stream);
+    }
     for (auto* p : kc) (void)hipFree(p);
     for (auto* p : vc) (void)hipFree(p);
     free_prefill();
@@ -408,6 +415,8 @@ int orator_decoder_create(const OratorDecoderConfig* cfg, const uint16_t* embed,
   if (c.num_layers <= 0 || c.hidden_size <= 0 || c.num_q_heads <= 0 || c.num_kv_heads <= 0 ||
       c.intermediate_size <= 0 || c.vocab_size <= 0 || c.max_seq_len <= 0)
     return fail(ORATOR_ERR_INVALID, "decoder_create: sizes must be positive");
+  if (c.max_seq_len > kDecoderMaxSeq)
+    return fail(ORATOR_ERR_UNSUPPORTED, "decoder_create: max_seq_len above 131072");
   if (c.head_dim != 128 || c.num_q_heads % c.num_kv_heads || c.hidden_size % 8 ||
       c.intermediate_size % 8 || c.hidden_size > kFusedMaxK || c.intermediate_size > kFusedMaxK ||
       c.num_q_heads * c.head_dim > kFusedMaxK)

@@ -638,7 +638,7 @@ int orator_argmax_banned(const float* logits, int n, int ban0, int ban1, int* ou
   const hipStream_t s = static_cast<hipStream_t>(stream);
   void* scratch = nullptr;
   if (argmax_scratch_bytes(n)) {
-    scratch = workspace(s, argmax_scratch_bytes(n), 0);
+    scratch = workspace(s, argmax_scratch_bytes(n));
     if (!scratch) return ORATOR_ERR_HIP;
   }
   return launch_argmax_banned(logits, n, ban0, ban1, out_idx, scratch, s);

@@ -20,11 +20,14 @@ int check_hip(hipError_t e, const char* what);
 // Checks hipGetLastError() after a launch.
 int check_launch(const char* what);
 
-// Device scratch owned by the library, one block per (device, stream), grown on
-// demand.  The first `counter_bytes` are zeroed when the block is (re)allocated and
-// every kernel that uses them leaves them zero again.  Returns nullptr on failure
-// (the error is recorded).
-void* workspace(hipStream_t stream, size_t bytes, size_t counter_bytes);
+// Device scratch owned by the library, one block per (device, stream, host thread), grown
+// on demand; a grown block's old memory is kept (queued work or a captured graph may still
+// read it) until workspace_release(stream).  Returns nullptr on failure (the error is
+// recorded).
+void* workspace(hipStream_t stream, size_t bytes);
+// Frees every workspace block of `stream` (all threads, current and retired) after the
+// stream's queued work; for the owner of a stream about to be destroyed.
+int workspace_release(hipStream_t stream);
 
 inline int ilog2_exact(int v) {
   if (v <= 0 || (v & (v - 1))) return -1;

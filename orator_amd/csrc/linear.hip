@@ -455,7 +455,7 @@ int orator_linear(const float* in_f32, const uint16_t* W_bf16, const float* bias
   if (!in_f32) return fail(ORATOR_ERR_INVALID, "linear: null pointer");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const long n = static_cast<long>(M) * K;
-  uint16_t* in_bf16 = static_cast<uint16_t*>(workspace(s, n * sizeof(uint16_t), 0));
+  uint16_t* in_bf16 = static_cast<uint16_t*>(workspace(s, n * sizeof(uint16_t)));
   if (!in_bf16) return ORATOR_ERR_HIP;
   if (int rc = orator_f32_to_bf16(in_f32, in_bf16, n, stream)) return rc;
   return launch_linear_pre(in_bf16, W_bf16, bias, out, M, K, N, act, s);

@@ -626,8 +626,9 @@ int launch_prefill(const float* q, const uint16_t* q_bf16, const uint16_t* kpool
     return fail(ORATOR_ERR_INVALID, "gqa_prefill: unknown precision mode");
   if (capacity <= 0) return fail(ORATOR_ERR_INVALID, "gqa_prefill: capacity must be > 0");
   if (!(scale > 0.0f)) return fail(ORATOR_ERR_INVALID, "gqa_prefill: scale must be > 0");
-  if (capacity > 16 * kMaxRowGroups)
-    return fail(ORATOR_ERR_UNSUPPORTED, "gqa_prefill: more than 16384 cached keys");
+  // the LDS page-row table of a paged cache covers 16384 keys; contiguous rows are arithmetic
+  if (page_table && capacity > 16 * kMaxRowGroups)
+    return fail(ORATOR_ERR_UNSUPPORTED, "gqa_prefill: paged caches hold at most 16384 keys");
   PrefillArgs args{};
   args.page_shift = 0;
   if (page_table) {

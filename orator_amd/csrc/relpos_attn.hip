@@ -104,7 +104,7 @@ int relpos_fp32(const float* q, const float* k, const float* v, const float* p, 
   const size_t td = static_cast<size_t>(H) * T * Dk, pd = static_cast<size_t>(H) * P * Dk;
   const size_t tt = static_cast<size_t>(H) * T * T, tp = static_cast<size_t>(H) * T * P;
   const size_t floats = 4 * td + pd + td /*vt*/ + tt + tp;
-  float* ws = static_cast<float*>(workspace(stream, floats * sizeof(float), 0));
+  float* ws = static_cast<float*>(workspace(stream, floats * sizeof(float)));
   if (!ws) return ORATOR_ERR_HIP;
   float* qu = ws;
   float* qv = qu + td;
@@ -235,6 +235,7 @@ struct RelPosArgs {
   float* out;
   int T, H, valid;
   float scale_log2e;
+  int uniform;  // every key masked (valid_len <= 0): all T scores equal, softmax = mean of V
 };
 
 template <typename IN>
@@ -352,7 +353,8 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
     for (int e = 0; e < 16; ++e) {
       const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
       const float bd = rt_lds[wave][col][jl - col + 31];
-      const float x = (q_ok && j0 + jl < a.valid) ? (s[e] + bd) * a.scale_log2e : -INFINITY;
+      const float sc = a.uniform ? 0.0f : (s[e] + bd) * a.scale_log2e;
+      const float x = (q_ok && j0 + jl < a.valid) ? sc : -INFINITY;
       s[e] = x;
       tmax = fmaxf(tmax, x);
     }
@@ -440,8 +442,12 @@ int orator_relpos_attention_fast(const void* q, const void* k, const void* v, co
   if (!q || !k || !v || !p || !pos_bias_u || !pos_bias_v || !out)
     return fail(ORATOR_ERR_INVALID, "relpos_attention_fast: null pointer");
   if (Dk != kRpDk) return fail(ORATOR_ERR_UNSUPPORTED, "relpos_attention_fast: Dk must be 64");
-  RelPosArgs args{q, k, v, p, pos_bias_u, pos_bias_v, out, T, H, valid_len > T ? T : valid_len,
-                  scale * 1.4426950408889634f};
+  // The reference masks keys >= valid_len with a finite -1e30 (conformer_layer.cu:140-143):
+  // with no valid key every score is the same and the softmax averages V over all T keys.
+  const bool none_valid = valid_len <= 0;
+  RelPosArgs args{q, k, v, p, pos_bias_u, pos_bias_v, out, T, H,
+                  none_valid ? T : (valid_len > T ? T : valid_len), scale * 1.4426950408889634f,
+                  none_valid ? 1 : 0};
   const dim3 grid(((T + 31) / 32) * H);
   if (in_f16)
     hipLaunchKernelGGL(relpos_fused_kernel<_Float16>, grid, dim3(64 * kRpWaves), 0,

@@ -1,27 +1,32 @@
-// Library runtime: error reporting, the per-(device, stream) workspace and the small
+// Library runtime: error reporting, the per-(device, stream, thread) workspace and the small
 // device-plumbing surface of the C ABI (allocation, copies, streams, events).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
-#include <map>
 #include <atomic>
-#include <mutex>
+#include <thread>
 #include <string>
 #include <utility>
 
 #include "internal.hpp"
+#include "workspace_pool.hpp"
 
 namespace orator_hip {
 
 namespace {
 thread_local std::string g_last_error;
 
-struct Block {
-  void* ptr = nullptr;
-  size_t bytes = 0;
-};
-std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, Block> g_ws;
+int ws_alloc(void** p, size_t bytes) { return hipMalloc(p, bytes) == hipSuccess ? 0 : 1; }
+void ws_free(void* p) { (void)hipFree(p); }
+int ws_sync(const void* stream) {
+  return hipStreamSynchronize(static_cast<hipStream_t>(const_cast<void*>(stream))) == hipSuccess
+             ? 0
+             : 1;
+}
+WorkspacePool& ws_pool() {
+  static WorkspacePool* pool = new WorkspacePool(ws_alloc, ws_free, ws_sync);  // never destroyed:
+  return *pool;  // blocks may be in use until the process ends
+}
 thread_local hipEvent_t g_ev_start = nullptr, g_ev_split = nullptr, g_ev_stop = nullptr;
 }  // namespace
 
@@ -55,28 +60,20 @@ int device_cu_count() {
   return n;
 }
 
-void* workspace(hipStream_t stream, size_t bytes, size_t counter_bytes) {
+void* workspace(hipStream_t stream, size_t bytes) {
   int dev = 0;
   if (check_hip(hipGetDevice(&dev), "hipGetDevice") != ORATOR_OK) return nullptr;
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  Block& blk = g_ws[{dev, stream}];
-  if (blk.bytes >= bytes) return blk.ptr;
-  if (blk.ptr) {
-    // The old block may still be read by queued work on this stream.
-    if (check_hip(hipStreamSynchronize(stream), "workspace sync") != ORATOR_OK) return nullptr;
-    if (check_hip(hipFree(blk.ptr), "workspace free") != ORATOR_OK) return nullptr;
-    blk = Block{};
-  }
-  void* p = nullptr;
-  if (check_hip(hipMalloc(&p, bytes), "workspace hipMalloc") != ORATOR_OK) return nullptr;
-  if (counter_bytes &&
-      check_hip(hipMemsetAsync(p, 0, counter_bytes, stream), "workspace zero") != ORATOR_OK) {
-    (void)hipFree(p);
-    return nullptr;
-  }
-  blk.ptr = p;
-  blk.bytes = bytes;
+  std::string err;
+  void* p = ws_pool().get(WsKey{dev, stream, std::this_thread::get_id()}, bytes, &err);
+  if (!p) (void)fail(ORATOR_ERR_HIP, err);
   return p;
+}
+
+int workspace_release(hipStream_t stream) {
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  return ws_pool().release_stream(dev, stream) ? fail(ORATOR_ERR_HIP, "workspace release: sync")
+                                               : ORATOR_OK;
 }
 
 }  // namespace orator_hip
@@ -146,7 +143,10 @@ int orator_stream_create(void** stream) {
 }
 
 int orator_stream_destroy(void* stream) {
-  return check_hip(hipStreamDestroy(static_cast<hipStream_t>(stream)), "hipStreamDestroy");
+  // the stream's workspace blocks go with it (graphs captured on it must be destroyed first)
+  const int rc = orator_hip::workspace_release(static_cast<hipStream_t>(stream));
+  const int rc2 = check_hip(hipStreamDestroy(static_cast<hipStream_t>(stream)), "hipStreamDestroy");
+  return rc ? rc : rc2;
 }
 
 int orator_stream_synchronize(void* stream) {
@@ -210,8 +210,8 @@ int orator_time_next_decode(void* start, void* split_end, void* stop) {
 }
 
 int orator_workspace_reserve(size_t bytes, void* stream) {
-  return orator_hip::workspace(static_cast<hipStream_t>(stream), bytes, 0) ? ORATOR_OK
-                                                                           : ORATOR_ERR_HIP;
+  return orator_hip::workspace(static_cast<hipStream_t>(stream), bytes) ? ORATOR_OK
+                                                                        : ORATOR_ERR_HIP;
 }
 
 }  // extern "C"

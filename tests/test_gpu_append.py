@@ -115,3 +115,39 @@ def test_append_equals_write_then_decode_on_device():
     np.testing.assert_array_equal(down(k1, kp.shape, np.uint16), down(k2, kp.shape, np.uint16))
     np.testing.assert_array_equal(down(v1, vp.shape, np.uint16), down(v2, vp.shape, np.uint16))
     assert rel_err(down(o2, (B, Hq, Dh)), down(o1, (B, Hq, Dh)), FLOOR) <= 2e-6
+
+
+@pytest.mark.parametrize("bad", ["unmapped", "past_pool"])
+def test_append_paged_unmapped_page_is_not_written(bad):
+    """The appended position's page-table entry is -1 (unmapped) or names a page past the pool:
+    the new row is not written anywhere (every pool byte unchanged), and it is still attended.
+    Reference: the row is attended from a spare page the oracle maps in its place."""
+    Hq, Hkv, Dh, ps = 16, 8, 128, 16
+    r = SplitMix64(7 if bad == "unmapped" else 8)
+    # each new row is the first of its page (2, 3, 256, 0): earlier positions stay mapped
+    pos = np.array([32, 48, 4096, 0], np.int32)
+    B = len(pos)
+    max_pages = int(pos.max()) // ps + 1
+    n_pages = B * max_pages
+    kp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    vp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    table = np.array(r.uniform(n_pages).argsort(), np.int32).reshape(B, max_pages)
+    bad_entry = -1 if bad == "unmapped" else n_pages + 5
+    ref_table = table.copy()
+    for b in range(B):
+        table[b, pos[b] // ps] = bad_entry
+    q, kn, vn = r.normal((B, Hq, Dh)), r.normal((B, Hkv, Dh)), r.normal((B, Hkv, Dh))
+    scale = 1.0 / math.sqrt(Dh)
+    # oracle: the original (mapped) table; the pages it writes are the ones the device skips
+    kp_ref, vp_ref = kp.copy(), vp.copy()
+    for b in range(B):
+        orc.kv_write_paged(kn[b][None], vn[b][None], kp_ref, vp_ref, ref_table[b], ps, int(pos[b]))
+    ref = orc.gqa_decode_paged(q, kp_ref, vp_ref, ref_table, ps, pos, scale, threads=8)
+    dk, dv = up(kp), up(vp)
+    dout = empty((B, Hq, Dh), np.float32)
+    say("append paged, appended page", bad)
+    da.GqaDecodeAttnAppendPaged(up(q), up(kn), up(vn), dk, dv, up(table), max_pages, ps, n_pages,
+                                up(pos), dout, B, Hq, Hkv, Dh, scale)
+    assert rel_err(down(dout, (B, Hq, Dh)), ref, FLOOR) <= TOL
+    np.testing.assert_array_equal(down(dk, kp.shape, np.uint16), kp)
+    np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp)

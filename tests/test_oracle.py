@@ -373,6 +373,11 @@ def test_relpos_reduces_to_mha_and_masks_keys():
     v2[valid:] = r.normal(v2[valid:].shape)
     b = orc.relpos_attention(q, k2, v2, p, u, vb, valid, 0.125)
     np.testing.assert_array_equal(a, b)
+    # valid = 0: the finite -1e30 mask makes every score equal, so each row is mean(V)
+    # (src/model/conformer_layer.cu:140-143)
+    none = orc.relpos_attention(q, k, v, p, u, vb, 0, 0.125)
+    np.testing.assert_allclose(none, np.broadcast_to(v.astype(np.float64).mean(0), v.shape),
+                               atol=1e-6)
 
 
 # ------------------------------------------------------------------ SGEMM ----
