@@ -114,3 +114,14 @@ def test_linear_and_decoder_validation():
         _lib.ORATOR_ERR_INVALID
     assert lib.orator_decoder_prefill_at(None, FAKE, 4, 0, None) == _lib.ORATOR_ERR_INVALID
     assert lib.orator_embed_gather(FAKE, FAKE, FAKE, 12, None) == _lib.ORATOR_ERR_INVALID
+
+
+def test_decoder_rejects_context_past_decode_limit():
+    import ctypes as C
+    lib = _lib.lib()
+    cfg = _lib.DecoderConfig(1, 512, 4, 2, 128, 1024, 4096, 131073, 1e-6, 1e6)
+    layers = (_lib.DecoderLayer * 1)(_lib.DecoderLayer(*([FAKE] * 8)))
+    h = C.c_void_p()
+    assert lib.orator_decoder_create(C.byref(cfg), FAKE, FAKE, None, layers, C.byref(h)) == \
+        _lib.ORATOR_ERR_UNSUPPORTED
+    assert b"131072" in lib.orator_last_error()
