@@ -140,6 +140,16 @@ int orator_gqa_decode_paged(const float* q, const uint16_t* kpool, const uint16_
                             const int* page_table, int max_pages, int page_size,
                             const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
                             float scale, void* stream);
+/* No counterpart in the reference: orator_gqa_decode_paged for callers that cannot allocate
+ * (code under HIP graph capture, serving loops that forbid hipMalloc).  Same arguments and
+ * results; the split partials live in a static 16 MiB device array per GPU instead of the
+ * library workspace, so the call allocates nothing.  Limit: B * Hq * ceil(max_pages *
+ * page_size / 128) * (Dh + 2) * 4 bytes <= 16 MiB (B = 16, Hq = 16, Dh = 128: 16128 keys),
+ * else ORATOR_ERR_CAPACITY.  Calls that overlap on one GPU share the array and race. */
+int orator_gqa_decode_paged_noalloc(const float* q, const uint16_t* kpool, const uint16_t* vpool,
+                                    const int* page_table, int max_pages, int page_size,
+                                    const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
+                                    float scale, void* stream);
 /* WriteKvCacheKernel + GqaDecodeAttnKernel of one decode step (src/model/asr_text_decoder.cu:
  * 412-418) in one launch: the new token's K/V rows k_new/v_new [Hkv, Dh] fp32 are stored (bf16,
  * round to nearest even) at position *d_pos, and q attends the *d_pos + 1 keys including them.

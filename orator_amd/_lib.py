@@ -120,6 +120,7 @@ SIGNATURES: dict[str, list] = {
     "orator_kv_write_paged": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p],
     "orator_gqa_decode": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+    "orator_gqa_decode_paged_noalloc": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
     "orator_conformer_create": [_i, _i, _i, _i, C.POINTER(ConformerWeights), C.POINTER(_p)],
     "orator_conformer_destroy": [_p],
     "orator_conformer_forward": [_p, _p, _i, _i, _p, _i, _p],

@@ -31,6 +31,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+#include <string>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -724,8 +727,18 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (max_splits > 1024) return fail(ORATOR_ERR_CAPACITY, "gqa_decode: more than 1024 splits");
   const size_t part_o = static_cast<size_t>(p.B) * p.Hq * max_splits * p.Dh * sizeof(float);
   const size_t part_ml = static_cast<size_t>(p.B) * p.Hq * max_splits * 2 * sizeof(float);
-  char* ws = static_cast<char*>(workspace(stream, part_o + part_ml));
-  if (!ws) return ORATOR_ERR_HIP;
+  char* ws = nullptr;
+  if (p.scratch) {
+    if (part_o + part_ml > p.scratch_bytes)
+      return fail(ORATOR_ERR_CAPACITY,
+                  "gqa_decode: split partials (" + std::to_string(part_o + part_ml) +
+                      " bytes) exceed the static scratch (" + std::to_string(p.scratch_bytes) +
+                      " bytes)");
+    ws = static_cast<char*>(p.scratch);
+  } else {
+    ws = static_cast<char*>(workspace(stream, part_o + part_ml));
+    if (!ws) return ORATOR_ERR_HIP;
+  }
 
   DecodeArgs args;
   args.pos_mode = p.pos_mode;
@@ -757,6 +770,39 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (p.kv_f32) return launch_kv<float>(args, p.B, p.Dh, G, split, stream);
   return launch_kv<uint16_t>(args, p.B, p.Dh, G, split, stream);
 }
+
+// ---- allocation-free decode: split partials in a static device array ----
+// Each GPU holds its own copy of `scratch` from load until the process ends.  Host code
+// never passes the array's name to a kernel (on the host it is only a stand-in for the
+// symbol): the device address comes from hipGetSymbolAddress, once per device, with that
+// device current.
+constexpr size_t kStaticScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) float scratch[kStaticScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch` (looked up on the first call on the device).
+int static_scratch(void** out) {
+  *out = nullptr;
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(ORATOR_ERR_UNSUPPORTED, "static scratch: device index past 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (int rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)),
+                           "hipGetSymbolAddress(scratch)"))
+      return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ORATOR_OK;
+}
+}  // namespace
 
 }  // namespace orator_hip
 
@@ -857,6 +903,45 @@ int orator_gqa_decode_paged(const float* q, const uint16_t* kpool, const uint16_
   p.Dh = Dh;
   p.capacity = max_pages * page_size;
   p.scale = scale;
+  return launch_gqa_decode(p, static_cast<hipStream_t>(stream));
+}
+
+// orator_gqa_decode_paged with the split partials in this file's static device scratch
+// (16 MiB per GPU): no allocation of any kind, so callers that cannot allocate (graph
+// capture, serving loops that forbid hipMalloc) can use it.  Calls that overlap on one GPU
+// share the scratch and race.  Nothing in it needs clearing: every partial is written before
+// it is read.
+int orator_gqa_decode_paged_noalloc(const float* q, const uint16_t* kpool, const uint16_t* vpool,
+                                    const int* page_table, int max_pages, int page_size,
+                                    const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
+                                    float scale, void* stream) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Dh <= 0) return ORATOR_OK;  // reference no-op
+  if (!page_table) return fail(ORATOR_ERR_INVALID, "gqa_decode_paged_noalloc: null page table");
+  // reject sizes past the scratch before touching the device
+  const size_t need = decode_workspace_bytes(B, Hq, Dh, max_pages * page_size);
+  if (max_pages > 0 && page_size > 0 && need > kStaticScratchBytes)
+    return fail(ORATOR_ERR_CAPACITY,
+                "gqa_decode_paged_noalloc: B * Hq * splits * (Dh + 2) * 4 = " +
+                    std::to_string(need) + " bytes exceeds the 16 MiB static scratch");
+  void* ptr = nullptr;
+  if (int rc = static_scratch(&ptr)) return rc;
+  DecodeProblem p{};
+  p.q = q;
+  p.kpool = kpool;
+  p.vpool = vpool;
+  p.page_table = page_table;
+  p.max_pages = max_pages;
+  p.page_size = page_size;
+  p.pos = d_pos;
+  p.out = out;
+  p.B = B;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.Dh = Dh;
+  p.capacity = max_pages * page_size;
+  p.scale = scale;
+  p.scratch = ptr;
+  p.scratch_bytes = kStaticScratchBytes;
   return launch_gqa_decode(p, static_cast<hipStream_t>(stream));
 }
 

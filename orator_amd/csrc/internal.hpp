@@ -93,6 +93,10 @@ struct DecodeProblem {
   const float* k_norm = nullptr;
   const float* rope = nullptr;
   float eps = 0.0f;
+  // Split-partial scratch supplied by the caller (scratch_bytes long) instead of the library
+  // workspace; a launch needing more fails with ORATOR_ERR_CAPACITY.
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
 };
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
 // (cos, sin) of RoPE pair j (head_dim 128, base theta) for positions [0, n_pos): out[(p * 64 +

@@ -42,6 +42,16 @@ def GqaDecodeAttnPaged(q, kpool, vpool, page_table, max_pages: int, page_size: i
          page_size, ptr(d_pos), ptr(out), B, Hq, Hkv, Dh, scale, _sh(stream))
 
 
+def GqaDecodeAttnPagedNoAlloc(q, kpool, vpool, page_table, max_pages: int, page_size: int,
+                              d_pos, out, B: int, Hq: int, Hkv: int, Dh: int, scale: float,
+                              stream=None) -> None:
+    """GqaDecodeAttnPaged with its split partials in the library's static device scratch:
+    allocates nothing (for graph capture / allocation-free loops); overlapping calls on one
+    GPU race."""
+    call("orator_gqa_decode_paged_noalloc", ptr(q), ptr(kpool), ptr(vpool), ptr(page_table),
+         max_pages, page_size, ptr(d_pos), ptr(out), B, Hq, Hkv, Dh, scale, _sh(stream))
+
+
 def GqaDecodeAttnAppend(q, k_new, v_new, kc, vc, out, Hq: int, Hkv: int, Dh: int, d_pos,
                         capacity: int, scale: float, stream=None) -> None:
     """WriteKvCacheKernel + GqaDecodeAttnKernel of one decode step in one launch: k_new/v_new

@@ -125,3 +125,15 @@ def test_decoder_rejects_context_past_decode_limit():
     assert lib.orator_decoder_create(C.byref(cfg), FAKE, FAKE, None, layers, C.byref(h)) == \
         _lib.ORATOR_ERR_UNSUPPORTED
     assert b"131072" in lib.orator_last_error()
+
+
+def test_noalloc_decode_rejects_sizes_past_static_scratch():
+    """The allocation-free decode checks its split partials against the 16 MiB static scratch
+    before touching the device: B = 16, Hq = 16, Dh = 128 at 16384 keys needs ~17 MB."""
+    lib = _lib.lib()
+    rc = lib.orator_gqa_decode_paged_noalloc(FAKE, FAKE, FAKE, FAKE, 1024, 16, FAKE, FAKE, 16, 16,
+                                             8, 128, 0.1, None)
+    assert rc == _lib.ORATOR_ERR_CAPACITY
+    assert b"16 MiB" in lib.orator_last_error()
+    assert lib.orator_gqa_decode_paged_noalloc(FAKE, FAKE, FAKE, None, 8, 16, FAKE, FAKE, 1, 16, 8,
+                                               128, 0.1, None) == _lib.ORATOR_ERR_INVALID
