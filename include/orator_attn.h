@@ -95,7 +95,8 @@ int orator_argmax_banned(const float* logits, int n, int ban0, int ban1, int* ou
                          void* stream);
 /* asr_ops::GqaAttention (include/model/asr_ops.cuh:50-56; src/model/asr_ops.cu:130-195,252-295).
  * fp32 q [T,Hq,Dh], k/v [T,Hkv,Dh]; row i attends keys [0,i] (causal) or [0,T).  Default
- * stream.  Dh in {64,128}, Hq/Hkv in {1,2,4} (the reference accepts any power-of-two Dh). */
+ * stream.  As the reference: any power-of-two Dh <= 1024 and any Hq that is a multiple of Hkv
+ * (Dh 64 / 128 with Hq/Hkv in {1,2,4} run on the split-K kernel, the rest on a generic one). */
 int orator_gqa_attention(const float* q, const float* k, const float* v, float* out, int T, int Hq,
                          int Hkv, int Dh, float scale, int causal);
 /* asr_gemm::F32ToBf16 / Bf16ToF32 (include/model/asr_gemm.h:23-25; src/model/asr_gemm.cu:45-57). */
@@ -127,6 +128,21 @@ int orator_qk_norm_rope_kv_write(float* q, float* k, const float* v, long q_stri
                                  int tokens_per_stream, int Hq, int Hkv, int Dh, uint16_t* kpool,
                                  uint16_t* vpool, const int* page_table, int max_pages,
                                  int page_size, int capacity, void* stream);
+/* The RoPE (cos, sin) of every rotate-half pair j < 64 (Dh = 128, base theta) for positions
+ * [0, n_pos): out[(p * 64 + j) * 2 + {0, 1}], the values RopeHalf forms
+ * (src/model/asr_ops.cu:102-109: angle = (float)p * powf(theta, -2j/128), rounded once from
+ * fp64 cos/sin).  Built once per model; the decoder keeps one for its context. */
+int orator_rope_table(float* out, int n_pos, float theta, void* stream);
+/* orator_qk_norm_rope_kv_write reading (cos, sin) from a table of orator_rope_table holding
+ * positions [0, rope_rows) instead of forming them per call (same values); positions past
+ * the table form them per call. */
+int orator_qk_norm_rope_kv_write_table(float* q, float* k, const float* v, long q_stride,
+                                       long kv_stride, const float* q_norm, const float* k_norm,
+                                       float eps, const int* positions, float theta,
+                                       const float* rope, int rope_rows, int n_tokens,
+                                       int tokens_per_stream, int Hq, int Hkv, int Dh,
+                                       uint16_t* kpool, uint16_t* vpool, const int* page_table,
+                                       int max_pages, int page_size, int capacity, void* stream);
 
 /* GqaDecodeAttnKernel (src/model/asr_text_decoder.cu:149-213, launch :416-418):
  * q [Hq, Dh] fp32 attends the S = *d_pos + 1 keys of the bf16 cache kc/vc.
@@ -150,6 +166,27 @@ int orator_gqa_decode_paged_noalloc(const float* q, const uint16_t* kpool, const
                                     const int* page_table, int max_pages, int page_size,
                                     const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
                                     float scale, void* stream);
+/* The attention half of one decode step (src/model/asr_text_decoder.cu:408-418: RmsNorm of q
+ * and k per head, RopeHalf of q and k, WriteKvCacheKernel, GqaDecodeAttnKernel) in one launch:
+ * q [Hq, Dh] and k_new/v_new [Hkv, Dh] are the raw projections (16-byte aligned, Dh = 128);
+ * q and k are normalised (q_norm / k_norm gains, eps) and rotated at position *d_pos with
+ * (cos, sin) from `rope` (orator_rope_table, rope_rows >= capacity), k and v stored as bf16
+ * at *d_pos, and q attends the *d_pos + 1 keys.  Same results as orator_qk_norm_rope_kv_write
+ * then orator_gqa_decode. */
+int orator_gqa_decode_append_qknorm(const float* q, const float* k_new, const float* v_new,
+                                    uint16_t* kc, uint16_t* vc, float* out, int Hq, int Hkv,
+                                    int Dh, const int* d_pos, int capacity, float scale,
+                                    const float* q_norm, const float* k_norm, float eps,
+                                    const float* rope, int rope_rows, void* stream);
+/* Batched paged form (B streams, page-table row b, capacity max_pages * page_size; rows of
+ * unmapped pages or pages >= n_pages are not written). */
+int orator_gqa_decode_append_qknorm_paged(const float* q, const float* k_new, const float* v_new,
+                                          uint16_t* kpool, uint16_t* vpool, const int* page_table,
+                                          int max_pages, int page_size, int n_pages,
+                                          const int* d_pos, float* out, int B, int Hq, int Hkv,
+                                          int Dh, float scale, const float* q_norm,
+                                          const float* k_norm, float eps, const float* rope,
+                                          int rope_rows, void* stream);
 /* WriteKvCacheKernel + GqaDecodeAttnKernel of one decode step (src/model/asr_text_decoder.cu:
  * 412-418) in one launch: the new token's K/V rows k_new/v_new [Hkv, Dh] fp32 are stored (bf16,
  * round to nearest even) at position *d_pos, and q attends the *d_pos + 1 keys including them.

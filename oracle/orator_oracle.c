@@ -2,8 +2,9 @@
  * orator_oracle.c -- CPU restatement of Orator's attention hot path.
  *
  * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels, never part of the
- * product path (see orator_oracle.h).  Built with -O2 -ffp-contract=off and no
- * SIMD intrinsics so the fp32 operation order is the one written here.
+ * product path (see orator_oracle.h).  Built with -O3 -ffp-contract=off, no fast-math and
+ * no SIMD intrinsics, so the fp32 operation order of every output is the one written here
+ * (the compiler may only run independent outputs side by side, as in orc_linear_bf16).
  *
  * Pinning (what checks each function, all in tests/test_oracle.py):
  *   orc_f32_to_bf16         known-answer values + torch's RNE bf16 cast, bit-exact
@@ -749,20 +750,83 @@ static float linear_act(float v, int act) {
   return v;
 }
 
-void orc_linear_bf16(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
-                     int K, int N, int act) {
-  float* x = (float*)malloc(sizeof(float) * (size_t)K);
-  for (int m = 0; m < M; ++m) {
-    for (int kk = 0; kk < K; ++kk) x[kk] = orc_bf16_to_f32(in[(size_t)m * K + kk]);
-    for (int n = 0; n < N; ++n) {
-      const uint16_t* w = W + (size_t)n * K;
-      float acc = 0.0f;
-      for (int kk = 0; kk < K; ++kk) acc += x[kk] * orc_bf16_to_f32(w[kk]);
-      if (bias) acc += bias[n];
-      out[(size_t)m * N + n] = linear_act(acc, act);
+/* Blocked over independent outputs only (LM rows x LN columns share each k step); every
+ * output is still one fp32 chain, acc += x[k] * w[k] for k = 0, 1, ..., K-1 with no
+ * contraction, so the bits equal the plain triple loop (tests/test_oracle.py checks). */
+enum { LM = 4, LN = 4, LN1 = 16 };
+/* M = 1 (decode GEMV): LN1 columns per k step, same per-output chain. */
+static void linear_bf16_row(const uint16_t* in, const uint16_t* W, const float* bias, float* out,
+                            int K, int N, int act) {
+  float* xs = (float*)malloc(sizeof(float) * (size_t)K);
+  float* ws = (float*)malloc(sizeof(float) * (size_t)K * LN1);
+  for (int kk = 0; kk < K; ++kk) xs[kk] = orc_bf16_to_f32(in[kk]);
+  for (int n0 = 0; n0 < N; n0 += LN1) {
+    const int nb = N - n0 < LN1 ? N - n0 : LN1;
+    for (int j = 0; j < LN1; ++j) {
+      const uint16_t* wr = W + (size_t)(n0 + (j < nb ? j : nb - 1)) * K;
+      for (int kk = 0; kk < K; ++kk) ws[(size_t)kk * LN1 + j] = orc_bf16_to_f32(wr[kk]);
+    }
+    float acc[LN1];
+    for (int j = 0; j < LN1; ++j) acc[j] = 0.0f;
+    for (int kk = 0; kk < K; ++kk) {
+      const float x = xs[kk];
+      const float* w = ws + (size_t)kk * LN1;
+      for (int j = 0; j < LN1; ++j) acc[j] += x * w[j];
+    }
+    for (int j = 0; j < nb; ++j) {
+      float v = acc[j];
+      if (bias) v += bias[n0 + j];
+      out[n0 + j] = linear_act(v, act);
     }
   }
-  free(x);
+  free(xs);
+  free(ws);
+}
+
+void orc_linear_bf16(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
+                     int K, int N, int act) {
+  if (M == 1) {
+    linear_bf16_row(in, W, bias, out, K, N, act);
+    return;
+  }
+  const int mblocks = (M + LM - 1) / LM;
+  /* xs[mb][k][i] = row LM*mb+i widened (rows past M repeat the last row; never stored) */
+  float* xs = (float*)malloc(sizeof(float) * (size_t)mblocks * K * LM);
+  float* ws = (float*)malloc(sizeof(float) * (size_t)K * LN);
+  for (int mb = 0; mb < mblocks; ++mb)
+    for (int kk = 0; kk < K; ++kk)
+      for (int i = 0; i < LM; ++i) {
+        int m = LM * mb + i;
+        if (m >= M) m = M - 1;
+        xs[((size_t)mb * K + kk) * LM + i] = orc_bf16_to_f32(in[(size_t)m * K + kk]);
+      }
+  for (int n0 = 0; n0 < N; n0 += LN) {
+    const int nb = N - n0 < LN ? N - n0 : LN;
+    for (int kk = 0; kk < K; ++kk)
+      for (int j = 0; j < LN; ++j)
+        ws[(size_t)kk * LN + j] = orc_bf16_to_f32(W[(size_t)(n0 + (j < nb ? j : nb - 1)) * K + kk]);
+    for (int mb = 0; mb < mblocks; ++mb) {
+      float acc[LM][LN];
+      for (int i = 0; i < LM; ++i)
+        for (int j = 0; j < LN; ++j) acc[i][j] = 0.0f;
+      const float* xb = xs + (size_t)mb * K * LM;
+      for (int kk = 0; kk < K; ++kk) {
+        const float* x = xb + (size_t)kk * LM;
+        const float* w = ws + (size_t)kk * LN;
+        for (int i = 0; i < LM; ++i)
+          for (int j = 0; j < LN; ++j) acc[i][j] += x[i] * w[j];
+      }
+      const int m0 = LM * mb, rows = M - m0 < LM ? M - m0 : LM;
+      for (int i = 0; i < rows; ++i)
+        for (int j = 0; j < nb; ++j) {
+          float v = acc[i][j];
+          if (bias) v += bias[n0 + j];
+          out[(size_t)(m0 + i) * N + n0 + j] = linear_act(v, act);
+        }
+    }
+  }
+  free(xs);
+  free(ws);
 }
 
 /* ------------------------------------------------------------------------- */

@@ -121,6 +121,11 @@ SIGNATURES: dict[str, list] = {
     "orator_gqa_decode": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
     "orator_gqa_decode_paged_noalloc": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+    "orator_gqa_decode_append_qknorm": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p, _p,
+                                        _f, _p, _i, _p],
+    "orator_gqa_decode_append_qknorm_paged": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _i, _i,
+                                              _i, _i, _f, _p, _p, _f, _p, _i, _p],
+    "orator_rope_table": [_p, _i, _f, _p],
     "orator_conformer_create": [_i, _i, _i, _i, C.POINTER(ConformerWeights), C.POINTER(_p)],
     "orator_conformer_destroy": [_p],
     "orator_conformer_forward": [_p, _p, _i, _i, _p, _i, _p],
@@ -131,6 +136,8 @@ SIGNATURES: dict[str, list] = {
                                        _i, _f, _p],
     "orator_qk_norm_rope_kv_write": [_p, _p, _p, _l, _l, _p, _p, _f, _p, _f, _i, _i, _i, _i, _i,
                                      _p, _p, _p, _i, _i, _i, _p],
+    "orator_qk_norm_rope_kv_write_table": [_p, _p, _p, _l, _l, _p, _p, _f, _p, _f, _p, _i, _i,
+                                           _i, _i, _i, _i, _p, _p, _p, _i, _i, _i, _p],
     "orator_sgemm": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "orator_sgemm_batched": [_p, _p, _p, _i, _i, _i, _i, _i, _l, _l, _l, _p],
     "orator_build_pos_emb": [_p, _i, _i],

@@ -883,6 +883,72 @@ int orator_gqa_decode_append_paged(const float* q, const float* k_new, const flo
   return launch_gqa_decode(p, static_cast<hipStream_t>(stream));
 }
 
+// The whole attention half of a decode step (asr_text_decoder.cu:408-418: RmsNorm q and k,
+// RopeHalf q and k, WriteKvCacheKernel, GqaDecodeAttnKernel) in one launch: q and k_new are
+// the raw projections; the per-head RMSNorm and the RoPE of position pos[b] (a table of
+// orator_rope_table holding `rope_rows` >= capacity positions) are applied before attending.
+static int decode_append_qknorm(const float* q, const float* k_new, const float* v_new,
+                                uint16_t* kpool, uint16_t* vpool, const int* page_table,
+                                int max_pages, int page_size, long pool_rows, int capacity,
+                                const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
+                                float scale, const float* q_norm, const float* k_norm, float eps,
+                                const float* rope, int rope_rows, hipStream_t stream) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Dh <= 0) return ORATOR_OK;
+  if (!k_new || !v_new || !q_norm || !k_norm || !rope)
+    return fail(ORATOR_ERR_INVALID, "gqa_decode_append_qknorm: null k/v, norm or RoPE table");
+  if (Dh != 128) return fail(ORATOR_ERR_UNSUPPORTED, "gqa_decode_append_qknorm: Dh must be 128");
+  if (rope_rows < capacity)
+    return fail(ORATOR_ERR_INVALID, "gqa_decode_append_qknorm: RoPE table shorter than capacity");
+  DecodeProblem p{};
+  p.q = q;
+  p.kpool = kpool;
+  p.vpool = vpool;
+  p.page_table = page_table;
+  p.max_pages = max_pages;
+  p.page_size = page_size;
+  p.pos = d_pos;
+  p.out = out;
+  p.B = B;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.Dh = Dh;
+  p.capacity = capacity;
+  p.scale = scale;
+  p.k_new = k_new;
+  p.v_new = v_new;
+  p.pool_rows = pool_rows;
+  p.q_norm = q_norm;
+  p.k_norm = k_norm;
+  p.rope = rope;
+  p.eps = eps;
+  return launch_gqa_decode(p, stream);
+}
+
+int orator_gqa_decode_append_qknorm(const float* q, const float* k_new, const float* v_new,
+                                    uint16_t* kc, uint16_t* vc, float* out, int Hq, int Hkv,
+                                    int Dh, const int* d_pos, int capacity, float scale,
+                                    const float* q_norm, const float* k_norm, float eps,
+                                    const float* rope, int rope_rows, void* stream) {
+  return decode_append_qknorm(q, k_new, v_new, kc, vc, nullptr, 0, 0, capacity, capacity, d_pos,
+                              out, 1, Hq, Hkv, Dh, scale, q_norm, k_norm, eps, rope, rope_rows,
+                              static_cast<hipStream_t>(stream));
+}
+
+int orator_gqa_decode_append_qknorm_paged(const float* q, const float* k_new, const float* v_new,
+                                          uint16_t* kpool, uint16_t* vpool, const int* page_table,
+                                          int max_pages, int page_size, int n_pages,
+                                          const int* d_pos, float* out, int B, int Hq, int Hkv,
+                                          int Dh, float scale, const float* q_norm,
+                                          const float* k_norm, float eps, const float* rope,
+                                          int rope_rows, void* stream) {
+  if (B > 0 && (!page_table || n_pages <= 0))
+    return fail(ORATOR_ERR_INVALID, "gqa_decode_append_qknorm_paged: page table / n_pages");
+  return decode_append_qknorm(q, k_new, v_new, kpool, vpool, page_table, max_pages, page_size,
+                              static_cast<long>(n_pages) * page_size, max_pages * page_size,
+                              d_pos, out, B, Hq, Hkv, Dh, scale, q_norm, k_norm, eps, rope,
+                              rope_rows, static_cast<hipStream_t>(stream));
+}
+
 int orator_gqa_decode_paged(const float* q, const uint16_t* kpool, const uint16_t* vpool,
                             const int* page_table, int max_pages, int page_size, const int* d_pos,
                             float* out, int B, int Hq, int Hkv, int Dh, float scale,
@@ -950,6 +1016,15 @@ int orator_gqa_decode_paged_noalloc(const float* q, const uint16_t* kpool, const
 // keys [0, i] (causal) or [0, T).  Default stream, as the reference.
 int orator_gqa_attention(const float* q, const float* k, const float* v, float* out, int T, int Hq,
                          int Hkv, int Dh, float scale, int causal) {
+  if (T <= 0 || Hq <= 0 || Hkv <= 0 || Dh <= 0) return ORATOR_OK;  // reference no-op
+  if (!q || !k || !v || !out) return fail(ORATOR_ERR_INVALID, "gqa_attention: null pointer");
+  if (Hq % Hkv) return fail(ORATOR_ERR_INVALID, "gqa_attention: Hq must be a multiple of Hkv");
+  if (Dh > 1024 || (Dh & (Dh - 1)))
+    return fail(ORATOR_ERR_UNSUPPORTED, "gqa_attention: Dh must be a power of two <= 1024");
+  const int G = Hq / Hkv;
+  if (!((Dh == 64 || Dh == 128) && (G == 1 || G == 2 || G == 4) && T <= 65535))
+    return launch_gqa_attention_generic(q, k, v, out, T, Hq, Hkv, Dh, scale, causal != 0,
+                                        nullptr);
   DecodeProblem p{};
   p.q = q;
   p.kpool = k;

@@ -679,6 +679,27 @@ int orator_kv_write_paged(const float* k, const float* v, uint16_t* kpool, uint1
   return check_launch("kv_write_paged");
 }
 
+int orator_rope_table(float* out, int n_pos, float theta, void* stream) {
+  if (n_pos > 0 && !out) return orator_hip::fail(ORATOR_ERR_INVALID, "rope_table: null pointer");
+  return orator_hip::launch_rope_table(out, n_pos, theta, static_cast<hipStream_t>(stream));
+}
+
+int orator_qk_norm_rope_kv_write_table(float* q, float* k, const float* v, long q_stride,
+                                       long kv_stride, const float* q_norm, const float* k_norm,
+                                       float eps, const int* positions, float theta,
+                                       const float* rope, int rope_rows, int n_tokens,
+                                       int tokens_per_stream, int Hq, int Hkv, int Dh,
+                                       uint16_t* kpool, uint16_t* vpool, const int* page_table,
+                                       int max_pages, int page_size, int capacity, void* stream) {
+  if (n_tokens > 0 && (!rope || rope_rows <= 0))
+    return orator_hip::fail(ORATOR_ERR_INVALID, "qk_norm_rope_kv_write_table: no RoPE table");
+  return orator_hip::launch_qk_norm_rope_kv(q, k, v, q_stride, kv_stride, q_norm, k_norm, eps,
+                                            positions, theta, rope, rope_rows, n_tokens,
+                                            tokens_per_stream, Hq, Hkv, Dh, kpool, vpool,
+                                            page_table, max_pages, page_size, capacity,
+                                            static_cast<hipStream_t>(stream));
+}
+
 int orator_qk_norm_rope_kv_write(float* q, float* k, const float* v, long q_stride, long kv_stride,
                                  const float* q_norm, const float* k_norm, float eps,
                                  const int* positions, float theta, int n_tokens,

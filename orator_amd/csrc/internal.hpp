@@ -99,6 +99,11 @@ struct DecodeProblem {
   size_t scratch_bytes = 0;
 };
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
+// asr_ops::GqaAttention for any power-of-two Dh <= 1024 and any Hq multiple of Hkv
+// (attention_generic.hip); the split-K kernel serves Dh 64 / 128 with Hq / Hkv in {1, 2, 4}.
+int launch_gqa_attention_generic(const float* q, const float* k, const float* v, float* out,
+                                 int T, int Hq, int Hkv, int Dh, float scale, bool causal,
+                                 hipStream_t s);
 // (cos, sin) of RoPE pair j (head_dim 128, base theta) for positions [0, n_pos): out[(p * 64 +
 // j) * 2 + {0, 1}], the values the fused QK-norm/RoPE kernels form.
 int launch_rope_table(float* out, int n_pos, float theta, hipStream_t s);

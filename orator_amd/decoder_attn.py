@@ -95,3 +95,38 @@ def QkNormRopeKvWrite(q, k, v, q_stride: int, kv_stride: int, q_norm, k_norm, ep
     call("orator_qk_norm_rope_kv_write", ptr(q), ptr(k), ptr(v), q_stride, kv_stride, ptr(q_norm),
          ptr(k_norm), eps, ptr(positions), theta, n_tokens, tokens_per_stream, Hq, Hkv, Dh,
          ptr(kpool), ptr(vpool), ptr(page_table), max_pages, page_size, capacity, _sh(stream))
+
+
+def RopeTable(out, n_pos: int, theta: float, stream=None) -> None:
+    """(cos, sin) of every rotate-half pair (Dh 128) for positions [0, n_pos): [n_pos][64][2]."""
+    call("orator_rope_table", ptr(out), n_pos, theta, _sh(stream))
+
+
+def QkNormRopeKvWriteTable(q, k, v, q_stride: int, kv_stride: int, q_norm, k_norm, eps: float,
+                           positions, theta: float, rope, rope_rows: int, n_tokens: int,
+                           tokens_per_stream: int, Hq: int, Hkv: int, Dh: int, kpool, vpool,
+                           page_table, max_pages: int, page_size: int, capacity: int,
+                           stream=None) -> None:
+    """QkNormRopeKvWrite with (cos, sin) from a RopeTable of rope_rows positions."""
+    call("orator_qk_norm_rope_kv_write_table", ptr(q), ptr(k), ptr(v), q_stride, kv_stride,
+         ptr(q_norm), ptr(k_norm), eps, ptr(positions), theta, ptr(rope), rope_rows, n_tokens,
+         tokens_per_stream, Hq, Hkv, Dh, ptr(kpool), ptr(vpool), ptr(page_table), max_pages,
+         page_size, capacity, _sh(stream))
+
+
+def GqaDecodeAttnAppendQkNorm(q, k_new, v_new, kc, vc, out, Hq: int, Hkv: int, Dh: int, d_pos,
+                              capacity: int, scale: float, q_norm, k_norm, eps: float, rope,
+                              rope_rows: int, stream=None) -> None:
+    """RmsNorm q/k + RopeHalf q/k + KV write + decode attention of one step, one launch."""
+    call("orator_gqa_decode_append_qknorm", ptr(q), ptr(k_new), ptr(v_new), ptr(kc), ptr(vc),
+         ptr(out), Hq, Hkv, Dh, ptr(d_pos), capacity, scale, ptr(q_norm), ptr(k_norm), eps,
+         ptr(rope), rope_rows, _sh(stream))
+
+
+def GqaDecodeAttnAppendQkNormPaged(q, k_new, v_new, kpool, vpool, page_table, max_pages: int,
+                                   page_size: int, n_pages: int, d_pos, out, B: int, Hq: int,
+                                   Hkv: int, Dh: int, scale: float, q_norm, k_norm, eps: float,
+                                   rope, rope_rows: int, stream=None) -> None:
+    call("orator_gqa_decode_append_qknorm_paged", ptr(q), ptr(k_new), ptr(v_new), ptr(kpool),
+         ptr(vpool), ptr(page_table), max_pages, page_size, n_pages, ptr(d_pos), ptr(out), B, Hq,
+         Hkv, Dh, scale, ptr(q_norm), ptr(k_norm), eps, ptr(rope), rope_rows, _sh(stream))

@@ -15,6 +15,25 @@ QWEN_2L = dict(num_layers=2, hidden_size=2048, num_q_heads=16, num_kv_heads=8, h
                rope_theta=1e6)
 
 
+# the full Qwen3-ASR-1.7B-shaped decoder (28 layers), context for a
+# 2048-row prefill plus 256 greedy steps.
+QWEN_28L = dict(QWEN_2L, num_layers=28, max_seq_len=2048 + 256)
+
+# The configs[4] greedy-parity run (tests/golden/make_decoder_greedy_golden.py writes its
+# oracle tokens; tests/test_gpu_decoder_c5.py replays them): seeds of the weights and of the
+# N(0, 0.02) prefill embeddings, lm_head tied to the embedding as in Qwen3-1.7B.
+C5 = dict(weight_seed=2026, embed_seed=2027, prefill=2048, new=256, topk=32)
+
+
+def c5_inputs():
+    """(cfg, weights, prefill embeddings) of the configs[4] greedy-parity run."""
+    from helpers import SplitMix64
+    cfg = dict(QWEN_28L)
+    w = make_weights(cfg, C5["weight_seed"], tied=True)
+    emb = SplitMix64(C5["embed_seed"]).normal((C5["prefill"], cfg["hidden_size"]), 0.02)
+    return cfg, w, emb
+
+
 def make_weights(cfg, seed: int, w_scale: float = 0.02, tied: bool = False,
                  layer_scale: float = 1.0):
     """Returns (embed, final_norm, lm_head or None, layers).  Matmul weights are random bf16

@@ -12,8 +12,9 @@ import numpy as np
 import pytest
 
 import oracle_lib as orc
+import truth64 as t64
 from gpu_helpers import down, empty, say, up
-from helpers import SplitMix64, rel_err
+from helpers import SplitMix64, check_fp32, rel_err
 from orator_amd import decoder_attn as da
 
 pytestmark = pytest.mark.gpu
@@ -38,7 +39,7 @@ def test_append_contiguous_matches_write_then_decode(pos, cap):
     say("append contiguous", pos, cap)
     da.GqaDecodeAttnAppend(up(q), up(kn), up(vn), dk, dv, dout, Hq, Hkv, Dh,
                            up(np.array([pos], np.int32)), cap, scale)
-    assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL
+    check_fp32(down(dout, (Hq, Dh)), ref, TOL, truth=t64.decode(q, kc_ref, vc_ref, pos, scale))
     np.testing.assert_array_equal(down(dk, kc.shape, np.uint16), kc_ref)
     np.testing.assert_array_equal(down(dv, vc.shape, np.uint16), vc_ref)
 
@@ -57,7 +58,7 @@ def test_append_past_capacity_is_dropped_and_clamped():
     say("append past capacity")
     da.GqaDecodeAttnAppend(up(q), up(kn), up(vn), dk, dv, dout, Hq, Hkv, Dh,
                            up(np.array([cap + 5], np.int32)), cap, 0.1)
-    assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL
+    check_fp32(down(dout, (Hq, Dh)), ref, TOL, truth=t64.decode(q, kc, vc, cap - 1, 0.1))
     np.testing.assert_array_equal(down(dk, kc.shape, np.uint16), kc)
     np.testing.assert_array_equal(down(dv, vc.shape, np.uint16), vc)
 
@@ -87,7 +88,8 @@ def test_append_paged_ragged_streams(lens):
     say("append paged", lens[:4], B)
     da.GqaDecodeAttnAppendPaged(up(q), up(kn), up(vn), dk, dv, up(table), max_pages, ps, n_pages,
                                 up(pos), dout, B, Hq, Hkv, Dh, scale)
-    assert rel_err(down(dout, (B, Hq, Dh)), ref, FLOOR) <= TOL
+    check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+               truth=t64.decode_paged(q, kp_ref, vp_ref, table, ps, pos, scale))
     np.testing.assert_array_equal(down(dk, kp.shape, np.uint16), kp_ref)
     np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp_ref)
 
@@ -148,6 +150,7 @@ def test_append_paged_unmapped_page_is_not_written(bad):
     say("append paged, appended page", bad)
     da.GqaDecodeAttnAppendPaged(up(q), up(kn), up(vn), dk, dv, up(table), max_pages, ps, n_pages,
                                 up(pos), dout, B, Hq, Hkv, Dh, scale)
-    assert rel_err(down(dout, (B, Hq, Dh)), ref, FLOOR) <= TOL
+    check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+               truth=t64.decode_paged(q, kp_ref, vp_ref, ref_table, ps, pos, scale))
     np.testing.assert_array_equal(down(dk, kp.shape, np.uint16), kp)
     np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp)

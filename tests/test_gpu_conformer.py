@@ -7,9 +7,11 @@ import math
 import numpy as np
 import pytest
 
+import fp16_model
 import oracle_lib as orc
+import truth64 as t64
 from gpu_helpers import down, empty, say, up
-from helpers import SplitMix64, rel_err
+from helpers import SplitMix64, check_fp32, rel_err
 from orator_amd import conformer_attn as ca
 from orator_amd import gemm
 
@@ -65,7 +67,8 @@ def test_relpos_fp32_vs_oracle(T, valid):
     dout = empty(q.shape, np.float32)
     say("relpos fp32", T, valid)
     ca.RelPosAttention(up(q), up(k), up(v), up(p), up(u), up(vb), dout, T, H, Dk, valid, scale)
-    assert rel_err(down(dout, q.shape), ref, 0.05) <= 1e-4
+    check_fp32(down(dout, q.shape), ref, 1e-4,
+               truth=orc.relpos_attention_f64(q, k, v, p, u, vb, valid, scale) if valid > 0 else None)
 
 
 def _to_f16_bits(x):
@@ -77,18 +80,24 @@ def _to_f16_bits(x):
                                              (40, 0, True), (70, 0, False)])
 def test_relpos_fused_vs_oracle(T, valid, in_f16):
     """Fused fp16-MFMA rel-pos attention (fp16 inputs N(0,1)).  fp16
-    operands with fp32 accumulation: max abs error <= 2e-2 on unit-scale outputs, judged
-    against the oracle run on the fp16-rounded inputs."""
+    operands with fp32 accumulation: max abs error <= 2e-2 on unit-scale outputs (the
+    north_star's bf16/fp16 bar), judged against the oracle run on the fp16-rounded inputs; and
+    within 2x (+2e-5) of the error the kernel's own fp16 roundings predict (tests/fp16_model.py,
+    computed before the device runs: ~6e-4 at T = 717)."""
     H, Dk = 8, 64
     r = SplitMix64(T * 13 + valid)
     q, k, v, p, u, vb = _relpos_inputs(r, T, H, Dk)
     q, k, v, p = (x.astype(np.float16).astype(np.float32) for x in (q, k, v, p))
     scale = 1.0 / math.sqrt(Dk)
     ref = orc.relpos_attention(q, k, v, p, u, vb, valid, scale)
+    predicted = np.max(np.abs(fp16_model.relpos_attention_f16(q, k, v, p, u, vb, valid, scale)
+                              - ref))
     dout = empty(q.shape, np.float32)
     say("relpos fused", T, valid, in_f16)
     ins = [up(_to_f16_bits(x)) if in_f16 else up(x) for x in (q, k, v, p)]
     ca.RelPosAttentionFast(*ins, up(u), up(vb), dout, T, H, Dk, valid, scale, in_f16=in_f16)
     got = down(dout, q.shape)
-    assert np.max(np.abs(got - ref)) <= 2e-2
-    assert np.max(np.abs(got - ref)) <= 5e-3  # observed class of fp16 rounding of q+u, q+v, P
+    err = np.max(np.abs(got - ref))
+    print(f"T={T} valid={valid}: max abs {err:.2e}, fp16 model predicts {predicted:.2e}")
+    assert err <= 2e-2
+    assert err <= 2.0 * predicted + 2e-5

@@ -10,8 +10,9 @@ import numpy as np
 import pytest
 
 import oracle_lib as orc
+import truth64 as t64
 from gpu_helpers import down, empty, say, up
-from helpers import SplitMix64, rel_err
+from helpers import SplitMix64, check_fp32, rel_err
 from orator_amd import decoder_attn as da
 
 pytestmark = pytest.mark.gpu
@@ -43,7 +44,7 @@ def test_decode_contiguous_matches_oracle(S, cap):
     say("decode contiguous", S, cap)
     da.GqaDecodeAttn(dq, dk, dv, dout, Hq, Hkv, Dh, dpos, cap, scale)
     got = down(dout, (Hq, Dh))
-    assert rel_err(got, ref, FLOOR) <= TOL
+    check_fp32(got, ref, TOL, truth=t64.decode(q, kc, vc, S - 1, scale))
     if S == 1:  # a single key: the output is v0 of the group's kv head
         np.testing.assert_allclose(got, np.repeat(orc.from_bf16(vc[0]), 2, axis=0), atol=1e-7)
 
@@ -58,7 +59,7 @@ def test_decode_group_and_headdim_variants(Hq, Hkv, Dh):
     say("decode variant", Hq, Hkv, Dh)
     da.GqaDecodeAttn(up(q), up(kc), up(vc), dout, Hq, Hkv, Dh, up(np.array([S - 1], np.int32)),
                      cap, scale)
-    assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL
+    check_fp32(down(dout, (Hq, Dh)), ref, TOL, truth=t64.decode(q, kc, vc, S - 1, scale))
 
 
 def test_decode_back_to_back_calls_reuse_combine_state():
@@ -73,7 +74,8 @@ def test_decode_back_to_back_calls_reuse_combine_state():
         da.GqaDecodeAttn(dq, dk, dv, dout, Hq, Hkv, Dh, up(np.array([pos], np.int32)), cap,
                          0.08838834764831845)
         ref = orc.gqa_decode(q, kc, vc, pos, 0.08838834764831845)
-        assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL, pos
+        check_fp32(down(dout, (Hq, Dh)), ref, TOL,
+                   truth=t64.decode(q, kc, vc, pos, 0.08838834764831845))
 
 
 def test_decode_position_past_capacity_is_clamped():
@@ -84,7 +86,7 @@ def test_decode_position_past_capacity_is_clamped():
     da.GqaDecodeAttn(up(q), up(kc), up(vc), dout, Hq, Hkv, Dh, up(np.array([5000], np.int32)), cap,
                      0.1)
     ref = orc.gqa_decode(q, kc, vc, cap - 1, 0.1)
-    assert rel_err(down(dout, (Hq, Dh)), ref, FLOOR) <= TOL
+    check_fp32(down(dout, (Hq, Dh)), ref, TOL, truth=t64.decode(q, kc, vc, cap - 1, 0.1))
 
 
 def _paged_case(seed, lens, Hq=16, Hkv=8, Dh=128, ps=16, spare_pages=3):
@@ -113,7 +115,8 @@ def test_decode_paged_ragged_streams(lens):
     say("decode paged", lens[:4], len(lens))
     da.GqaDecodeAttnPaged(up(q), up(kp), up(vp), up(table), max_pages, ps, up(pos), dout, B, Hq,
                           Hkv, Dh, scale)
-    assert rel_err(down(dout, (B, Hq, Dh)), ref, FLOOR) <= TOL
+    check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+               truth=t64.decode_paged(q, kp, vp, table, ps, pos, scale))
 
 
 def test_decode_paged_equals_contiguous_for_identity_table():

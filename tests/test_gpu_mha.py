@@ -10,8 +10,9 @@ import numpy as np
 import pytest
 
 import oracle_lib as orc
+import truth64 as t64
 from gpu_helpers import down, empty, say, up
-from helpers import SplitMix64, rel_err
+from helpers import SplitMix64, check_fp32, rel_err
 from orator_amd.sortformer_attn import MaskedSelfAttention
 
 pytestmark = pytest.mark.gpu
@@ -31,4 +32,6 @@ def test_masked_mha_vs_oracle(T, H, Dk, valid):
     out = empty((T, H, Dk), np.float32)
     say("masked mha", T, H, Dk, valid)
     MaskedSelfAttention(up(q), up(k), up(v), out, T, H, Dk, valid, scale)
-    assert rel_err(down(out, (T, H, Dk)), ref, FLOOR) <= TOL
+    truth = (np.broadcast_to(v.astype(np.float64).mean(0), v.shape) if valid <= 0 else
+             t64.attention_ranges(q, k, v, scale, 0, min(valid, T)))
+    check_fp32(down(out, (T, H, Dk)), ref, TOL, truth=truth)

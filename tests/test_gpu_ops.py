@@ -6,8 +6,9 @@ import numpy as np
 import pytest
 
 import oracle_lib as orc
+import truth64 as t64
 from gpu_helpers import down, empty, say, up
-from helpers import SplitMix64, rel_err
+from helpers import SplitMix64, check_fp32, rel_err
 from orator_amd import asr_ops
 
 pytestmark = pytest.mark.gpu
@@ -128,12 +129,18 @@ def test_gqa_attention_fixture(golden):
     asr_ops.GqaAttention(up(q), up(k), up(v), dout, T, Hq, Hkv, Dh, 1.0 / np.sqrt(Dh), True)
     got = down(dout, q.shape)
     assert np.max(np.abs(got - golden["gqa_out"])) < 5e-4
-    assert rel_err(got, orc.gqa_attention(q, k, v, 1.0 / np.sqrt(Dh), True), 0.05) <= 1e-4
+    check_fp32(got, orc.gqa_attention(q, k, v, 1.0 / np.sqrt(Dh), True), 1e-4,
+               truth=t64.self_attention(q, k, v, 1.0 / np.sqrt(Dh), True))
 
 
 @pytest.mark.parametrize("T,Hq,Hkv,Dh,causal", [(1, 16, 8, 128, True), (256, 16, 8, 128, True),
                                                (100, 8, 8, 64, False), (300, 16, 4, 64, True),
-                                               (129, 16, 8, 128, False)])
+                                               (129, 16, 8, 128, False),
+                                               # the generic kernel: other power-of-two head
+                                               # sizes and group sizes (G = 8, 3, 16)
+                                               (64, 16, 2, 32, True), (50, 8, 1, 256, False),
+                                               (33, 16, 2, 1024, True), (40, 12, 4, 16, True),
+                                               (17, 16, 1, 1, False), (200, 8, 4, 512, True)])
 def test_gqa_attention_vs_oracle(T, Hq, Hkv, Dh, causal):
     r = SplitMix64(T * 7 + Hkv)
     q, k, v = r.normal((T, Hq, Dh), 0.3), r.normal((T, Hkv, Dh), 0.3), r.normal((T, Hkv, Dh))
@@ -142,4 +149,4 @@ def test_gqa_attention_vs_oracle(T, Hq, Hkv, Dh, causal):
     say("gqa_attention", T, Hq, Hkv, Dh, causal)
     asr_ops.GqaAttention(up(q), up(k), up(v), dout, T, Hq, Hkv, Dh, scale, causal)
     ref = orc.gqa_attention(q, k, v, scale, causal)
-    assert rel_err(down(dout, q.shape), ref, 0.05) <= 1e-4
+    check_fp32(down(dout, q.shape), ref, 1e-4, truth=t64.self_attention(q, k, v, scale, causal))

@@ -12,8 +12,9 @@ import numpy as np
 import pytest
 
 import oracle_lib as orc
+import truth64 as t64
 from gpu_helpers import down, empty, say, up
-from helpers import SplitMix64, rel_err
+from helpers import SplitMix64, check_fp32, rel_err
 from orator_amd import decoder_attn as da
 
 pytestmark = pytest.mark.gpu
@@ -66,7 +67,7 @@ def test_prefill_config2_shape(mode):
     say("prefill config2", mode)
     got = _run(q, kc, vc, 0, T, mode, Hkv)
     if mode == da.PREFILL_FP32:
-        assert rel_err(got, ref, FLOOR) <= TOL32
+        check_fp32(got, ref, TOL32, truth=t64.prefill(q, kc, vc, 0, 1.0 / math.sqrt(Dh)))
     else:
         assert np.max(np.abs(got - ref)) <= TOL16
 
@@ -84,9 +85,9 @@ def test_prefill_streaming_split_equals_full():
     assert rel_err(np.concatenate([a, b]), full, FLOOR) <= 2e-6
 
 
-def _check(got, ref, mode):
+def _check(got, ref, mode, truth=None):
     if mode == da.PREFILL_FP32:
-        assert rel_err(got, ref, FLOOR) <= TOL32
+        check_fp32(got, ref, TOL32, truth=truth)
     else:
         assert np.max(np.abs(got - ref)) <= TOL16
 
@@ -104,7 +105,7 @@ def test_prefill_offsets_and_ragged(T, pos0, cap, mode):
     ref = orc.gqa_prefill(q, kc, vc, pos0, 1.0 / math.sqrt(Dh), threads=8)
     say("prefill offsets", T, pos0, cap, mode)
     got = _run(q, kc, vc, pos0, cap, mode, Hkv)
-    _check(got, ref, mode)
+    _check(got, ref, mode, t64.prefill(q, kc, vc, pos0, 1.0 / math.sqrt(Dh)))
     if T == 1 and pos0 == 0:  # one key: the output is v0
         np.testing.assert_allclose(got[0], np.repeat(orc.from_bf16(vc[0]), 2, axis=0), atol=1e-6)
 
@@ -117,7 +118,7 @@ def test_prefill_group_variants(Hq, Hkv, mode):
     ref = orc.gqa_prefill(q, kc, vc, pos0, 1.0 / math.sqrt(Dh), threads=8)
     say("prefill groups", Hq, Hkv, mode)
     got = _run(q, kc, vc, pos0, pos0 + T, mode, Hkv)
-    _check(got, ref, mode)
+    _check(got, ref, mode, t64.prefill(q, kc, vc, pos0, 1.0 / math.sqrt(Dh)))
 
 
 @pytest.mark.parametrize("mode", MODES)
@@ -175,6 +176,7 @@ def test_decode_equals_last_prefill_row(S):
                      up(np.array([S - 1], np.int32)), S, scale)
     dec = down(dout, (Hq, Dh))
     ref = orc.gqa_decode(q[T - 1], kc, vc, S - 1, scale)
-    assert rel_err(dec, ref, FLOOR) <= TOL32
-    assert rel_err(pre, ref, FLOOR) <= TOL32
+    truth = t64.decode(q[T - 1], kc, vc, S - 1, scale)
+    check_fp32(dec, ref, TOL32, truth=truth)
+    check_fp32(pre, ref, TOL32, truth=truth)
     assert rel_err(pre, dec, FLOOR) <= 2 * TOL32

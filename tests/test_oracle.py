@@ -164,6 +164,25 @@ def test_gqa_attention_reference_fixture(golden):
     assert rel_err(out, truth, 0.05) < 5e-5
 
 
+@pytest.mark.parametrize("T,Hq,Hkv,Dh,causal", [(20, 16, 2, 32, True), (9, 12, 4, 256, False),
+                                               (5, 8, 1, 1024, True)])
+def test_gqa_attention_any_head_size_vs_sdpa(T, Hq, Hkv, Dh, causal):
+    """GqaAttention accepts any power-of-two Dh <= 1024 and any Hq multiple of Hkv
+    (src/model/asr_ops.cu:252-295): the oracle against torch SDPA in fp64 with K/V heads
+    repeat-interleaved (the recipe of tools/dump/dump_asr_ops.py:101-108)."""
+    torch, F = _torch()
+    r = SplitMix64(T * Dh + Hq)
+    q, k, v = r.normal((T, Hq, Dh), 0.3), r.normal((T, Hkv, Dh), 0.3), r.normal((T, Hkv, Dh))
+    scale = 1.0 / math.sqrt(Dh)
+    out = orc.gqa_attention(q, k, v, scale, causal)
+    G = Hq // Hkv
+    qt = torch.from_numpy(q).double().permute(1, 0, 2)
+    kt = torch.from_numpy(k).double().permute(1, 0, 2).repeat_interleave(G, 0)
+    vt = torch.from_numpy(v).double().permute(1, 0, 2).repeat_interleave(G, 0)
+    ref = F.scaled_dot_product_attention(qt, kt, vt, is_causal=causal, scale=scale)
+    assert rel_err(out, ref.permute(1, 0, 2).numpy(), 0.05) < 5e-6
+
+
 def test_gqa_attention_noncausal_vs_sdpa():
     torch, F = _torch()
     r = SplitMix64(15)
@@ -470,6 +489,20 @@ def test_linear_bf16_vs_fp64(M, K, N):
                                   orc.linear_bf16(x, W, None, 0))
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 300, 37), (6, 257, 9), (9, 64, 5)])
+def test_linear_bf16_blocking_keeps_the_serial_chain(M, K, N):
+    """orc_linear_bf16 runs outputs side by side; each output must still be the reference's
+    serial fp32 chain acc += x[k] * w[k] (mul then add, k ascending), bit for bit."""
+    r = SplitMix64(M + 7 * K + N)
+    x, W = orc.to_bf16(r.normal((M, K))), orc.to_bf16(r.normal((N, K), 0.05))
+    got = orc.linear_bf16(x, W)
+    xf, wf = orc.from_bf16(x), orc.from_bf16(W)
+    want = np.zeros((M, N), np.float32)
+    for k in range(K):  # numpy float32 ops round exactly as the C chain does
+        want = want + (xf[:, k][:, None] * wf[:, k][None, :])
+    np.testing.assert_array_equal(got, want)
+
+
 # -------------------------------------------------------------------- decoder ----
 
 
@@ -700,3 +733,81 @@ def test_conformer_layer_vs_torch_composition():
     X = X + 0.5 * ffn(X, "ff2")
     want = ln(X, "out").numpy()
     assert rel_err(got, want, 0.05) < 1e-4
+
+
+# ------------------------------------------ decoder composition vs transformers Qwen3 ----
+class _SwapGateUp(orc.OracleDecoder):
+    def _layer_tail(self, L, x, attn):
+        I = self.c["intermediate_size"]
+        L = dict(L, gateup_w=np.concatenate([L["gateup_w"][I:], L["gateup_w"][:I]]))
+        return super()._layer_tail(L, x, attn)
+
+
+class _SwapLayerNorms(orc.OracleDecoder):
+    def _layer_qkv(self, L, x, pos):
+        return super()._layer_qkv(dict(L, in_ln=L["post_ln"], post_ln=L["in_ln"]), x, pos)
+
+    def _layer_tail(self, L, x, attn):
+        return super()._layer_tail(dict(L, in_ln=L["post_ln"], post_ln=L["in_ln"]), x, attn)
+
+
+class _SwapQkNorms(orc.OracleDecoder):
+    def _layer_qkv(self, L, x, pos):
+        return super()._layer_qkv(dict(L, q_norm=L["k_norm"], k_norm=L["q_norm"]), x, pos)
+
+
+class _NormedResidual(orc.OracleDecoder):
+    """Adds the MLP to the normed stream instead of the residual stream."""
+    def _layer_tail(self, L, x, attn):
+        c = self.c
+        T, I = x.shape[0], c["intermediate_size"]
+        x = x + self._lin(orc.to_bf16(attn.reshape(T, -1)), L["o_w"])
+        n = orc.rms_norm(x, L["post_ln"], c["rms_norm_eps"])
+        nb = orc.to_bf16(n)
+        gate, up = self._lin(nb, L["gateup_w"][:I]), self._lin(nb, L["gateup_w"][I:])
+        return n + self._lin(orc.to_bf16(orc.swiglu(gate, up)), L["down_w"])
+
+
+HF_BAR = 1e-2  # max |oracle - HF| / max |HF| on the logits
+
+
+@pytest.mark.parametrize("tied", [False, True])
+def test_decoder_composition_matches_transformers_qwen3(tied):
+    """OracleDecoder (the decoder composition every a8/a9/a15 GPU result is checked against)
+    against an independent restatement: transformers' Qwen3ForCausalLM in fp32 with the same
+    bf16-valued weights (q/k/v and gate/up split out of the fused layout as
+    src/model/asr_text_decoder.cu:283-306 fuses them), rope_theta 1e6, eps 1e-6, eager
+    attention, and the reference's bf16 roundings as hooks (every projection input, the K/V
+    cache rows).  Both sides round to bf16 at the same points, so what remains is fp32
+    summation order re-rounded to bf16 (a whole bf16 step on the ~1 % of K/V elements whose
+    two fp32 values straddle a rounding boundary), 0.25-0.35 % of max |logit| here.  Bar:
+    1 %.  Composition mistakes land far outside it (each is checked): gate/up swapped ~18 %,
+    in/post layer norms swapped ~27 %, q/k norms swapped ~5.6 %, MLP added to the normed
+    stream ~80 %.  Prefill (last row) and one decode step."""
+    import decoder_model as dm
+    import hf_qwen3 as hq
+
+    cfg = dict(dm.SMALL)
+    w = dm.make_weights(cfg, 5, tied=tied)
+    T, tok = 40, 123
+    emb = SplitMix64(9).normal((T, cfg["hidden_size"]), 0.02)
+    model, ctx = hq.build(cfg, w)
+
+    def run(cls):
+        d = cls(cfg, *w)
+        d.prefill_at(emb, 0)
+        lp = d.logits.copy()
+        d.decode_step(d.embed_row(tok), T)
+        return lp, d.logits.copy(), d.embed_row(tok)
+
+    lp, ld, row = run(orc.OracleDecoder)
+    ref = hq.logits(model, ctx, np.concatenate([emb, row[None]]))
+    err_p = np.max(np.abs(lp - ref[T - 1])) / np.max(np.abs(ref[T - 1]))
+    err_d = np.max(np.abs(ld - ref[T])) / np.max(np.abs(ref[T]))
+    print(f"oracle vs HF Qwen3: prefill {err_p:.2e}, decode {err_d:.2e} of max|logit|")
+    assert err_p <= HF_BAR and err_d <= HF_BAR
+    assert int(np.argmax(lp)) == int(np.argmax(ref[T - 1]))
+    for cls in (_SwapGateUp, _SwapLayerNorms, _SwapQkNorms, _NormedResidual):
+        mp, _, _ = run(cls)
+        err = np.max(np.abs(mp - ref[T - 1])) / np.max(np.abs(ref[T - 1]))
+        assert err > 4 * HF_BAR, (cls.__name__, err)
