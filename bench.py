@@ -59,7 +59,7 @@ def parse():
                     help="decoder part: run the greedy steps eagerly (same kernels, no graph "
                          "replay), e.g. for a per-kernel profile")
     ap.add_argument("--only", choices=["decode", "prefill", "conformer", "sweep", "decoder",
-                                       "aux"],
+                                       "aux", "copy"],
                     default=None,
                     help="run one part (for profiling); prints that part's numbers only")
     return ap.parse_args()
@@ -419,6 +419,29 @@ def run_decoder_e2e(T: int = 2048, new: int = 256, use_graph: bool = True):
             "graph_equals_eager_first_tokens": [int(t) for t in eager] == [int(t) for t in toks[:n_chk]]}
 
 
+def run_copy_bandwidth(nbytes: int = 1 << 30, reps: int = 10):
+    """Attainable HBM bandwidth of a plain device copy (hipMemcpyAsync device to device, the
+    runtime's copy kernel) of 1 GiB: (read + write bytes) / time, the practical ceiling the
+    decode kernel's fraction of the published 8 TB/s should be read against."""
+    from orator_amd._lib import call
+    from orator_amd.runtime import DeviceBuffer, Event, Stream
+
+    st = Stream()
+    src, dst = DeviceBuffer(nbytes), DeviceBuffer(nbytes)
+    call("orator_memset", src.ptr, 1, nbytes, st.handle)
+    call("orator_memcpy_dtod", dst.ptr, src.ptr, nbytes, st.handle)
+    st.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(st)
+    for _ in range(reps):
+        call("orator_memcpy_dtod", dst.ptr, src.ptr, nbytes, st.handle)
+    e1.record(st)
+    st.synchronize()
+    us = e0.elapsed_ms(e1) * 1e3 / reps
+    return {"bytes_copied": nbytes, "us": round(us, 1),
+            "GBs_read_plus_write": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}
+
+
 def run_decode_sweep():
     """BASELINE configs[2] sweep: decode kernel GB/s at L in {1024, 2048, 4096}, B in {1, 16}
     (one launch per layer over 28 layers' paged caches)."""
@@ -497,16 +520,46 @@ def spot_check(kpool, vpool, table, max_pages, qs, outs, last_pos, var, scale):
     return {"streams": nb, "max_rel_err": rel_err(got, ref, 0.05), "floor": 0.05}
 
 
-def cpu_baseline(seconds: float):
-    """Oracle decode (scalar C, -O2) over one layer of the workload, repeated for a bounded
-    time on the host cores."""
-    sys.path.insert(0, str(ROOT / "tests"))
-    import oracle_lib as orc
-
+def _cpu_info():
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return cores, model
+
+
+def _median_rate(fn, units_per_call, seconds, max_calls=400, min_calls=3):
+    """Runs fn until `seconds` have passed (at least min_calls); returns (median units/s,
+    calls)."""
+    rates, t_end = [], time.perf_counter() + seconds
+    while len(rates) < max_calls:
+        t0 = time.perf_counter()
+        fn()
+        rates.append(units_per_call / (time.perf_counter() - t0))
+        if len(rates) >= min_calls and time.perf_counter() >= t_end:
+            break
+    return float(np.median(rates)), len(rates)
+
+
+def cpu_baseline(seconds: float):
+    """The oracle (scalar C, -O3, no SIMD intrinsics, no fp contraction) timed on the host cores
+    beside the GPU: the headline decode workload (one layer-step of B = 16 paged streams at S =
+    4097) on 1 thread and on all cores (<= 16), the median of repeated calls within a bounded
+    time each; plus fp32 prefill attention (T = 503 on 1 thread and all cores, T = 2048 on all
+    cores) and the fp32 Conformer rel-pos core (T = 717, the reference's decomposition,
+    1 thread) at their algorithmic flops."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as orc
+
+    cores, model = _cpu_info()
     threads = max(1, min(16, cores))
     S = L_BASE + 1
     max_pages = (S + PAGE - 1) // PAGE
@@ -520,26 +573,43 @@ def cpu_baseline(seconds: float):
     table = rng.permutation(n_pages).astype(np.int32).reshape(B, max_pages)
     q = rng.standard_normal((B, HQ, DH)).astype(np.float32)
     pos = np.full(B, S - 1, np.int32)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        orc.gqa_decode_paged(q, kp, vp, table, PAGE, pos, 1.0 / math.sqrt(DH), threads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 400:
-            break
-    gbs = n * B * decode_bytes(S, max_pages) / el / 1e9
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{n} layer-steps of B={B} paged decode at S={S} "
-                      f"(oracle orc_gqa_decode_paged_mt, {threads} threads, {el:.1f} s, "
-                      f"{cores} cores visible, {model})"}
+    op_bytes = B * decode_bytes(S, max_pages)
+    dec = lambda th: orc.gqa_decode_paged(q, kp, vp, table, PAGE, pos, 1.0 / math.sqrt(DH),
+                                          threads=th)
+    gbs_1, n_1 = _median_rate(lambda: dec(1), op_bytes / 1e9, 0.25 * seconds)
+    gbs_n, n_n = _median_rate(lambda: dec(threads), op_bytes / 1e9, 0.25 * seconds)
+
+    # prefill (fp32 mode, bf16 cache) and the Conformer core
+    def prefill_case(T, th):
+        qq = rng.standard_normal((T, HQ, DH)).astype(np.float32)
+        kc = (rng.standard_normal((T, HKV, DH)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        vc = (rng.standard_normal((T, HKV, DH)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        fl = 4.0 * HQ * DH * T * (T + 1) / 2 / 1e9
+        return _median_rate(lambda: orc.gqa_prefill(qq, kc, vc, 0, 1.0 / math.sqrt(DH),
+                                                    threads=th), fl, 0.1 * seconds, min_calls=1)
+    p503_1, _ = prefill_case(503, 1)
+    p503_n, _ = prefill_case(503, threads)
+    p2048_n, _ = prefill_case(2048, threads)
+    T, H, Dk = 717, 8, 64
+    x = lambda shape: rng.standard_normal(shape).astype(np.float32)
+    cq, ck, cv, cp, cu, cb = x((T, H, Dk)), x((T, H, Dk)), x((T, H, Dk)), x((2 * T - 1, H, Dk)), \
+        x((H, Dk)), x((H, Dk))
+    conf_1, _ = _median_rate(lambda: orc.relpos_attention(cq, ck, cv, cp, cu, cb, T, 0.125),
+                             6.0 * H * T * T * Dk / 1e9, 0.1 * seconds, min_calls=1)
+    return {"value": round(gbs_n, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"median of {n_n} calls of one layer-step of the headline workload (B={B} "
+                      f"paged decode at S={S}, {op_bytes / 1e6:.1f} MB) through the oracle's "
+                      f"orc_gqa_decode_paged_mt on {threads} threads",
+            "single_thread": {"value": round(gbs_1, 3), "unit": "GB/s", "cores": 1,
+                              "sample": f"median of {n_1} calls, same layer-step"},
+            "prefill_fp32": {"T503_1thread_gflops": round(p503_1, 3),
+                             f"T503_{threads}threads_gflops": round(p503_n, 3),
+                             f"T2048_{threads}threads_gflops": round(p2048_n, 3),
+                             "flops": "4*Hq*Dh*T(T+1)/2 (causal, algorithmic)"},
+            "conformer_relpos_fp32": {"T717_1thread_gflops": round(conf_1, 3),
+                                      "flops": "6*H*T^2*Dk (algorithmic; the oracle runs the "
+                                               "reference decomposition)"},
+            "cpu_model": model, "cores_visible": cores}
 
 
 def main():
@@ -555,11 +625,14 @@ def main():
                 "prefill": lambda: [run_prefill(503, da.PREFILL_BF16),
                                     run_prefill(2048, da.PREFILL_BF16)],
                 "conformer": run_conformer, "sweep": run_decode_sweep,
+                "copy": run_copy_bandwidth,
                 "decoder": lambda: run_decoder_e2e(use_graph=not args.no_graph),
                 "aux": run_aux}[args.only]()
         print(json.dumps({"only": args.only, "result": part}, default=float))
         return
     dec = run_decode(args.steps, args.warmup)
+    copy = run_copy_bandwidth()
+    log("copy:", copy)
     log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value_gbs']:.1f} GB/s; op "
         f"{dec['kernel_avg_us']:.1f} us avg -> {dec['achieved_gbs']:.1f} GB/s; parity {dec['parity']}")
     from orator_amd import decoder_attn as da
@@ -603,7 +676,10 @@ def main():
                                "gqa_decode_combine_kernel (split merge); average over the "
                                "timed region's back-to-back ops (HIP events on its stream)",
                      "kernel_avg_us": round(dec["kernel_avg_us"], 2),
-                     "bytes_per_launch": int(dec["kernel_bytes"])},
+                     "bytes_per_launch": int(dec["kernel_bytes"]),
+                     "attainable_copy_gbs": copy["GBs_read_plus_write"],
+                     "frac_of_attainable_copy": round(dec["achieved_gbs"] /
+                                                      copy["GBs_read_plus_write"], 4)},
         "cpu_baseline": cpu,
         "parity": dec["parity"],
         "prefill": pre,

@@ -250,11 +250,16 @@ int orator_record_token(int* out, int* d_count, const int* d_token, int capacity
 int orator_inc_pos(int* d_pos, void* stream);
 
 /* ----------------------------------------------------------------- decoder ---- */
-/* AsrTextConfig (include/model/asr_text_decoder.h:30-42). */
+/* AsrTextConfig (include/model/asr_text_decoder.h:30-42).  profile != 0 times, as the
+ * reference does (src/model/asr_text_decoder.cu:369-377, 504-583, 762-889), with events and
+ * host clocks and prints to stderr: eager decode steps on the default stream (per-token GPU
+ * average every 16 steps), single-row prefills (layer loop vs final norm + LM head), and each
+ * DecodeGreedy call (seed, loop, tokens emitted, host syncs). */
 typedef struct OratorDecoderConfig {
   int num_layers, hidden_size, num_q_heads, num_kv_heads, head_dim, intermediate_size,
       vocab_size, max_seq_len;
   float rms_norm_eps, rope_theta;
+  int profile;
 } OratorDecoderConfig;
 /* One layer's device weights, in the reference's fused layout
  * (src/model/asr_text_decoder.cu:288-307): qkv_w = q | k | v rows [(Hq + 2 Hkv) Dh, hidden],

@@ -154,6 +154,13 @@ class ConformerLayer {
                int attn_mode = 0) {
     gpu::Check(orator_conformer_forward(h_, x, T, valid_len, pos_emb, attn_mode, stream));
   }
+  // ConformerLayer::BuildPosEmb (include/model/conformer_layer.h:45-46): the relative
+  // positional encoding [2T-1, d_model] built on the host.
+  static std::vector<float> BuildPosEmb(int T, int d_model) {
+    std::vector<float> pe(T > 0 && d_model > 0 ? static_cast<size_t>(2 * T - 1) * d_model : 0);
+    gpu::Check(orator_build_pos_emb(pe.data(), T, d_model));
+    return pe;
+  }
 
  private:
   void* h_ = nullptr;
@@ -191,6 +198,7 @@ struct AsrTextConfig {  // include/model/asr_text_decoder.h:30-42
   float rms_norm_eps = 1e-6f;
   float rope_theta = 1000000.0f;
   int max_seq_len = 2048;
+  bool profile = false;            // event timing to stderr (decode steps, prefill, greedy)
   bool cuda_graph_enabled = true;  // graph replay in DecodeGreedy
 };
 
@@ -204,7 +212,7 @@ class AsrTextDecoder {
     const OratorDecoderConfig oc{c.num_layers,  c.hidden_size,       c.num_q_heads,
                                  c.num_kv_heads, c.head_dim,         c.intermediate_size,
                                  c.vocab_size,  c.max_seq_len,       c.rms_norm_eps,
-                                 c.rope_theta};
+                                 c.rope_theta,  c.profile ? 1 : 0};
     gpu::Check(orator_decoder_create(&oc, embed, final_norm, lm_head, layers, &h_));
   }
   ~AsrTextDecoder() { orator_decoder_destroy(h_); }

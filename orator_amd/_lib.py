@@ -37,7 +37,7 @@ class DecoderConfig(C.Structure):
     _fields_ = [("num_layers", _i), ("hidden_size", _i), ("num_q_heads", _i),
                 ("num_kv_heads", _i), ("head_dim", _i), ("intermediate_size", _i),
                 ("vocab_size", _i), ("max_seq_len", _i), ("rms_norm_eps", _f),
-                ("rope_theta", _f)]
+                ("rope_theta", _f), ("profile", _i)]
 
 
 class DecoderLayer(C.Structure):

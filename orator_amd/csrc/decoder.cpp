@@ -21,7 +21,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -40,6 +42,30 @@ int dalloc(T** p, size_t n) {
   if (n == 0) return ORATOR_OK;
   return check_hip(hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T)), "decoder hipMalloc");
 }
+
+// Three events on a stream: start, mark, finish -> (start..mark, mark..finish) in ms.
+struct Timer {
+  hipEvent_t e[3] = {nullptr, nullptr, nullptr};
+  ~Timer() {
+    for (hipEvent_t x : e)
+      if (x) (void)hipEventDestroy(x);
+  }
+  void start(hipStream_t s) {
+    for (hipEvent_t& x : e)
+      if (hipEventCreate(&x) != hipSuccess) x = nullptr;
+    if (e[0]) (void)hipEventRecord(e[0], s);
+  }
+  void mark(hipStream_t s) {
+    if (e[1]) (void)hipEventRecord(e[1], s);
+  }
+  bool finish(hipStream_t s, float* a, float* b) {
+    if (!e[0] || !e[1] || !e[2]) return false;
+    if (hipEventRecord(e[2], s) != hipSuccess || hipEventSynchronize(e[2]) != hipSuccess)
+      return false;
+    return hipEventElapsedTime(a, e[0], e[1]) == hipSuccess &&
+           hipEventElapsedTime(b, e[1], e[2]) == hipSuccess;
+  }
+};
 
 struct Decoder {
   OratorDecoderConfig c{};
@@ -65,6 +91,10 @@ struct Decoder {
   int sout_cap = 0;
   int* host_int = nullptr;  // pinned staging for scalars
   hipStream_t capture_stream = nullptr;
+  // profile (c.profile): per-token GPU time of eager default-stream decode steps
+  double prof_sum_ms = 0.0;
+  int prof_count = 0;
+  bool prof_prefill_printed = false;
   hipGraphExec_t graph = nullptr, graph_banned = nullptr;
   bool graph_ready = false;
   int graph_ban0 = -1, graph_ban1 = -1;
@@ -154,6 +184,11 @@ struct Decoder {
     const int H = c.hidden_size, I = c.intermediate_size, Hq = c.num_q_heads,
               Hkv = c.num_kv_heads, Dh = c.head_dim;
     const float eps = c.rms_norm_eps;
+    // profile: a single-row forward times its layer loop and its final norm + LM head
+    // (asr_text_decoder.cu:504-583), printed once per decoder
+    Timer prof;
+    const bool timed = c.profile && T == 1 && !prof_prefill_printed;
+    if (timed) prof.start(s);
     for (int t = 0; t < T; ++t) pos_host[t] = pos0 + t;
     pos_host[T] = pos0;
     int rc = check_hip(hipMemcpyAsync(pos_dev, pos_host, sizeof(int) * (T + 1),
@@ -186,9 +221,37 @@ struct Decoder {
     }
     if (rc) return rc;
     cache_len = pos0 + T;
+    if (timed) prof.mark(s);
     const float* last = x + static_cast<size_t>(T - 1) * H;
-    return launch_gemv_fused(kGemvInRmsNorm, last, final_norm, eps, lm_head, logits, H,
-                             c.vocab_size, false, s);
+    rc = launch_gemv_fused(kGemvInRmsNorm, last, final_norm, eps, lm_head, logits, H,
+                           c.vocab_size, false, s);
+    if (timed && !rc) {
+      float layers_ms = 0.0f, head_ms = 0.0f;
+      if (prof.finish(s, &layers_ms, &head_ms)) {
+        std::fprintf(stderr, "[dec2] %d-layer loop=%.2fms lm_head+norm=%.2fms\n", c.num_layers,
+                     layers_ms, head_ms);
+        prof_prefill_printed = true;
+      }
+    }
+    return rc;
+  }
+
+  // profile: GPU time of one eager decode step on the default stream
+  // (asr_text_decoder.cu:369-377, 439-454); the running average is printed every 16 steps.
+  int decode_forward_profiled(hipStream_t s) {
+    if (!(c.profile && s == nullptr)) return decode_forward(s);
+    Timer prof;
+    prof.start(s);
+    const int rc = decode_forward(s);
+    float ms = 0.0f, unused = 0.0f;
+    prof.mark(s);
+    if (!rc && prof.finish(s, &ms, &unused)) {
+      prof_sum_ms += ms;
+      if (++prof_count % 16 == 0)
+        std::fprintf(stderr, "[dec2] per-token GPU compute avg = %.3f ms (n=%d)\n",
+                     prof_sum_ms / prof_count, prof_count);
+    }
+    return rc;
   }
 
   // One-token forward of sx at the device position spos (asr_text_decoder.cu:360-455).
@@ -333,11 +396,29 @@ struct Decoder {
       }
       return ORATOR_OK;
     };
+    // profile: host-clock split of the call (asr_text_decoder.cu:762-889)
+    using clk = std::chrono::steady_clock;
+    const auto t_seed0 = clk::now();
+    auto t_seed1 = t_seed0, t_loop0 = t_seed0;
+    int batches = 0;
+    double first_sync_ms = 0.0;
+    auto report = [&]() {
+      if (!c.profile) return;
+      const auto ms = [](clk::time_point a, clk::time_point b) {
+        return std::chrono::duration<double, std::milli>(b - a).count();
+      };
+      std::fprintf(stderr,
+                   "[decprof] seed+drain=%.1fms loop=%.1fms (emitted=%d batches=%d"
+                   " first_batch_sync=%.1fms)\n",
+                   ms(t_seed0, t_seed1), ms(t_loop0, clk::now()), static_cast<int>(out.size()),
+                   batches, first_sync_ms);
+    };
     // seed: argmax of the prefill logits -> the first token
     const bool seed_ban = 0 < ban_steps;
     if ((rc = argmax(seed_ban ? eos0 : -1, seed_ban ? eos1 : -1, stok, s)) ||
         (rc = check_hip(hipStreamSynchronize(s), "decoder sync")))
       return rc;
+    t_seed1 = t_loop0 = clk::now();
     int emitted = 0;
     if (use_graph && !graph_ready) {
       const bool ban_first = (0 + 1) < ban_steps;
@@ -359,9 +440,13 @@ struct Decoder {
         (void)hipGetLastError();
       }
       graph_ready = true;
+      if (c.profile)
+        std::fprintf(stderr, "[graph] ready (banned=%p normal=%p)\n",
+                     static_cast<void*>(graph_banned), static_cast<void*>(graph));
       if ((rc = harvest(emitted))) return rc;
       if (stop) {
         cache_len = start_pos + emitted;
+        report();
         return ORATOR_OK;
       }
     }
@@ -369,14 +454,18 @@ struct Decoder {
       while (emitted < max_new) {
         const bool next_ban = (emitted + 1) < ban_steps;
         const int this_batch = next_ban ? 1 : std::min(batch, max_new - emitted);
+        const auto tb = clk::now();
         for (int b = 0; b < this_batch && !rc; ++b)
           rc = body(s, next_ban ? eos0 : -1, next_ban ? eos1 : -1);
         if (rc || (rc = check_hip(hipStreamSynchronize(s), "decoder sync"))) return rc;
+        if (batches++ == 0)
+          first_sync_ms = std::chrono::duration<double, std::milli>(clk::now() - tb).count();
         emitted += this_batch;
         if ((rc = harvest(emitted))) return rc;
         if (stop) break;
       }
       cache_len = start_pos + emitted;
+      report();
       return ORATOR_OK;
     }
     while (emitted < max_new) {
@@ -384,13 +473,17 @@ struct Decoder {
       hipGraphExec_t g = in_ban ? graph_banned : graph;
       const int limit = in_ban ? std::min(ban_steps - 1, max_new) : max_new;
       const int this_batch = std::max(1, std::min(batch, limit - emitted));
+      const auto tb = clk::now();
       for (int b = 0; b < this_batch && !rc; ++b) rc = check_hip(hipGraphLaunch(g, s), "graph launch");
       if (rc || (rc = check_hip(hipStreamSynchronize(s), "decoder sync"))) return rc;
+      if (batches++ == 0)
+        first_sync_ms = std::chrono::duration<double, std::milli>(clk::now() - tb).count();
       emitted += this_batch;
       if ((rc = harvest(emitted))) return rc;
       if (stop) break;
     }
     cache_len = start_pos + emitted;
+    report();
     return ORATOR_OK;
   }
 };
@@ -476,7 +569,7 @@ int orator_decoder_decode_step(void* handle, const float* embed, int pos, void* 
                      "decoder embed");
   if (!rc) rc = d->set_int(d->spos, pos, s);
   d->cache_len = pos + 1;
-  if (!rc) rc = d->decode_forward(s);
+  if (!rc) rc = d->decode_forward_profiled(s);
   return rc ? rc : check_hip(hipStreamSynchronize(s), "decoder sync");
 }
 
@@ -489,7 +582,7 @@ int orator_decoder_decode_step_device(void* handle, const int* d_token, int pos,
   int rc = d->set_int(d->spos, pos, s);
   d->cache_len = pos + 1;
   if (!rc) rc = orator_embed_gather(d->embed, d_token, d->sx, d->c.hidden_size, s);
-  return rc ? rc : d->decode_forward(s);
+  return rc ? rc : d->decode_forward_profiled(s);
 }
 
 int orator_decoder_argmax_to_device(void* handle, int* d_out, int ban0, int ban1, void* stream) {

@@ -27,12 +27,13 @@ class AsrTextConfig:
     max_seq_len: int = 2048
     rms_norm_eps: float = 1e-6
     rope_theta: float = 1e6
+    profile: bool = False  # event timing printed to stderr, as the reference's
 
     def c_struct(self) -> DecoderConfig:
         return DecoderConfig(self.num_layers, self.hidden_size, self.num_q_heads,
                              self.num_kv_heads, self.head_dim, self.intermediate_size,
                              self.vocab_size, self.max_seq_len, self.rms_norm_eps,
-                             self.rope_theta)
+                             self.rope_theta, int(self.profile))
 
 
 def _addr(x):

@@ -157,6 +157,21 @@ int main(int argc, char** argv) {
                   threw ? "ok" : "FAIL");
       if (!threw) ++g_failures;
     }
+    {  // ConformerLayer::BuildPosEmb is a static of the class (conformer_layer.h:45-46):
+       // pe[m][2k] = sin((T-1-m) * 10000^(-2k/d)), pe[m][2k+1] = cos(...)
+      const int T = 3, d = 8;
+      const std::vector<float> pe = orator::model::conformer_attn::ConformerLayer::BuildPosEmb(T, d);
+      double e = pe.size() == static_cast<size_t>((2 * T - 1) * d) ? 0.0 : 1.0;
+      for (int m = 0; m < 2 * T - 1 && e == 0.0; ++m)
+        for (int k = 0; k < d / 2; ++k) {
+          const double a = (T - 1 - m) * std::exp(-std::log(10000.0) * 2 * k / d);
+          e = std::max(e, std::fabs(pe[m * d + 2 * k] - std::sin(a)));
+          e = std::max(e, std::fabs(pe[m * d + 2 * k + 1] - std::cos(a)));
+        }
+      std::printf("  pos_emb    static BuildPosEmb(3, 8) max abs err = %.3e %s\n", e,
+                  e < 1e-6 ? "ok" : "FAIL");
+      if (!(e < 1e-6)) ++g_failures;
+    }
     {  // throughput print, representative decoder self-attention (:177-202)
       const int T = 256, Hq = 16, Hkv = 8, Dh = 128;
       std::vector<float> hq(static_cast<size_t>(T) * Hq * Dh, 0.1f), hk(static_cast<size_t>(T) * Hkv * Dh, 0.1f);

@@ -34,10 +34,17 @@ OUT = Path(__file__).resolve().parent / "decoder_greedy_c5.npz"
 
 
 class BlasOrderDecoder(orc.OracleDecoder):
-    """The oracle's composition with float32 BLAS products instead of serial chains."""
+    """The oracle's composition with float32 BLAS products instead of serial chains (weights
+    widened to fp32 once and kept)."""
+
+    _wide: dict = {}
 
     def _lin(self, x_bf16, W):
-        return np.matmul(orc.from_bf16(x_bf16), orc.from_bf16(W).T).astype(np.float32)
+        key = (W.__array_interface__["data"][0], W.shape)
+        Wf = self._wide.get(key)
+        if Wf is None:
+            Wf = self._wide[key] = np.ascontiguousarray(orc.from_bf16(W))
+        return np.matmul(orc.from_bf16(x_bf16), Wf.T).astype(np.float32)
 
 
 def top(logits, k):

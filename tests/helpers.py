@@ -41,13 +41,14 @@ def rel_err(got, ref, floor):
     return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), floor)))
 
 
-def check_fp32(got, ref, tol=1e-4, label="", truth=None, floor3_tol=None):
+def check_fp32(got, ref, tol=1e-4, label="", truth=None, floor3_tol=None, truth_mult=2.0):
     """fp32-mode parity gate.  Always: rel_err(floor 0.05) <= tol.  At the reference's floor
     1e-3 (test/unit/model/test_asr_gemm.cc:368): rel_err(floor 1e-3) <= floor3_tol (tol if
     not given); where fp32 summation over long rows cannot meet that against the oracle (an
     output near 0 is a cancellation of terms ~1000x larger), a test passes `truth` (fp64) and
-    the device must be as close to the exact value as the oracle is: rel_err(got, truth,
-    1e-3) <= max(floor3_tol, 2 * rel_err(ref, truth, 1e-3)).  Every figure is printed (and
+    the device must be about as close to the exact value as the oracle is: rel_err(got, truth,
+    1e-3) <= max(floor3_tol, truth_mult * rel_err(ref, truth, 1e-3)), truth_mult 2 unless a
+    test states why its formula is less exact than the oracle's.  Every figure is printed (and
     appended to $ORATOR_PARITY_LOG when set)."""
     import json
     import os
@@ -61,7 +62,7 @@ def check_fp32(got, ref, tol=1e-4, label="", truth=None, floor3_tol=None):
         eo = rel_err(ref, truth, 1e-3)
         eg = rel_err(got, truth, 1e-3)
         rec.update({"oracle_vs_fp64_1e-3": eo, "device_vs_fp64_1e-3": eg})
-        ok3 = eg <= max(t3, 2.0 * eo)
+        ok3 = eg <= max(t3, truth_mult * eo)
     print("[parity]", json.dumps(rec), flush=True)
     path = os.environ.get("ORATOR_PARITY_LOG")
     if path:
