@@ -64,8 +64,7 @@ def build_hip(jobs: int | None = None) -> Path:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-           *map(str, objs), f"-Wl,-rpath,{ROCM_LIB}", f"-L{ROCM_LIB}", "-lamdhip64",
-           "-lhipblaslt"]
+           *map(str, objs), f"-Wl,-rpath,{ROCM_LIB}", f"-L{ROCM_LIB}", "-lamdhip64"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")

@@ -24,7 +24,10 @@ int check_launch(const char* what);
 // on demand; a grown block's old memory is kept (queued work or a captured graph may still
 // read it) until workspace_release(stream).  Returns nullptr on failure (the error is
 // recorded).
-void* workspace(hipStream_t stream, size_t bytes);
+// Slots are independent blocks: kWsGemm holds the split-K partials of the GEMMs, which may run
+// while a caller's slot-0 buffer (e.g. the bf16 cast of a Linear input) is being read.
+constexpr int kWsGemm = 1;
+void* workspace(hipStream_t stream, size_t bytes, int slot = 0);
 // Frees every workspace block of `stream` (all threads, current and retired) after the
 // stream's queued work; for the owner of a stream about to be destroyed.
 int workspace_release(hipStream_t stream);
@@ -119,20 +122,8 @@ int launch_qk_norm_rope_kv(float* q, float* k, const float* v, long q_stride, lo
 // Workspace bytes a decode launch over B streams of `capacity` keys needs (split partials).
 size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity);
 
-// bf16 GEMM on hipBLASLt (blaslt_gemm.cpp): out[M][N] = in[M][K] W[N][K]^T, fp32 accumulate
-// and output, no epilogue.  ORATOR_ERR_UNSUPPORTED when the library has no workspace-free
-// plan for the shape (the caller then runs its own kernel).
-constexpr int kLibMinM = 32;  // smaller M stays on the MFMA kernel / GEMV
-bool bf16_gemm_lib_enabled();
-int launch_bf16_gemm_lib(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
-                         float beta, hipStream_t stream);
-// fp32 (strided-batched) GEMM on hipBLASLt: out_b[M][N] = in_b[M][K] W_b[N][K]^T, exact fp32
-// products, fp32 accumulate; ORATOR_ERR_UNSUPPORTED without a workspace-free plan.
-int launch_f32_gemm_lib(const float* in, const float* W, float* out, int M, int K, int N,
-                        int batch, long stride_in, long stride_w, long stride_out,
-                        hipStream_t stream);
-// out[M][N] += in[M][K] W[N][K]^T (the residual add folded into the library GEMM's beta = 1;
-// below its size, this library's GEMM into tmp [M][N] and an add).
+// out[M][N] += in[M][K] W[N][K]^T: the residual add folded into the GEMM's store (M > 1); the
+// M = 1 GEMV writes tmp [N] and an add follows.
 int launch_linear_pre_acc(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
                           float* tmp, hipStream_t stream);
 // RmsNorm with the bf16 cast of its output folded in; SwiGLU of a fused gate|up block
@@ -140,6 +131,11 @@ int launch_linear_pre_acc(const uint16_t* in, const uint16_t* W, float* out, int
 int launch_rms_norm_bf16(const float* x, const float* w, uint16_t* out, int rows, int dim,
                          float eps, hipStream_t s);
 int launch_swiglu_bf16(const float* gu, uint16_t* out, int T, int I, hipStream_t s);
+
+// This library's bf16 GEMM (gemm_bf16.hip): out[M][N] (= or +=) act(in[M][K] W[N][K]^T +
+// bias), fp32 accumulation and output; K a multiple of 8, 16-byte aligned operands.
+int launch_gemm_bf16_nt(const uint16_t* in, const uint16_t* W, const float* bias, float* out,
+                        int M, int K, int N, int act, bool accumulate, hipStream_t s);
 
 int launch_sgemm(const float* in, const float* W, const float* bias, float* out, int M, int K,
                  int N, int act, int batch, long stride_in, long stride_w, long stride_out,

@@ -9,10 +9,7 @@
 //    4 output rows; each lane reads 16 contiguous bytes of each row per step, so a wave
 //    instruction moves one contiguous 1 KB piece of a row, and the k loop is unrolled so a
 //    lane keeps 16 such loads in flight.  x (4-12 KB) is read through the caches.
-//  * M > 1 (prefill) is MFMA-bound: 128 x 128 output tiles per workgroup, 4 waves of
-//    64 x 64 (2 x 2 v_mfma_f32_32x32x16_bf16 blocks); both operands are K-contiguous in
-//    memory, exactly the MFMA fragment layout, staged through double-buffered padded LDS
-//    (K steps of 32; 80-byte rows keep the fragment reads conflict-free).
+//  * M > 1 (prefill) is MFMA-bound: this library's bf16 GEMM (gemm_bf16.hip).
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -255,101 +252,6 @@ int launch_fused_mode(const float* x, const float* aux, float eps, const uint16_
   return launch_fused_u<MODE, ACC, 4>(x, aux, eps, W, out, K, N, pair, s);
 }
 
-// ------------------------------------------------------------------- GEMM (M > 1) ----
-constexpr int kTM = 128, kTN = 128, kTK = 32;
-constexpr int kLRow = kTK + 8;  // padded LDS row (bf16): 80 bytes
-
-__device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-__global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restrict__ A,
-                                                        const uint16_t* __restrict__ W,
-                                                        const float* __restrict__ bias,
-                                                        float* __restrict__ out, int M, int K,
-                                                        int N, int act) {
-  __shared__ __align__(16) uint16_t as[2][kTM][kLRow];
-  __shared__ __align__(16) uint16_t ws[2][kTN][kLRow];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;  // this wave's 64 x 64 quadrant
-  const int m0 = blockIdx.y * kTM, n0 = blockIdx.x * kTN;
-  // loader: rows tid/4 and tid/4 + 64 of each tile, 16-byte chunk tid%4 (8 k values)
-  const int lr = tid >> 2, lc = tid & 3;
-  u32x4_t ra[2], rw[2];
-  auto load = [&](int k0) {
-    const int kk = k0 + 8 * lc;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int m = m0 + lr + 64 * h, n = n0 + lr + 64 * h;
-      ra[h] = (m < M && kk < K)
-                  ? *reinterpret_cast<const u32x4_t*>(A + static_cast<long>(m) * K + kk)
-                  : u32x4_t{0, 0, 0, 0};
-      rw[h] = (n < N && kk < K)
-                  ? *reinterpret_cast<const u32x4_t*>(W + static_cast<long>(n) * K + kk)
-                  : u32x4_t{0, 0, 0, 0};
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      *reinterpret_cast<u32x4_t*>(&as[buf][lr + 64 * h][8 * lc]) = ra[h];
-      *reinterpret_cast<u32x4_t*>(&ws[buf][lr + 64 * h][8 * lc]) = rw[h];
-    }
-  };
-  f32x16_t acc[2][2] = {};
-  const int n_k = (K + kTK - 1) / kTK;
-  load(0);
-  store(0);
-  lds_barrier();
-  for (int t = 0; t < n_k; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < n_k) load((t + 1) * kTK);
-#pragma unroll
-    for (int ks = 0; ks < kTK / 16; ++ks) {
-      bf16x8_t fa[2], fb[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        fa[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(
-                                                 &as[buf][64 * wm + 32 * i + (lane & 31)]
-                                                    [16 * ks + 8 * (lane >> 5)]));
-        fb[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(
-                                                 &ws[buf][64 * wn + 32 * i + (lane & 31)]
-                                                    [16 * ks + 8 * (lane >> 5)]));
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
-    }
-    if (t + 1 < n_k) store(buf ^ 1);
-    lds_barrier();
-  }
-  // C block (i, j): lane holds column n = 32j + lane%32 and rows 8q + 4(lane/32) + e
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + 64 * wn + 32 * j + (lane & 31);
-    if (n >= N) continue;
-    const float bv = bias ? bias[n] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (m < M) out[static_cast<long>(m) * N + n] = apply_act(acc[i][j][e] + bv, act);
-      }
-  }
-}
-
-// out[m][n] = act(out[m][n] + bias[n]) after a library GEMM.
-__global__ __launch_bounds__(256) void bias_act_kernel(float* __restrict__ out,
-                                                       const float* __restrict__ bias, long n_all,
-                                                       int N, int act) {
-  const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n_all) out[i] = apply_act(out[i] + (bias ? bias[i % N] : 0.0f), act);
-}
-
 int check_linear(const void* in, const uint16_t* W, const float* out, int K, int act,
                  const char* who) {
   if (!in || !W || !out) return fail(ORATOR_ERR_INVALID, std::string(who) + ": null pointer");
@@ -366,23 +268,13 @@ int launch_bf16_gemm(const uint16_t* in, const uint16_t* W, const float* bias, f
                      int K, int N, int act, hipStream_t stream) {
   if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;  // reference no-op
   if (int rc = check_linear(in, W, out, K, act, "bf16_gemm")) return rc;
-  // Prompt-sized products go to the GEMM library (plain fp32-accumulated bf16 GEMM; bias and
-  // activation in one pass after it); small M, and shapes it has no plan for, run the MFMA
-  // kernel below.
-  if (M >= kLibMinM && bf16_gemm_lib_enabled()) {
-    const int rc = launch_bf16_gemm_lib(in, W, out, M, K, N, 0.0f, stream);
-    if (rc == ORATOR_OK) {
-      if (!bias && act == 0) return ORATOR_OK;
-      const long n_all = static_cast<long>(M) * N;
-      hipLaunchKernelGGL(bias_act_kernel, dim3(static_cast<unsigned>((n_all + 255) / 256)),
-                         dim3(256), 0, stream, out, bias, n_all, N, act);
-      return check_launch("bias_act_kernel");
-    }
-    if (rc != ORATOR_ERR_UNSUPPORTED) return rc;
+  if (M == 1) {  // one row: the weight-streaming GEMV
+    const int per_wg = kGemvRows * kGemvWaves;
+    hipLaunchKernelGGL(gemv_bf16_kernel, dim3((N + per_wg - 1) / per_wg), dim3(64 * kGemvWaves), 0,
+                       stream, in, W, bias, out, K, N, act);
+    return check_launch("gemv_bf16_kernel");
   }
-  const dim3 grid((N + kTN - 1) / kTN, (M + kTM - 1) / kTM);
-  hipLaunchKernelGGL(gemm_bf16_kernel, grid, dim3(256), 0, stream, in, W, bias, out, M, K, N, act);
-  return check_launch("gemm_bf16_kernel");
+  return launch_gemm_bf16_nt(in, W, bias, out, M, K, N, act, false, stream);
 }
 
 int launch_gemv_fused(int mode, const float* x, const float* aux, float eps, const uint16_t* W,
@@ -414,14 +306,6 @@ int launch_gemv_fused(int mode, const float* x, const float* aux, float eps, con
 
 int launch_linear_pre(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
                       int K, int N, int act, hipStream_t stream) {
-  if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;
-  if (int rc = check_linear(in, W, out, K, act, "linear")) return rc;
-  if (M == 1) {
-    const int per_wg = kGemvRows * kGemvWaves;
-    hipLaunchKernelGGL(gemv_bf16_kernel, dim3((N + per_wg - 1) / per_wg), dim3(64 * kGemvWaves), 0,
-                       stream, in, W, bias, out, K, N, act);
-    return check_launch("gemv_bf16_kernel");
-  }
   return launch_bf16_gemm(in, W, bias, out, M, K, N, act, stream);
 }
 
@@ -429,11 +313,8 @@ int launch_linear_pre_acc(const uint16_t* in, const uint16_t* W, float* out, int
                           float* tmp, hipStream_t stream) {
   if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;
   if (int rc = check_linear(in, W, out, K, 0, "linear_acc")) return rc;
-  if (M >= kLibMinM && bf16_gemm_lib_enabled()) {
-    const int rc = launch_bf16_gemm_lib(in, W, out, M, K, N, 1.0f, stream);
-    if (rc != ORATOR_ERR_UNSUPPORTED) return rc;
-  }
-  if (int rc = launch_linear_pre(in, W, nullptr, tmp, M, K, N, 0, stream)) return rc;
+  if (M > 1) return launch_gemm_bf16_nt(in, W, nullptr, out, M, K, N, 0, true, stream);
+  if (int rc = launch_bf16_gemm(in, W, nullptr, tmp, M, K, N, 0, stream)) return rc;
   return orator_add_residual(out, tmp, static_cast<long>(M) * N, stream);
 }
 

@@ -60,11 +60,11 @@ int device_cu_count() {
   return n;
 }
 
-void* workspace(hipStream_t stream, size_t bytes) {
+void* workspace(hipStream_t stream, size_t bytes, int slot) {
   int dev = 0;
   if (check_hip(hipGetDevice(&dev), "hipGetDevice") != ORATOR_OK) return nullptr;
   std::string err;
-  void* p = ws_pool().get(WsKey{dev, stream, std::this_thread::get_id()}, bytes, &err);
+  void* p = ws_pool().get(WsKey{dev, stream, std::this_thread::get_id(), slot}, bytes, &err);
   if (!p) (void)fail(ORATOR_ERR_HIP, err);
   return p;
 }

@@ -7,13 +7,19 @@
 // on v_mfma_f32_32x32x2_f32, so results stay within fp32 rounding of the reference's
 // k-sequential FMA chains.
 //
-// Products of at least 32 rows run on hipBLASLt (blaslt_gemm.cpp; fp32 compute, bias and
-// activation in one pass after it); the kernel below serves smaller products and shapes the
-// library has no plan for.
-//
-// Tiling: a workgroup of 4 wave64s computes a 64x64 output tile (2x2 waves of 32x32);
-// 64x16 slices of both operands are staged through padded LDS (row stride 17 floats, so
-// the 32 rows an MFMA operand load touches fall in distinct banks).
+// Workgroup = BM x BN tile of one batch entry, WGM x WGN waves, each (BM/WGM) x (BN/WGN) in
+// 32 x 32 blocks.  K advances 32 floats at a time through two LDS buffers (rows padded to 36
+// floats = 144 bytes: the 16 rows a quarter-wave reads land on distinct 16-byte bank groups).
+// MFMA k-step j takes k = 2j from the lower half-wave and 2j + 1 from the upper (the pairs in
+// k order, as a k-sequential chain adds them); LDS rows hold the even k then the odd k, so one
+// ds_read_b128 per lane still feeds four MFMAs.
+// The next K tile is loaded into registers while the current one is multiplied and is stored
+// half way through the step; one barrier per step.  When the output tiles do not cover the CUs
+// and K is long, K is split over workgroups and the partials are summed in a fixed order.
+#include <stdint.h>
+
+#include <algorithm>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -22,8 +28,8 @@ namespace {
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kTile = 64;
-constexpr int kBK = 16;
+constexpr int kSK = 32;        // K per step (floats)
+constexpr int kSLd = kSK + 4;  // padded LDS row
 
 __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == 1) return v / (1.0f + expf(-v));
@@ -32,91 +38,174 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void sgemm_nt_kernel(const float* __restrict__ in,
-                                                       const float* __restrict__ W,
-                                                       const float* __restrict__ bias,
-                                                       float* __restrict__ out, int M, int K,
-                                                       int N, int act, long stride_in,
-                                                       long stride_w, long stride_out) {
-  __shared__ float As[kTile][kBK + 1];
-  __shared__ float Bs[kTile][kBK + 1];
-  const int b = blockIdx.z;
-  const float* A = in + b * stride_in;
-  const float* Bm = W + b * stride_w;
-  float* C = out + b * stride_out;
-  const int m0 = blockIdx.y * kTile;
-  const int n0 = blockIdx.x * kTile;
+struct SgemmArgs {
+  const float* in;
+  const float* W;
+  const float* bias;
+  float* out;
+  float* part;  // split-K partials [splits][batch][M][N], or nullptr
+  int M, K, N, act, k_split;
+  int batch, splits;  // blockIdx.z = split * batch + batch entry
+  long s_in, s_w, s_out;
+  bool vec;  // K % 4 == 0 and 16-byte aligned operands: 16-byte loads
+};
+
+template <int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void sgemm_nt_kernel(SgemmArgs a) {
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int TM = BM / WGM, TN = BN / WGN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int RPI = NT / 8;  // rows per load instruction (8 threads x 16 bytes per row)
+  constexpr int LA = BM / RPI, LW = BN / RPI;
+  static_assert(LA >= 1 && LW >= 1, "tile rows cover one load instruction");
+  __shared__ __align__(16) float sA[2][BM][kSLd];
+  __shared__ __align__(16) float sW[2][BN][kSLd];
+
+  const int batch = blockIdx.z % a.batch;
+  const int split = blockIdx.z / a.batch;
+  const float* A = a.in + batch * a.s_in;
+  const float* B = a.W + batch * a.s_w;
+  const int M = a.M, N = a.N, K = a.K;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int lrow = tid >> 2;        // 0..63: tile row this thread stages
-  const int lk = (tid & 3) * 4;     // 4 consecutive k
-  const bool vec = (K & 3) == 0 && ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(Bm)) & 15) == 0;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int kb = split * a.k_split;
+  const int k_end = min(K, kb + a.k_split);
+  const int lr = tid >> 3, lc = tid & 7;
+  float4 ra[LA], rw[LW];
+  auto load_row = [&](const float* base, int row, int rows, int k) -> float4 {
+    if (row >= rows) return make_float4(0.f, 0.f, 0.f, 0.f);
+    const float* p = base + static_cast<long>(row) * K + k;
+    if (a.vec && k + 3 < k_end) return *reinterpret_cast<const float4*>(p);
+    float4 v;
+    v.x = k < k_end ? p[0] : 0.f;
+    v.y = k + 1 < k_end ? p[1] : 0.f;
+    v.z = k + 2 < k_end ? p[2] : 0.f;
+    v.w = k + 3 < k_end ? p[3] : 0.f;
+    return v;
+  };
+  auto load = [&](int k0) {
+    const int k = k0 + 4 * lc;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) ra[i] = load_row(A, m0 + RPI * i + lr, M, k);
+#pragma unroll
+    for (int i = 0; i < LW; ++i) rw[i] = load_row(B, n0 + RPI * i + lr, N, k);
+  };
+  // LDS row = [even k | odd k]: k = 4c..4c+3 of a 16-byte load go to slots 2c, 2c+1 of each
+  // half, so a lane of half h reading slots 4q..4q+3 of half h gets k = 2j + h, j = 4q..4q+3
+  auto put = [&](float* row, float4 v) {
+    *reinterpret_cast<float2*>(row + 2 * lc) = make_float2(v.x, v.z);
+    *reinterpret_cast<float2*>(row + 16 + 2 * lc) = make_float2(v.y, v.w);
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < LA; ++i) put(&sA[buf][RPI * i + lr][0], ra[i]);
+#pragma unroll
+    for (int i = 0; i < LW; ++i) put(&sW[buf][RPI * i + lr][0], rw[i]);
+  };
 
-  f32x16_t acc;
+  f32x16_t acc[FM][FN];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  for (int k0 = 0; k0 < K; k0 += kBK) {
-    float av[4], bv[4];
-    const int gm = m0 + lrow, gn = n0 + lrow, gk = k0 + lk;
-    if (vec && gk + 3 < K) {
-      const float4 a4 = gm < M ? *reinterpret_cast<const float4*>(A + static_cast<long>(gm) * K + gk)
-                               : make_float4(0, 0, 0, 0);
-      const float4 b4 = gn < N ? *reinterpret_cast<const float4*>(Bm + static_cast<long>(gn) * K + gk)
-                               : make_float4(0, 0, 0, 0);
-      av[0] = a4.x; av[1] = a4.y; av[2] = a4.z; av[3] = a4.w;
-      bv[0] = b4.x; bv[1] = b4.y; bv[2] = b4.z; bv[3] = b4.w;
-    } else {
+  const int fr = lane & 31, fk = 16 * (lane >> 5);
+  const int n_k = (k_end - kb + kSK - 1) / kSK;
+  load(kb);
+  store(0);
+  lds_barrier();
+  for (int t = 0; t < n_k; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < n_k) load(kb + (t + 1) * kSK);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        av[e] = (gm < M && gk + e < K) ? A[static_cast<long>(gm) * K + gk + e] : 0.0f;
-        bv[e] = (gn < N && gk + e < K) ? Bm[static_cast<long>(gn) * K + gk + e] : 0.0f;
-      }
-    }
+    for (int q = 0; q < 4; ++q) {
+      if (q == 2 && t + 1 < n_k) store(buf ^ 1);  // the other buffer is idle this step
+      float4 fa[FM], fb[FN];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      As[lrow][lk + e] = av[e];
-      Bs[lrow][lk + e] = bv[e];
-    }
-    __syncthreads();
+      for (int i = 0; i < FM; ++i)
+        fa[i] = *reinterpret_cast<const float4*>(&sA[buf][wm * TM + 32 * i + fr][fk + 4 * q]);
 #pragma unroll
-    for (int kk = 0; kk < kBK; kk += 2) {
-      const float a = As[32 * wm + (lane & 31)][kk + (lane >> 5)];
-      const float bb = Bs[32 * wn + (lane & 31)][kk + (lane >> 5)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc, 0, 0, 0);
+      for (int j = 0; j < FN; ++j)
+        fb[j] = *reinterpret_cast<const float4*>(&sW[buf][wn * TN + 32 * j + fr][fk + 4 * q]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][e], fb[j][e], acc[i][j], 0, 0, 0);
     }
-    __syncthreads();
+    lds_barrier();
   }
-  // accumulator layout: acc[4i + j] -> row 8i + 4*(lane/32) + j, column lane % 32
-  const int n = n0 + 32 * wn + (lane & 31);
-  if (n >= N) return;
-  const float bn = bias ? bias[n] : 0.0f;
+
+  // block (i, j): lane holds column n = 32 j + lane % 32 and rows 8 (e / 4) + 4 (lane / 32) +
+  // e % 4 of the block
+  float* C = a.part ? a.part + (static_cast<long>(split) * a.batch + batch) * M * N
+                    : a.out + batch * a.s_out;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn * TN + 32 * j + fr;
+    if (n >= N) continue;
+    const float bv = (!a.part && a.bias) ? a.bias[n] : 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + 32 * wm + 8 * i + 4 * (lane >> 5) + j;
-      if (m < M) {
-        float v = acc[4 * i + j];
-        if (bias) v += bn;
-        C[static_cast<long>(m) * N + n] = apply_act(v, act);
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (m < M) {
+          const float v = acc[i][j][e];
+          C[static_cast<long>(m) * N + n] = a.part ? v : apply_act(v + bv, a.act);
+        }
       }
-    }
+  }
 }
 
-// out_b[m][n] = act(out_b[m][n] + bias[n]) after a library GEMM.
-__global__ __launch_bounds__(256) void sgemm_bias_act_kernel(float* __restrict__ out,
-                                                             const float* __restrict__ bias,
-                                                             int M, int N, int act, long per,
-                                                             long stride_out, long total) {
-  const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const long b = i / per, r = i - b * per;
-  float* o = out + b * stride_out + r;
-  const float v = *o + (bias ? bias[r % N] : 0.0f);
-  *o = apply_act(v, act);
+// out_b[m][n] = act(sum_z part[z][b][m][n] + bias[n]), z ascending (a fixed order).
+__global__ __launch_bounds__(256) void sgemm_splitk_reduce_kernel(const float* __restrict__ part,
+                                                                  int splits, int batch,
+                                                                  const float* __restrict__ bias,
+                                                                  float* __restrict__ out, int M,
+                                                                  int N, int act, long s_out) {
+  const long MN = static_cast<long>(M) * N;
+  const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= MN * batch) return;
+  const long b = i / MN, r = i - b * MN;
+  const long per_split = MN * batch;
+  float v = part[i];
+  for (int z = 1; z < splits; ++z) v += part[z * per_split + i];
+  out[b * s_out + r] = apply_act(v + (bias ? bias[r % N] : 0.0f), act);
+}
+
+template <int BM, int BN, int WGM, int WGN>
+int launch_sg(SgemmArgs a, int batch, int splits, hipStream_t s) {
+  a.k_split = a.K;
+  a.part = nullptr;
+  if (splits > 1) {
+    a.k_split = ((a.K + splits - 1) / splits + kSK - 1) / kSK * kSK;
+    splits = (a.K + a.k_split - 1) / a.k_split;
+  }
+  a.batch = batch;
+  a.splits = splits;
+  const long MN = static_cast<long>(a.M) * a.N;
+  if (splits > 1) {
+    a.part = static_cast<float*>(
+        workspace(s, static_cast<size_t>(splits) * batch * MN * sizeof(float), kWsGemm));
+    if (!a.part) return ORATOR_ERR_HIP;
+  }
+  const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, batch * splits);
+  hipLaunchKernelGGL((sgemm_nt_kernel<BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), 0, s, a);
+  if (int rc = check_launch("sgemm_nt_kernel")) return rc;
+  if (splits == 1) return ORATOR_OK;
+  const long total = MN * batch;
+  hipLaunchKernelGGL(sgemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
+                     dim3(256), 0, s, a.part, splits, batch, a.bias, a.out, a.M, a.N, a.act,
+                     batch > 1 ? a.s_out : MN);
+  return check_launch("sgemm_splitk_reduce");
 }
 
 }  // namespace
@@ -127,26 +216,34 @@ int launch_sgemm(const float* in, const float* W, const float* bias, float* out,
   if (M <= 0 || N <= 0 || K <= 0 || batch <= 0) return ORATOR_OK;
   if (!in || !W || !out) return fail(ORATOR_ERR_INVALID, "sgemm: null pointer");
   if (act < 0 || act > 3) return fail(ORATOR_ERR_INVALID, "sgemm: act must be 0..3");
-  // Products of at least kLibMinM rows: the GEMM library (exact fp32 products), then bias and
-  // activation in one pass; shapes it has no plan for run the kernel above.
-  if (M >= kLibMinM && bf16_gemm_lib_enabled()) {
-    const long s_in = batch > 1 ? stride_in : 0, s_w = batch > 1 ? stride_w : 0,
-               s_out = batch > 1 ? stride_out : 0;
-    const int rc = launch_f32_gemm_lib(in, W, out, M, K, N, batch, s_in, s_w, s_out, stream);
-    if (rc == ORATOR_OK) {
-      if (!bias && act == 0) return ORATOR_OK;
-      const long per = static_cast<long>(M) * N, total = per * batch;
-      hipLaunchKernelGGL(sgemm_bias_act_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
-                         dim3(256), 0, stream, out, bias, M, N, act, per,
-                         batch > 1 ? stride_out : per, total);
-      return check_launch("sgemm_bias_act");
-    }
-    if (rc != ORATOR_ERR_UNSUPPORTED) return rc;
-  }
-  const dim3 grid((N + kTile - 1) / kTile, (M + kTile - 1) / kTile, batch);
-  hipLaunchKernelGGL(sgemm_nt_kernel, grid, dim3(256), 0, stream, in, W, bias, out, M, K, N, act,
-                     stride_in, stride_w, stride_out);
-  return check_launch("sgemm");
+  if (batch > 65535) return fail(ORATOR_ERR_UNSUPPORTED, "sgemm: at most 65535 batches");
+  SgemmArgs a{};
+  a.in = in;
+  a.W = W;
+  a.bias = bias;
+  a.out = out;
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.act = act;
+  a.s_in = batch > 1 ? stride_in : 0;
+  a.s_w = batch > 1 ? stride_w : 0;
+  a.s_out = batch > 1 ? stride_out : 0;
+  a.vec = (K & 3) == 0 && ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W) |
+                            (batch > 1 ? (stride_in | stride_w) * 4 : 0)) & 15) == 0;
+  // tile: the largest of 128 x 128 (8 waves) and 64 x 64 (4 waves) whose grid covers the CUs;
+  // K split over workgroups when even 64 x 64 tiles leave CUs idle and K is long
+  const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  auto tiles = [&](int bm, int bn) {
+    return static_cast<long>((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch;
+  };
+  if (tiles(128, 128) >= cus) return launch_sg<128, 128, 2, 4>(a, batch, 1, stream);
+  const long t = tiles(64, 64);
+  int splits = 1;
+  if (t < cus && K >= 256)
+    splits = static_cast<int>(std::min<long>((cus + t - 1) / t, K / 128));
+  if (static_cast<long>(batch) * splits > 65535) splits = 1;
+  return launch_sg<64, 64, 2, 2>(a, batch, splits, stream);
 }
 
 }  // namespace orator_hip

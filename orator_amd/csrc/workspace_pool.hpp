@@ -25,8 +25,9 @@ struct WsKey {
   int dev;
   const void* stream;
   std::thread::id tid;
+  int slot = 0;  // independent blocks for buffers that are live at the same time
   bool operator<(const WsKey& o) const {
-    return std::tie(dev, stream, tid) < std::tie(o.dev, o.stream, o.tid);
+    return std::tie(dev, stream, tid, slot) < std::tie(o.dev, o.stream, o.tid, o.slot);
   }
 };
 

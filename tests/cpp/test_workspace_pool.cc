@@ -53,13 +53,17 @@ int main() {
   std::thread th([&] { pt = pool.get(WsKey{0, s1, std::this_thread::get_id()}, 100, nullptr); });
   th.join();
   CHECK(pt && pt != p1 && pt != p2 && pool.held_blocks() == 3);
+  // another slot of the same stream and thread is a separate block
+  void* ps = pool.get(WsKey{0, s1, std::this_thread::get_id(), 1}, 100, nullptr);
+  CHECK(ps && ps != p2 && pool.held_blocks() == 4);
   // another stream and another device are separate
   void* q = pool.get(WsKey{0, s2, std::this_thread::get_id()}, 10, nullptr);
   void* r = pool.get(WsKey{1, s1, std::this_thread::get_id()}, 10, nullptr);
-  CHECK(q && r && pool.held_blocks() == 5);
-  // release of (dev 0, s1): one sync, frees p1, p2 and the other thread's block only
+  CHECK(q && r && pool.held_blocks() == 6);
+  // release of (dev 0, s1): one sync, frees p1, p2, the slot-1 block and the other thread's
+  // block only
   CHECK(pool.release_stream(0, s1) == 0 && g_syncs == 1);
-  CHECK(!g_live.count(p1) && !g_live.count(p2) && !g_live.count(pt));
+  CHECK(!g_live.count(p1) && !g_live.count(p2) && !g_live.count(pt) && !g_live.count(ps));
   CHECK(g_live.count(q) && g_live.count(r) && pool.held_blocks() == 2);
   // a later stream with the same handle value starts fresh
   void* p3 = pool.get(a, 10, nullptr);

@@ -21,8 +21,11 @@ QWEN_28L = dict(QWEN_2L, num_layers=28, max_seq_len=2048 + 256)
 
 # The configs[4] greedy-parity run (tests/golden/make_decoder_greedy_golden.py writes its
 # oracle tokens; tests/test_gpu_decoder_c5.py replays them): seeds of the weights and of the
-# N(0, 0.02) prefill embeddings, lm_head tied to the embedding as in Qwen3-1.7B.
-C5 = dict(weight_seed=2026, embed_seed=2027, prefill=2048, new=256, topk=32)
+# N(0, 0.02) prefill embeddings, lm_head tied to the embedding as in Qwen3-1.7B.  The weight
+# seed is one whose greedy stream does not repeat a token 6 times within 256 steps, so the
+# reference's repetition stop (asr_text_decoder.cu:741-757) does not end the graph-replayed
+# run early (seed 2026 stopped after 26 tokens, 2028 after 73, 2030 after 214).
+C5 = dict(weight_seed=2032, embed_seed=2033, prefill=2048, new=256, topk=32)
 
 
 def c5_inputs():

@@ -7,10 +7,11 @@ from the same seeds; src/model/asr_text_decoder.cu:457-617, :360-455, :698-889).
 Near ties.  The composition re-rounds activations to bf16 before every projection, so any
 two fp32 restatements that sum in different orders differ by whole bf16 steps and their
 logits drift apart.  The golden file measures that drift: a second CPU restatement whose
-linear layers are BLAS products (B) is run teacher-forced beside the oracle (A), and
-NOISE = 2 * max over all steps of |B - A| on A's top-32 logits.  A step is excused only when
-the oracle's own top-1 - top-2 margin is below NOISE; every other step must give the
-oracle's token.  Checks:
+linear layers are BLAS products (B) is run teacher-forced beside the oracle (A).  NOISE = the
+largest change of A's top-1 - top-2 margin that B's summation order causes at any of the 257
+steps (0.021 on max |logit| ~ 3; B itself picks another token at 6 steps, all with margins
+below 0.005).  A step is excused only when the oracle's margin there is below NOISE; every
+other step must give the oracle's token.  Checks:
   * teacher-forced: the device decodes the oracle's token stream step by step; its argmax
     (the library's ArgmaxBanned) must be the oracle's token at every non-excused step, and
     its logits at the oracle's top-32 ids within 1e-2 * max |logit| of the oracle's;
@@ -34,7 +35,6 @@ pytestmark = pytest.mark.gpu
 
 GOLD = Path(__file__).resolve().parent / "golden" / "decoder_greedy_c5.npz"
 LOGIT_TOL = 1e-2
-NOISE_MULT = 2.0
 
 
 def _expected_emitted(tokens, new):
@@ -60,7 +60,8 @@ def test_c5_greedy_token_ids_match_oracle():
     del layers, dl
     gold = g["tokens"]
     margins = (g["top_a"][:, 0] - g["top_a"][:, 1]).astype(np.float64)
-    noise = NOISE_MULT * float(np.max(np.abs(g["top_b"] - g["top_a"])))
+    margins_b = (g["top_b"][:, 0] - g["top_b"][:, 1]).astype(np.float64)
+    noise = float(np.max(np.abs(margins_b - margins)))
     excused = margins < noise
     print(f"c5: NOISE {noise:.4e}; oracle steps with margin below it: "
           f"{np.flatnonzero(excused).tolist()}", flush=True)
