@@ -7,17 +7,25 @@
 // consecutive k per lane), so tiles go from HBM to LDS row by row and back out as fragments
 // without any transpose.
 //
-// Workgroup = BM x BN output tile, 4 waves in a 2 x 2 grid, each wave (BM/2) x (BN/2) =
-// (BM/64) x (BN/64) blocks of 32 x 32 accumulators.  K advances 64 at a time through two LDS
-// buffers (rows padded to 72 elements = 144 bytes, which puts the 16 rows a quarter-wave reads
-// on 16 distinct 16-byte bank groups); the next K tile is loaded into registers while the
-// current one is multiplied and stored after it, one barrier per step.  Larger wave tiles
-// reuse each fragment read from LDS for more MFMAs (128 x 128 per wave: 8 fragment reads per
-// 16 MFMAs); the tile shape is chosen per problem so the grid covers the 256 CUs.
+// Workgroup = BM x BN output tile, 4 waves (one per SIMD) in a WGM x WGN grid, each wave
+// (BM/WGM) x (BN/WGN) = FM x FN blocks of 32 x 32 accumulators, two workgroups per CU (73.7 KB
+// of LDS each), so one workgroup's epilogue and barrier waits overlap the other's MFMAs.  K
+// advances 64 at a time through two LDS buffers (rows padded to 72 elements = 144 bytes,
+// which puts the 16 rows a quarter-wave reads on 16 distinct 16-byte bank groups); the next K
+// tile is loaded into registers during the current step and stored to the other buffer
+// before the step's last MFMAs, the next 16-deep fragments are read from LDS under the
+// current ones' MFMAs, one barrier per step.  Rows past M / N load the last valid row (their
+// outputs are never stored) and k chunks past K are zeroed by a mask, so the loads carry no
+// branches.  128 x 128 tiles when they give every CU a workgroup, else 128 x 64, with K split
+// over workgroups when even those leave CUs idle.  (Measured alternatives: 256 x 256 and
+// 256 x 128 tiles with 8 waves, one workgroup per CU, were 25-55 % slower at the decoder's
+// prompt shapes: their grids quantize badly on 256 CUs and their epilogue is not overlapped;
+// K = 32 steps with 3-4 workgroups per CU were 10-35 % slower.)
 #include <stdlib.h>
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 #include "internal.hpp"
@@ -38,8 +46,12 @@ __device__ __forceinline__ float gb_act(float v, int act) {
   return v;
 }
 
-template <int BM, int BN, int WGM, int WGN>
-__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_bf16_nt_kernel(
+// Epilogues: raw split-K partials, out = acc (no bias), out += acc + bias, and the general
+// out (= or +=) act(acc + bias).
+constexpr int kEpiPartial = 0, kEpiStore = 1, kEpiAccumulate = 2, kEpiAct = 3;
+
+template <int BM, int BN, int WGM, int WGN, int MINW, int EPI>
+__global__ __launch_bounds__(64 * WGM * WGN, MINW) void gemm_bf16_nt_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ W,
     const float* __restrict__ bias, float* __restrict__ C, int M, int K, int N, int act,
     int accumulate, float* __restrict__ part, int k_split) {
@@ -48,8 +60,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_bf16_nt_kernel(
   constexpr int FM = TM / 32, FN = TN / 32;        // 32 x 32 blocks per wave
   constexpr int RPI = NT / 8;                      // rows per load instruction
   constexpr int LA = BM / RPI, LW = BN / RPI;      // 16-byte loads per thread per K step
-  __shared__ __align__(16) uint16_t sA[2][BM][kLdk];
-  __shared__ __align__(16) uint16_t sW[2][BN][kLdk];
+  constexpr int KS = kBK / 16;                     // MFMA k-steps per K step
+  // LDS: the double-buffered A and W tiles during the K loop, then the fp32 output tile (rows
+  // padded by 8 floats: lanes 0-31 and 32-63 of an accumulator store, 4 rows apart, land 32
+  // banks apart)
+  constexpr int kCLd = BN + 8;
+  constexpr int kTileBytes = 2 * (BM + BN) * kLdk * 2;
+  constexpr int kOutBytes = BM * kCLd * 4;
+  __shared__ __align__(16) unsigned char smem[kTileBytes > kOutBytes ? kTileBytes : kOutBytes];
+  auto sA = reinterpret_cast<uint16_t(*)[BM][kLdk]>(smem);
+  auto sW = reinterpret_cast<uint16_t(*)[BN][kLdk]>(smem + 2 * BM * kLdk * 2);
+  auto sC = reinterpret_cast<float(*)[kCLd]>(smem);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -68,28 +89,44 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_bf16_nt_kernel(
   const int gm = min(tiles_m - first_m, kGroup);
   const int in_group = L - group * kGroup * tiles_n;
   const int m0 = (first_m + in_group % gm) * BM, n0 = (in_group / gm) * BN;
-  // loader: 32 rows x 128 bytes per instruction, thread = (row tid / 8, 16-byte chunk tid % 8)
+
+  // split-K: workgroup z covers k in [z * k_split, (z + 1) * k_split) (k_split a multiple of
+  // kBK) and leaves its raw partial sums in part[z]
+  const int kb = blockIdx.z * k_split;
+  const int k_lim = min(K - kb, k_split);  // a multiple of 8
+  const int n_k = (k_lim + kBK - 1) / kBK;
+  A += kb;
+  W += kb;
+  // loader: 32 rows x 128 bytes per instruction, thread = (row tid / 8, 16-byte chunk tid % 8);
+  // rows clamped into range, chunks past k_lim read in range and masked to zero
   const int lr = tid >> 3, lc = tid & 7;
-  gb_u32x4_t ra[LA], rw[LW];
   const long ld = K;  // row stride of A and W (elements)
-  int k_lim = K;      // set below for the split
+  const uint16_t* arow[LA];
+  const uint16_t* wrow[LW];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) arow[i] = A + min(m0 + RPI * i + lr, M - 1) * ld;
+#pragma unroll
+  for (int i = 0; i < LW; ++i) wrow[i] = W + min(n0 + RPI * i + lr, N - 1) * ld;
+  gb_u32x4_t ra[LA], rw[LW];
+  uint32_t keep = 0;  // mask of the chunk in flight; applied at the LDS store, and only on the
+                      // last K step when k_lim is not a multiple of kBK (a uniform branch)
   auto load = [&](int k0) {
     const int kk = k0 + 8 * lc;
-    const bool k_ok = kk < k_lim;
+    const int kc = min(kk, k_lim - 8);
+    keep = kk < k_lim ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      const int m = m0 + RPI * i + lr;
-      ra[i] = (m < M && k_ok) ? *reinterpret_cast<const gb_u32x4_t*>(A + m * ld + kk)
-                              : gb_u32x4_t{0, 0, 0, 0};
-    }
+    for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const gb_u32x4_t*>(arow[i] + kc);
 #pragma unroll
-    for (int i = 0; i < LW; ++i) {
-      const int n = n0 + RPI * i + lr;
-      rw[i] = (n < N && k_ok) ? *reinterpret_cast<const gb_u32x4_t*>(W + n * ld + kk)
-                              : gb_u32x4_t{0, 0, 0, 0};
-    }
+    for (int i = 0; i < LW; ++i) rw[i] = *reinterpret_cast<const gb_u32x4_t*>(wrow[i] + kc);
   };
-  auto store = [&](int buf) {
+  const bool ragged = (k_lim % kBK) != 0;
+  auto store = [&](int buf, bool masked) {
+    if (masked) {
+#pragma unroll
+      for (int i = 0; i < LA; ++i) ra[i] &= keep;
+#pragma unroll
+      for (int i = 0; i < LW; ++i) rw[i] &= keep;
+    }
 #pragma unroll
     for (int i = 0; i < LA; ++i)
       *reinterpret_cast<gb_u32x4_t*>(&sA[buf][RPI * i + lr][8 * lc]) = ra[i];
@@ -107,48 +144,48 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_bf16_nt_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   const int fr = lane & 31, fk = 8 * (lane >> 5);
-  // split-K: workgroup z covers k in [z * k_split, (z + 1) * k_split) (k_split a multiple of
-  // kBK) and leaves its raw partial sums in part[z]
-  const int kb = blockIdx.z * k_split;
-  const int n_k = (min(K, kb + k_split) - kb + kBK - 1) / kBK;
-  A += kb;
-  W += kb;
-  k_lim = min(K - kb, k_split);
   load(0);
-  store(0);
+  store(0, ragged && n_k == 1);
   lds_barrier();
   for (int t = 0; t < n_k; ++t) {
     const int buf = t & 1;
     if (t + 1 < n_k) load((t + 1) * kBK);
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      // the next tile's rows go to the other buffer half way through (its loads have long
-      // arrived; nobody reads that buffer during this step)
-      if (ks == kBK / 32 && t + 1 < n_k) store(buf ^ 1);
-      gb_bf16x8_t fa[FM], fb[FN];
+    gb_bf16x8_t fa[2][FM], fb[2][FN];
+    auto read = [&](int ks, int s) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        fa[i] = __builtin_bit_cast(
+        fa[s][i] = __builtin_bit_cast(
             gb_bf16x8_t, *reinterpret_cast<const gb_u32x4_t*>(
                              &sA[buf][wm * TM + 32 * i + fr][16 * ks + fk]));
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        fb[j] = __builtin_bit_cast(
+        fb[s][j] = __builtin_bit_cast(
             gb_bf16x8_t, *reinterpret_cast<const gb_u32x4_t*>(
                              &sW[buf][wn * TN + 32 * j + fr][16 * ks + fk]));
+    };
+    read(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int s = ks & 1;
+      if (ks + 1 < KS) read(ks + 1, s ^ 1);
+      // the next tile's rows go to the other buffer before the last k-step's MFMAs (nobody
+      // reads that buffer during this step)
+      if (ks == KS - 1 && t + 1 < n_k) store(buf ^ 1, ragged && t + 2 == n_k);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
     }
     lds_barrier();
   }
 
-  // block (i, j): lane holds column n = 32 j + lane % 32 and rows 8 (e / 4) + 4 (lane / 32) +
-  // e % 4 of the block
-  if (part) {
-    float* P = part + static_cast<long>(blockIdx.z) * M * N;
+  // Plain stores (no bias) and split-K partials: straight from the accumulators (block (i, j):
+  // lane holds column 32 j + lane % 32 and rows 8 (e / 4) + 4 (lane / 32) + e % 4 of the
+  // block); nothing is loaded, so the stores never wait.
+  if constexpr (EPI == kEpiStore || EPI == kEpiPartial) {
+    float* out = C;
+    if constexpr (EPI == kEpiPartial) out = part + static_cast<long>(blockIdx.z) * M * N;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = n0 + wn * TN + 32 * j + fr;
@@ -158,27 +195,68 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_bf16_nt_kernel(
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-          if (m < M) P[static_cast<long>(m) * N + n] = acc[i][j][e];
+          if (m < M) out[static_cast<long>(m) * N + n] = acc[i][j][e];
         }
     }
     return;
   }
+  // Bias, activation or accumulate: through LDS.  The accumulators go to the fp32 tile in LDS
+  // (same lane mapping), then the workgroup writes the tile out row by row in 16-byte pieces.  An accumulating
+  // epilogue loads all its old values before its first store: stores count against the same
+  // wait counter as loads, so a load issued behind stores would wait for them too.
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn * TN + 32 * j + fr;
-    if (n >= N) continue;
-    const float bv = bias ? bias[n] : 0.0f;
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (m < M) {
-          float* o = C + static_cast<long>(m) * N + n;
-          const float v = gb_act(acc[i][j][e] + bv, act);
-          *o = accumulate ? *o + v : v;
-        }
-      }
+      for (int e = 0; e < 16; ++e)
+        sC[wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)][wn * TN + 32 * j + fr] =
+            acc[i][j][e];
+  __syncthreads();
+
+  float* out = C;
+  constexpr int TPRo = BN / 4;            // threads per output row (4 floats each)
+  constexpr int RPIo = NT / TPRo;         // rows per pass
+  constexpr int PASSES = BM / RPIo;
+  const int orow = tid / TPRo, ocol = 4 * (tid % TPRo);
+  const int n = n0 + ocol;
+  const bool vec = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  const bool add_old = EPI == kEpiAccumulate || (EPI == kEpiAct && accumulate);
+  float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (bias) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv[q] = bias[min(n + q, N - 1)];
+  }
+  float old[PASSES][4];
+  if (add_old) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const float* src = out + static_cast<long>(min(m0 + RPIo * p + orow, M - 1)) * N;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) old[p][q] = src[min(n + q, N - 1)];
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int r = RPIo * p + orow;
+    const int m = m0 + r;
+    const float4 c = *reinterpret_cast<const float4*>(&sC[r][ocol]);
+    float v[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v[q] += bv[q];
+      if constexpr (EPI == kEpiAct) v[q] = gb_act(v[q], act);
+      if (add_old) v[q] += old[p][q];
+    }
+    if (m >= M) continue;
+    float* dst = out + static_cast<long>(m) * N + n;
+    if (vec && n + 3 < N) {
+      *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n + q < N) dst[q] = v[q];
+    }
   }
 }
 
@@ -195,7 +273,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   out[i] = accumulate ? out[i] + v : v;
 }
 
-template <int BM, int BN, int WGM, int WGN>
+template <int BM, int BN, int WGM, int WGN, int MINW>
 int launch_tile(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
                 int K, int N, int act, bool accumulate, int splits, hipStream_t s) {
   const int k_split = splits > 1 ? ((K + splits - 1) / splits + kBK - 1) / kBK * kBK : K;
@@ -208,20 +286,34 @@ int launch_tile(const uint16_t* in, const uint16_t* W, const float* bias, float*
     if (!part) return ORATOR_ERR_HIP;
   }
   const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, splits);
-  hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), 0, s,
-                     in, W, bias, out, M, K, N, act, accumulate ? 1 : 0, part, k_split);
+  const dim3 block(64 * WGM * WGN);
+  const int acc = accumulate ? 1 : 0;
+  if (splits > 1)
+    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiPartial>), grid, block, 0,
+                       s, in, W, bias, out, M, K, N, act, acc, part, k_split);
+  else if (act != 0 || (bias && !accumulate))
+    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiAct>), grid, block, 0, s,
+                       in, W, bias, out, M, K, N, act, acc, part, k_split);
+  else if (accumulate)
+    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiAccumulate>), grid, block,
+                       0, s, in, W, bias, out, M, K, N, act, acc, part, k_split);
+  else
+    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiStore>), grid, block, 0,
+                       s, in, W, bias, out, M, K, N, act, acc, part, k_split);
   if (int rc = check_launch("gemm_bf16_nt_kernel")) return rc;
   if (splits == 1) return ORATOR_OK;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((MN + 255) / 256)),
-                     dim3(256), 0, s, part, splits, bias, out, MN, N, act, accumulate ? 1 : 0);
+                     dim3(256), 0, s, part, splits, bias, out, MN, N, act, acc);
   return check_launch("splitk_reduce_kernel");
 }
 
 }  // namespace
 
-// Tile shape by grid size: 8 waves per workgroup (two per SIMD) on the largest tile whose grid
-// still gives every CU a workgroup; when even 128 x 128 tiles leave CUs idle and K is long, K
-// is split over workgroups (partials reduced in a fixed order: deterministic).
+// Tile shape by grid size: 128 x 128 when that grid gives every CU a workgroup, else 128 x 64;
+// when even that leaves CUs idle and K is long, K is split over workgroups (partials reduced
+// in a fixed order: deterministic).  Measured at the 503-row prompt shapes: 128 x 64 unsplit
+// beats a K split whenever its grid covers the CUs (qkv, 21.7 vs 23.7 us); below that, splits
+// to two workgroups per CU beat one (down projection, 28.4 vs 36.8 us).
 int launch_gemm_bf16_nt(const uint16_t* in, const uint16_t* W, const float* bias, float* out,
                         int M, int K, int N, int act, bool accumulate, hipStream_t s) {
   if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;
@@ -229,14 +321,15 @@ int launch_gemm_bf16_nt(const uint16_t* in, const uint16_t* W, const float* bias
   auto tiles = [&](int bm, int bn) {
     return static_cast<long>((M + bm - 1) / bm) * ((N + bn - 1) / bn);
   };
-  if (tiles(256, 256) >= cus)
-    return launch_tile<256, 256, 2, 4>(in, W, bias, out, M, K, N, act, accumulate, 1, s);
-  if (tiles(256, 128) >= cus)
-    return launch_tile<256, 128, 4, 2>(in, W, bias, out, M, K, N, act, accumulate, 1, s);
-  const long t = tiles(128, 128);
+  if (tiles(128, 128) >= cus)
+    return launch_tile<128, 128, 2, 2, 2>(in, W, bias, out, M, K, N, act, accumulate, 1, s);
+  // when even 128 x 64 tiles leave CUs idle, split K until the grid gives every CU two
+  // workgroups (K / 512 splits at most)
+  const long t = tiles(128, 64);
   int splits = 1;
-  if (t < cus) splits = static_cast<int>(std::min<long>((cus + t - 1) / t, std::max(1, K / 512)));
-  return launch_tile<128, 128, 2, 4>(in, W, bias, out, M, K, N, act, accumulate, splits, s);
+  if (t < cus)
+    splits = static_cast<int>(std::min<long>((2 * cus + t - 1) / t, std::max(1, K / 512)));
+  return launch_tile<128, 64, 4, 1, 2>(in, W, bias, out, M, K, N, act, accumulate, splits, s);
 }
 
 }  // namespace orator_hip

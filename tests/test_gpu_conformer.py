@@ -33,7 +33,8 @@ def test_sgemm_batched_reference_test(rows, inner, cols, batch):
 
 
 @pytest.mark.parametrize("M,K,N,act", [(7, 13, 9, 0), (717, 512, 512, 0), (65, 64, 130, 1),
-                                       (100, 33, 70, 2), (5, 2048, 3, 3), (1433, 512, 512, 0)])
+                                       (100, 33, 70, 2), (5, 2048, 3, 3), (1433, 512, 512, 0),
+                                       (717, 512, 2048, 1), (2048, 512, 2048, 0)])
 def test_sgemm_bias_act_vs_oracle(M, K, N, act):
     r = SplitMix64(M * 3 + K + N)
     a, w, bias = r.normal((M, K)), r.normal((N, K), 1.0 / math.sqrt(K)), r.normal((N,))

@@ -56,6 +56,24 @@ def test_linear_pre_vs_oracle(M, K, N, act, with_bias):
     assert np.all(np.abs(got - ref) <= bound), np.max(np.abs(got - ref) / bound)
 
 
+@pytest.mark.parametrize("M,K,N", [(2048, 2048, 4096), (2048, 2048, 12288), (2048, 6144, 2048)])
+def test_linear_pre_prompt_tiles(M, K, N):
+    """The decoder's 2048-token prompt projections (q|k|v 4096, gate|up 12288, down 2048 rows of
+    2048 / 6144): the 256 x 128 and 256 x 256 tile paths of the GEMM (the shapes above take the
+    128 x 128 and split-K paths), same bound."""
+    r = SplitMix64(M + K + N)
+    x = orc.to_bf16(r.normal((M, K)))
+    W = orc.to_bf16(r.normal((N, K), 0.05))
+    xd, Wd = orc.from_bf16(x).astype(np.float64), orc.from_bf16(W).astype(np.float64)
+    ref = xd @ Wd.T
+    bound = 3e-5 * (np.abs(xd) @ np.abs(Wd).T + 1.0)
+    out = empty((M, N), np.float32)
+    say("linear_pre prompt", M, K, N)
+    asr_gemm.LinearPre(up(x), up(W), None, out, M, K, N, 0)
+    got = down(out, (M, N))
+    assert np.all(np.abs(got - ref) <= bound), np.max(np.abs(got - ref) / bound)
+
+
 @pytest.mark.parametrize("M", [1, 33])
 def test_linear_f32_input_casts_rne(M):
     """Linear == F32ToBf16 + LinearPre (the cast is round-to-nearest-even, bit-exact)."""
