@@ -7,15 +7,18 @@
 // on v_mfma_f32_32x32x2_f32, so results stay within fp32 rounding of the reference's
 // k-sequential FMA chains.
 //
-// Workgroup = BM x BN tile of one batch entry, WGM x WGN waves, each (BM/WGM) x (BN/WGN) in
-// 32 x 32 blocks.  K advances 32 floats at a time through two LDS buffers (rows padded to 36
-// floats = 144 bytes: the 16 rows a quarter-wave reads land on distinct 16-byte bank groups).
-// MFMA k-step j takes k = 2j from the lower half-wave and 2j + 1 from the upper (the pairs in
-// k order, as a k-sequential chain adds them); LDS rows hold the even k then the odd k, so one
-// ds_read_b128 per lane still feeds four MFMAs.
-// The next K tile is loaded into registers while the current one is multiplied and is stored
-// half way through the step; one barrier per step.  When the output tiles do not cover the CUs
-// and K is long, K is split over workgroups and the partials are summed in a fixed order.
+// Workgroup = 64 x 64 tile of one batch entry, 4 waves of one 32 x 32 block each, four
+// workgroups per CU (fp32 MFMA is 16x slower per flop than bf16, so these small products are
+// latency-bound and want many resident waves, not big tiles: 128 x 128 tiles measured 1.6-2.8x
+// slower at the Conformer's shapes).  K advances 32 floats at a time through two LDS buffers
+// (rows padded to 36 floats = 144 bytes: the 16 rows a quarter-wave reads land on distinct
+// 16-byte bank groups).  MFMA k-step j takes k = 2j from the lower half-wave and 2j + 1 from
+// the upper (the pairs in k order, as a k-sequential chain adds them); LDS rows hold the even k
+// then the odd k, so one ds_read_b128 per lane still feeds four MFMAs.  The next K tile is
+// loaded into registers while the current one is multiplied and stored before the step's last
+// MFMAs, the next fragments are read under the current ones; one barrier per step.  When the
+// grid leaves CUs idle and K is long, K is split over workgroups and the partials are summed
+// in a fixed order.
 #include <stdint.h>
 
 #include <algorithm>
@@ -47,19 +50,30 @@ struct SgemmArgs {
   int M, K, N, act, k_split;
   int batch, splits;  // blockIdx.z = split * batch + batch entry
   long s_in, s_w, s_out;
-  bool vec;  // K % 4 == 0 and 16-byte aligned operands: 16-byte loads
+  bool vec;  // K % 32 == 0 and 16-byte aligned operands: 16-byte loads
 };
 
-template <int BM, int BN, int WGM, int WGN>
-__global__ __launch_bounds__(64 * WGM * WGN) void sgemm_nt_kernel(SgemmArgs a) {
+// Epilogues: raw split-K partials, out = acc (no bias, act 0), and out = act(acc + bias)
+// through LDS.
+constexpr int kSEpiPartial = 0, kSEpiStore = 1, kSEpiAct = 2;
+
+template <int BM, int BN, int WGM, int WGN, int MINW, bool VEC, int EPI>
+__global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArgs a) {
   constexpr int NT = 64 * WGM * WGN;
   constexpr int TM = BM / WGM, TN = BN / WGN;
   constexpr int FM = TM / 32, FN = TN / 32;
   constexpr int RPI = NT / 8;  // rows per load instruction (8 threads x 16 bytes per row)
   constexpr int LA = BM / RPI, LW = BN / RPI;
   static_assert(LA >= 1 && LW >= 1, "tile rows cover one load instruction");
-  __shared__ __align__(16) float sA[2][BM][kSLd];
-  __shared__ __align__(16) float sW[2][BN][kSLd];
+  // LDS: the double-buffered tiles during the K loop, then (bias / activation epilogue) the
+  // fp32 output tile, rows padded by 8 floats
+  constexpr int kCLd = BN + 8;
+  constexpr int kTileBytes = 2 * (BM + BN) * kSLd * 4;
+  constexpr int kOutBytes = BM * kCLd * 4;
+  __shared__ __align__(16) unsigned char smem[kTileBytes > kOutBytes ? kTileBytes : kOutBytes];
+  auto sA = reinterpret_cast<float(*)[BM][kSLd]>(smem);
+  auto sW = reinterpret_cast<float(*)[BN][kSLd]>(smem + 2 * BM * kSLd * 4);
+  auto sC = reinterpret_cast<float(*)[kCLd]>(smem);
 
   const int batch = blockIdx.z % a.batch;
   const int split = blockIdx.z / a.batch;
@@ -74,11 +88,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void sgemm_nt_kernel(SgemmArgs a) {
   const int kb = split * a.k_split;
   const int k_end = min(K, kb + a.k_split);
   const int lr = tid >> 3, lc = tid & 7;
+  // 16-byte loads (VEC: K a multiple of the 32-float step, 16-byte aligned operands, so every
+  // split is whole steps): rows clamped into range (their outputs are never stored), no
+  // branches.  Otherwise guarded scalar loads.
+  const float* arow[LA];
+  const float* wrow[LW];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) arow[i] = A + static_cast<long>(min(m0 + RPI * i + lr, M - 1)) * K;
+#pragma unroll
+  for (int i = 0; i < LW; ++i) wrow[i] = B + static_cast<long>(min(n0 + RPI * i + lr, N - 1)) * K;
   float4 ra[LA], rw[LW];
-  auto load_row = [&](const float* base, int row, int rows, int k) -> float4 {
+  auto load_guarded = [&](const float* base, int row, int rows, int k) -> float4 {
     if (row >= rows) return make_float4(0.f, 0.f, 0.f, 0.f);
     const float* p = base + static_cast<long>(row) * K + k;
-    if (a.vec && k + 3 < k_end) return *reinterpret_cast<const float4*>(p);
     float4 v;
     v.x = k < k_end ? p[0] : 0.f;
     v.y = k + 1 < k_end ? p[1] : 0.f;
@@ -88,10 +110,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void sgemm_nt_kernel(SgemmArgs a) {
   };
   auto load = [&](int k0) {
     const int k = k0 + 4 * lc;
+    if constexpr (VEC) {
 #pragma unroll
-    for (int i = 0; i < LA; ++i) ra[i] = load_row(A, m0 + RPI * i + lr, M, k);
+      for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const float4*>(arow[i] + k);
 #pragma unroll
-    for (int i = 0; i < LW; ++i) rw[i] = load_row(B, n0 + RPI * i + lr, N, k);
+      for (int i = 0; i < LW; ++i) rw[i] = *reinterpret_cast<const float4*>(wrow[i] + k);
+    } else {
+#pragma unroll
+      for (int i = 0; i < LA; ++i) ra[i] = load_guarded(A, m0 + RPI * i + lr, M, k);
+#pragma unroll
+      for (int i = 0; i < LW; ++i) rw[i] = load_guarded(B, n0 + RPI * i + lr, N, k);
+    }
   };
   // LDS row = [even k | odd k]: k = 4c..4c+3 of a 16-byte load go to slots 2c, 2c+1 of each
   // half, so a lane of half h reading slots 4q..4q+3 of half h gets k = 2j + h, j = 4q..4q+3
@@ -122,46 +151,92 @@ __global__ __launch_bounds__(64 * WGM * WGN) void sgemm_nt_kernel(SgemmArgs a) {
   for (int t = 0; t < n_k; ++t) {
     const int buf = t & 1;
     if (t + 1 < n_k) load(kb + (t + 1) * kSK);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (q == 2 && t + 1 < n_k) store(buf ^ 1);  // the other buffer is idle this step
-      float4 fa[FM], fb[FN];
+    float4 fa[2][FM], fb[2][FN];
+    auto read = [&](int q, int s) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        fa[i] = *reinterpret_cast<const float4*>(&sA[buf][wm * TM + 32 * i + fr][fk + 4 * q]);
+        fa[s][i] = *reinterpret_cast<const float4*>(&sA[buf][wm * TM + 32 * i + fr][fk + 4 * q]);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        fb[j] = *reinterpret_cast<const float4*>(&sW[buf][wn * TN + 32 * j + fr][fk + 4 * q]);
+        fb[s][j] = *reinterpret_cast<const float4*>(&sW[buf][wn * TN + 32 * j + fr][fk + 4 * q]);
+    };
+    read(0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int s = q & 1;
+      if (q + 1 < 4) read(q + 1, s ^ 1);  // next fragments under this q's MFMAs
+      // the next tile goes to the other (idle) buffer before the step's last MFMAs
+      if (q == 3 && t + 1 < n_k) store(buf ^ 1);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][e], fb[j][e], acc[i][j], 0, 0, 0);
+            acc[i][j] =
+                __builtin_amdgcn_mfma_f32_32x32x2f32(fa[s][i][e], fb[s][j][e], acc[i][j], 0, 0, 0);
     }
     lds_barrier();
   }
 
-  // block (i, j): lane holds column n = 32 j + lane % 32 and rows 8 (e / 4) + 4 (lane / 32) +
-  // e % 4 of the block
-  float* C = a.part ? a.part + (static_cast<long>(split) * a.batch + batch) * M * N
-                    : a.out + batch * a.s_out;
+  // block (i, j): lane holds column 32 j + lane % 32 and rows 8 (e / 4) + 4 (lane / 32) + e % 4
+  // of the block.  Plain stores and partials go straight out (nothing is loaded, so no store
+  // waits); bias / activation go through LDS with the bias loaded before the first store
+  // (stores count against the same wait counter as loads).
+  if constexpr (EPI != kSEpiAct) {
+    float* C = EPI == kSEpiPartial
+                   ? a.part + (static_cast<long>(split) * a.batch + batch) * M * N
+                   : a.out + batch * a.s_out;
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn * TN + 32 * j + fr;
-    if (n >= N) continue;
-    const float bv = (!a.part && a.bias) ? a.bias[n] : 0.0f;
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * TN + 32 * j + fr;
+      if (n >= N) continue;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (m < M) {
-          const float v = acc[i][j][e];
-          C[static_cast<long>(m) * N + n] = a.part ? v : apply_act(v + bv, a.act);
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          if (m < M) C[static_cast<long>(m) * N + n] = acc[i][j][e];
         }
-      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        sC[wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)][wn * TN + 32 * j + fr] =
+            acc[i][j][e];
+  __syncthreads();
+  float* C = a.out + batch * a.s_out;
+  constexpr int TPRo = BN / 4, RPIo = NT / TPRo, PASSES = BM / RPIo;
+  const int orow = tid / TPRo, ocol = 4 * (tid % TPRo);
+  const int n = n0 + ocol;
+  const bool vec_out = (N % 4) == 0 && ((reinterpret_cast<uintptr_t>(C)) & 15) == 0;
+  float bv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (a.bias) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv[q] = a.bias[min(n + q, N - 1)];
+  }
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int r = RPIo * p + orow;
+    const int m = m0 + r;
+    const float4 c = *reinterpret_cast<const float4*>(&sC[r][ocol]);
+    float v[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = apply_act(v[q] + bv[q], a.act);
+    if (m >= M) continue;
+    float* dst = C + static_cast<long>(m) * N + n;
+    if (vec_out && n + 3 < N) {
+      *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n + q < N) dst[q] = v[q];
+    }
   }
 }
 
@@ -181,7 +256,7 @@ __global__ __launch_bounds__(256) void sgemm_splitk_reduce_kernel(const float* _
   out[b * s_out + r] = apply_act(v + (bias ? bias[r % N] : 0.0f), act);
 }
 
-template <int BM, int BN, int WGM, int WGN>
+template <int BM, int BN, int WGM, int WGN, int MINW, bool VEC>
 int launch_sg(SgemmArgs a, int batch, int splits, hipStream_t s) {
   a.k_split = a.K;
   a.part = nullptr;
@@ -198,7 +273,16 @@ int launch_sg(SgemmArgs a, int batch, int splits, hipStream_t s) {
     if (!a.part) return ORATOR_ERR_HIP;
   }
   const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, batch * splits);
-  hipLaunchKernelGGL((sgemm_nt_kernel<BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), 0, s, a);
+  const dim3 block(64 * WGM * WGN);
+  if (splits > 1)
+    hipLaunchKernelGGL((sgemm_nt_kernel<BM, BN, WGM, WGN, MINW, VEC, kSEpiPartial>), grid, block,
+                       0, s, a);
+  else if (a.bias || a.act)
+    hipLaunchKernelGGL((sgemm_nt_kernel<BM, BN, WGM, WGN, MINW, VEC, kSEpiAct>), grid, block, 0,
+                       s, a);
+  else
+    hipLaunchKernelGGL((sgemm_nt_kernel<BM, BN, WGM, WGN, MINW, VEC, kSEpiStore>), grid, block,
+                       0, s, a);
   if (int rc = check_launch("sgemm_nt_kernel")) return rc;
   if (splits == 1) return ORATOR_OK;
   const long total = MN * batch;
@@ -229,21 +313,21 @@ int launch_sgemm(const float* in, const float* W, const float* bias, float* out,
   a.s_in = batch > 1 ? stride_in : 0;
   a.s_w = batch > 1 ? stride_w : 0;
   a.s_out = batch > 1 ? stride_out : 0;
-  a.vec = (K & 3) == 0 && ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W) |
+  a.vec = (K % kSK) == 0 && ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W) |
                             (batch > 1 ? (stride_in | stride_w) * 4 : 0)) & 15) == 0;
-  // tile: the largest of 128 x 128 (8 waves) and 64 x 64 (4 waves) whose grid covers the CUs;
-  // K split over workgroups when even 64 x 64 tiles leave CUs idle and K is long
+  // 64 x 64 tiles, 4 waves of one 32 x 32 block each, four workgroups per CU.  K is split over
+  // workgroups only when the grid leaves more than half the CUs idle (up to two workgroups per
+  // CU, K / 256 splits at most).  Measured at the Conformer's shapes: 717 x 2048 -> 512 takes
+  // 27.7 us with 6 splits against 45.9 unsplit; 1433 x 512 -> 512 (184 tiles) 13.6 unsplit
+  // against 19.1 with 2 splits.
   const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  auto tiles = [&](int bm, int bn) {
-    return static_cast<long>((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch;
-  };
-  if (tiles(128, 128) >= cus) return launch_sg<128, 128, 2, 4>(a, batch, 1, stream);
-  const long t = tiles(64, 64);
+  const long t = static_cast<long>((M + 63) / 64) * ((N + 63) / 64) * batch;
   int splits = 1;
-  if (t < cus && K >= 256)
-    splits = static_cast<int>(std::min<long>((cus + t - 1) / t, K / 128));
+  if (2 * t <= cus && K >= 512)
+    splits = static_cast<int>(std::min<long>((2 * cus + t - 1) / t, K / 256));
   if (static_cast<long>(batch) * splits > 65535) splits = 1;
-  return launch_sg<64, 64, 2, 2>(a, batch, splits, stream);
+  if (a.vec) return launch_sg<64, 64, 2, 2, 4, true>(a, batch, splits, stream);
+  return launch_sg<64, 64, 2, 2, 4, false>(a, batch, splits, stream);
 }
 
 }  // namespace orator_hip
