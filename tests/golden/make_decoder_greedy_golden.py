@@ -33,20 +33,6 @@ import oracle_lib as orc  # noqa: E402
 OUT = Path(__file__).resolve().parent / "decoder_greedy_c5.npz"
 
 
-class BlasOrderDecoder(orc.OracleDecoder):
-    """The oracle's composition with float32 BLAS products instead of serial chains (weights
-    widened to fp32 once and kept)."""
-
-    _wide: dict = {}
-
-    def _lin(self, x_bf16, W):
-        key = (W.__array_interface__["data"][0], W.shape)
-        Wf = self._wide.get(key)
-        if Wf is None:
-            Wf = self._wide[key] = np.ascontiguousarray(orc.from_bf16(W))
-        return np.matmul(orc.from_bf16(x_bf16), Wf.T).astype(np.float32)
-
-
 def top(logits, k):
     ids = np.argsort(-logits.astype(np.float64), kind="stable")[:k]
     return ids.astype(np.int32), logits[ids].astype(np.float32)
@@ -58,7 +44,7 @@ def main() -> None:
     T, new, k = dm.C5["prefill"], dm.C5["new"], dm.C5["topk"]
     print(f"weights + embeddings {time.time() - t0:.1f} s", flush=True)
     A = orc.OracleDecoder(cfg, *w, threads=8)
-    B = BlasOrderDecoder(cfg, *w, threads=8)
+    B = orc.BlasOrderDecoder(cfg, *w, threads=8)
     n = new + 1
     rec = dict(tokens=np.zeros(n, np.int32), top_ids=np.zeros((n, k), np.int32),
                top_a=np.zeros((n, k), np.float32), top_b=np.zeros((n, k), np.float32),

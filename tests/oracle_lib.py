@@ -530,6 +530,41 @@ class OracleDecoder:
         return out, bodies
 
 
+class BlasOrderDecoder(OracleDecoder):
+    """The oracle's composition with every linear layer a float32 BLAS product (blocked
+    summation with FMA: another valid fp32 order) instead of the serial chains; weights
+    widened to fp32 once and kept.  Its logits beside the oracle's measure the noise that fp32
+    summation order alone causes in this composition (bf16 re-rounding of activations turns
+    last-bit differences into whole bf16 steps)."""
+
+    _wide: dict = {}
+
+    def _lin(self, x_bf16, W):
+        key = (W.__array_interface__["data"][0], W.shape)
+        Wf = self._wide.get(key)
+        if Wf is None:
+            Wf = self._wide[key] = np.ascontiguousarray(from_bf16(W))
+        return np.matmul(from_bf16(x_bf16), Wf.T).astype(np.float32)
+
+
+class TwinDecoder(OracleDecoder):
+    """The oracle (its logits are this object's) with a BlasOrderDecoder shadow stepped on the
+    same inputs (`shadow.logits`), so a greedy checker can tell a near tie that summation order
+    alone can flip from a real disagreement."""
+
+    def __init__(self, cfg, embed, final_norm, lm_head, layers, threads: int = 1):
+        super().__init__(cfg, embed, final_norm, lm_head, layers, threads)
+        self.shadow = BlasOrderDecoder(cfg, embed, final_norm, lm_head, layers, threads)
+
+    def prefill_at(self, embeds, pos0: int) -> None:
+        super().prefill_at(embeds, pos0)
+        self.shadow.prefill_at(embeds, pos0)
+
+    def decode_step(self, embed_row, pos: int) -> None:
+        super().decode_step(embed_row, pos)
+        self.shadow.decode_step(embed_row, pos)
+
+
 def greedy_schedule(max_new, ban_steps, batch, use_graph, graph_ready):
     """Cumulative body counts at each host harvest of DecodeGreedy
     (src/model/asr_text_decoder.cu:801-884): the eager loop runs banned bodies one at a time

@@ -590,6 +590,23 @@ def test_decoder_split_prefill_and_decode_step_equivalence():
     assert rel_err(d.logits, full, 0.05) < 1e-5
 
 
+def test_twin_decoder_keeps_the_oracle_and_shadows_it():
+    """The greedy checkers' TwinDecoder: its own logits are the oracle's bit for bit, and its
+    BLAS-order shadow differs from them only by fp32 summation order (within the decoder
+    logit bar, 1e-2 of max |logit|, and not identical: the orders do differ)."""
+    import decoder_model as dm
+    cfg = dict(dm.SMALL, num_layers=1, max_seq_len=64)
+    w = dm.make_weights(cfg, 5)
+    a, t = orc.OracleDecoder(cfg, *w), orc.TwinDecoder(cfg, *w)
+    emb = SplitMix64(6).normal((11, cfg["hidden_size"]), 0.02)
+    for d in (a, t):
+        d.prefill_at(emb[:10], 0)
+        d.decode_step(emb[10], 10)
+    np.testing.assert_array_equal(t.logits, a.logits)
+    gap = np.max(np.abs(t.shadow.logits - a.logits))
+    assert 0 < gap <= 1e-2 * np.max(np.abs(a.logits)), gap
+
+
 def test_decoder_zero_layers_is_embedding_head():
     """Zero projection weights leave the residual stream at the input: logits =
     lm_head . bf16(RmsNorm(x) * final_norm), checked with fp64 numpy."""
