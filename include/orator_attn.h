@@ -229,6 +229,13 @@ int orator_masked_mha(const float* q, const float* k, const float* v, float* out
  * GEMM.  K % 8 == 0, in and W 16-byte aligned. */
 int orator_linear_pre(const uint16_t* in_bf16, const uint16_t* W_bf16, const float* bias,
                       float* out, int M, int K, int N, int act, void* stream);
+/* The decoder MLP's gate|up projection with SwiGLU and the bf16 cast folded into the GEMM's
+ * epilogue: asr_gemm::LinearPre on the fused [gate; up] weight (2I rows), asr_ops::SwiGLU and
+ * F32ToBf16 (src/model/asr_text_decoder.cu:547-552, :424-428) in one launch.  out_bf16[M,I] =
+ * bf16_rne(silu(g) * u), g = in . W[0:I]^T, u = in . W[I:2I]^T, the same values as the three
+ * separate calls.  K % 8 == 0, I % 4 == 0.  No reference counterpart as one entry. */
+int orator_linear_pre_swiglu(const uint16_t* in_bf16, const uint16_t* W_gateup,
+                             uint16_t* out_bf16, int M, int K, int I, void* stream);
 /* asr_gemm::Linear (asr_gemm.h:27-31, asr_gemm.cu:160-167): the same with fp32 `in`, cast to
  * bf16 (round to nearest even) into library workspace first. */
 int orator_linear(const float* in_f32, const uint16_t* W_bf16, const float* bias, float* out,

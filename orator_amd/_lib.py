@@ -63,6 +63,7 @@ class ConformerWeights(C.Structure):
 SIGNATURES: dict[str, list] = {
     # bf16-weight linear and decode-step glue
     "orator_linear_pre": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "orator_linear_pre_swiglu": [_p, _p, _p, _i, _i, _i, _p],
     "orator_linear": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "orator_bf16_gemm": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "orator_embed_gather": [_p, _p, _p, _i, _p],

@@ -21,6 +21,15 @@ def LinearPre(in_bf16, W_bf16, bias, out, M: int, K: int, N: int, act: int,
          _sh(stream))
 
 
+def LinearPreSwiGLU(in_bf16, W_gateup_bf16, out_bf16, M: int, K: int, I: int,
+                    stream=None) -> None:
+    """The decoder MLP's gate|up projection, SwiGLU and bf16 cast in one launch:
+    out[M,I] (bf16) = bf16(silu(in . W[0:I]^T) * (in . W[I:2I]^T)) (asr_text_decoder.cu:
+    547-552); the same values as LinearPre + SwiGLU + F32ToBf16."""
+    call("orator_linear_pre_swiglu", ptr(in_bf16), ptr(W_gateup_bf16), ptr(out_bf16), M, K, I,
+         _sh(stream))
+
+
 def Shutdown() -> None:
     """The reference frees its cast scratch here; the library's workspace is released with
     the process, so there is nothing to do."""

@@ -179,6 +179,16 @@ struct Decoder {
     return ORATOR_OK;
   }
 
+  // act_bf16 = bf16(SwiGLU(norm_bf16 . gateup_w^T)) for T rows: one GEMM with the SwiGLU in
+  // its epilogue; a single row runs the GEMV and the standalone SwiGLU pass (same values).
+  int gate_up_swiglu(const uint16_t* gateup_w, int T, hipStream_t s) {
+    const int H = c.hidden_size, I = c.intermediate_size;
+    if (T > 1) return launch_gemm_bf16_swiglu(norm_bf16, gateup_w, act_bf16, gu, T, H, I, s);
+    if (int rc = orator_linear_pre(norm_bf16, gateup_w, nullptr, gu, T, H, 2 * I, 0, s))
+      return rc;
+    return launch_swiglu_bf16(gu, act_bf16, T, I, s);
+  }
+
   // Forward of T rows of residual stream x at positions pos0.. (asr_text_decoder.cu:457-583).
   int forward(int T, int pos0, hipStream_t s) {
     const int H = c.hidden_size, I = c.intermediate_size, Hq = c.num_q_heads,
@@ -198,7 +208,8 @@ struct Decoder {
     // Per layer, the reference's passes with the casts and residual adds folded in (same
     // fp32 values rounded once each): RmsNorm -> bf16, q and k|v projections (row slices of
     // the fused qkv weight), QK-norm/RoPE/KV write, attention, bf16 cast, o projection += x,
-    // RmsNorm -> bf16, the fused gate|up projection, SwiGLU -> bf16, down projection += x.
+    // RmsNorm -> bf16, the fused gate|up projection with SwiGLU -> bf16 in its epilogue, down
+    // projection += x.
     const long TQ = static_cast<long>(T) * Qd();
     for (int li = 0; li < c.num_layers && !rc; ++li) {
       const OratorDecoderLayer& L = layers[li];
@@ -215,8 +226,7 @@ struct Decoder {
           (rc = orator_f32_to_bf16(attn, act_bf16, TQ, s)) ||
           (rc = launch_linear_pre_acc(act_bf16, L.o_w, x, T, Qd(), H, proj, s)) ||
           (rc = launch_rms_norm_bf16(x, L.post_ln, norm_bf16, T, H, eps, s)) ||
-          (rc = orator_linear_pre(norm_bf16, L.gateup_w, nullptr, gu, T, H, 2 * I, 0, s)) ||
-          (rc = launch_swiglu_bf16(gu, act_bf16, T, I, s)) ||
+          (rc = gate_up_swiglu(L.gateup_w, T, s)) ||
           (rc = launch_linear_pre_acc(act_bf16, L.down_w, x, T, I, H, proj, s));
     }
     if (rc) return rc;

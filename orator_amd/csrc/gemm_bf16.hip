@@ -46,9 +46,11 @@ __device__ __forceinline__ float gb_act(float v, int act) {
   return v;
 }
 
-// Epilogues: raw split-K partials, out = acc (no bias), out += acc + bias, and the general
-// out (= or +=) act(acc + bias).
-constexpr int kEpiPartial = 0, kEpiStore = 1, kEpiAccumulate = 2, kEpiAct = 3;
+// Epilogues: raw split-K partials, out = acc (no bias), out += acc + bias, the general
+// out (= or +=) act(acc + bias), and SwiGLU: W holds gate rows [0, I) then up rows [I, 2I)
+// (N = 2I); a tile takes BN/2 gate rows and the matching BN/2 up rows, and stores
+// bf16(silu(gate) * up) for its BN/2 columns of the [M][I] bf16 output.
+constexpr int kEpiPartial = 0, kEpiStore = 1, kEpiAccumulate = 2, kEpiAct = 3, kEpiSwiglu = 4;
 
 template <int BM, int BN, int WGM, int WGN, int MINW, int EPI>
 __global__ __launch_bounds__(64 * WGM * WGN, MINW) void gemm_bf16_nt_kernel(
@@ -106,7 +108,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void gemm_bf16_nt_kernel(
 #pragma unroll
   for (int i = 0; i < LA; ++i) arow[i] = A + min(m0 + RPI * i + lr, M - 1) * ld;
 #pragma unroll
-  for (int i = 0; i < LW; ++i) wrow[i] = W + min(n0 + RPI * i + lr, N - 1) * ld;
+  for (int i = 0; i < LW; ++i) {
+    const int j = RPI * i + lr;  // tile row
+    long row;
+    if constexpr (EPI == kEpiSwiglu) {
+      const int I = N / 2, c0 = (n0 / BN) * (BN / 2);
+      row = j < BN / 2 ? min(c0 + j, I - 1) : I + min(c0 + j - BN / 2, I - 1);
+    } else {
+      row = min(n0 + j, N - 1);
+    }
+    wrow[i] = W + row * ld;
+  }
   gb_u32x4_t ra[LA], rw[LW];
   uint32_t keep = 0;  // mask of the chunk in flight; applied at the LDS store, and only on the
                       // last K step when k_lim is not a multiple of kBK (a uniform branch)
@@ -214,6 +226,38 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void gemm_bf16_nt_kernel(
             acc[i][j][e];
   __syncthreads();
 
+  if constexpr (EPI == kEpiSwiglu) {
+    // 4 output columns per thread: gate from tile column c, up from column BN/2 + c; the
+    // arithmetic of the standalone SwiGLU + cast (silu(g) * u in fp32, bf16 round to nearest
+    // even), so the result is bit-identical to GEMM -> SwiGLU -> F32ToBf16
+    const int I = N / 2, c0 = (n0 / BN) * (BN / 2);
+    uint16_t* ob = reinterpret_cast<uint16_t*>(C);
+    constexpr int TPRs = BN / 8;  // threads per output row
+    constexpr int RPIs = NT / TPRs;
+    const int srow = tid / TPRs, scol = 4 * (tid % TPRs);
+    const int col = c0 + scol;
+    const bool vec8 = (I % 4) == 0 && (reinterpret_cast<uintptr_t>(ob) & 7) == 0;
+#pragma unroll
+    for (int p = 0; p < BM / RPIs; ++p) {
+      const int r = RPIs * p + srow;
+      const int m = m0 + r;
+      const float4 g = *reinterpret_cast<const float4*>(&sC[r][scol]);
+      const float4 u = *reinterpret_cast<const float4*>(&sC[r][BN / 2 + scol]);
+      const float y0 = (g.x / (1.0f + expf(-g.x))) * u.x, y1 = (g.y / (1.0f + expf(-g.y))) * u.y;
+      const float y2 = (g.z / (1.0f + expf(-g.z))) * u.z, y3 = (g.w / (1.0f + expf(-g.w))) * u.w;
+      if (m >= M) continue;
+      uint16_t* dst = ob + static_cast<long>(m) * I + col;
+      if (vec8 && col + 3 < I) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(y0, y1), pack_bf16x2(y2, y3));
+      } else {
+        const float y[4] = {y0, y1, y2, y3};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (col + q < I) dst[q] = f32_to_bf16(y[q]);
+      }
+    }
+    return;
+  }
   float* out = C;
   constexpr int TPRo = BN / 4;            // threads per output row (4 floats each)
   constexpr int RPIo = NT / TPRo;         // rows per pass
@@ -308,6 +352,25 @@ int launch_tile(const uint16_t* in, const uint16_t* W, const float* bias, float*
 }
 
 }  // namespace
+
+// out[M][I] bf16 = bf16(silu(in W_gate^T) * (in W_up^T)), W = [gate; up] of 2I rows: the
+// gate|up projection with SwiGLU and the bf16 cast in its epilogue.  Grids too short for the
+// CUs (small M) take the plain GEMM (split K) and the standalone SwiGLU pass instead: the same
+// values either way.
+int launch_gemm_bf16_swiglu(const uint16_t* in, const uint16_t* W, uint16_t* out, float* tmp,
+                            int M, int K, int I, hipStream_t s) {
+  if (M <= 0 || K <= 0 || I <= 0) return ORATOR_OK;
+  const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const long tiles = static_cast<long>((M + 127) / 128) * ((I + 63) / 64);
+  if (tiles < cus) {
+    if (int rc = launch_gemm_bf16_nt(in, W, nullptr, tmp, M, K, 2 * I, 0, false, s)) return rc;
+    return launch_swiglu_bf16(tmp, out, M, I, s);
+  }
+  const dim3 grid(static_cast<unsigned>((I + 63) / 64), static_cast<unsigned>((M + 127) / 128), 1);
+  hipLaunchKernelGGL((gemm_bf16_nt_kernel<128, 128, 2, 2, 2, kEpiSwiglu>), grid, dim3(256), 0, s,
+                     in, W, nullptr, reinterpret_cast<float*>(out), M, K, 2 * I, 0, 0, nullptr, K);
+  return check_launch("gemm_bf16_nt_kernel (swiglu)");
+}
 
 // Tile shape by grid size: 128 x 128 when that grid gives every CU a workgroup, else 128 x 64;
 // when even that leaves CUs idle and K is long, K is split over workgroups (partials reduced

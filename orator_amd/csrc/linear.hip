@@ -330,6 +330,25 @@ int orator_linear_pre(const uint16_t* in_bf16, const uint16_t* W_bf16, const flo
                            static_cast<hipStream_t>(stream));
 }
 
+int orator_linear_pre_swiglu(const uint16_t* in_bf16, const uint16_t* W_gateup,
+                             uint16_t* out_bf16, int M, int K, int I, void* stream) {
+  if (M <= 0 || K <= 0 || I <= 0) return ORATOR_OK;
+  if (!out_bf16) return fail(ORATOR_ERR_INVALID, "linear_pre_swiglu: null pointer");
+  if (I % 4) return fail(ORATOR_ERR_UNSUPPORTED, "linear_pre_swiglu: I must be a multiple of 4");
+  if (int rc = check_linear(in_bf16, W_gateup, reinterpret_cast<const float*>(out_bf16), K, 0,
+                            "linear_pre_swiglu"))
+    return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  // the fp32 gate|up block is materialised only by the short-grid and M = 1 paths
+  float* tmp = static_cast<float*>(workspace(s, static_cast<size_t>(M) * 2 * I * sizeof(float)));
+  if (!tmp) return ORATOR_ERR_HIP;
+  if (M == 1) {
+    if (int rc = launch_bf16_gemm(in_bf16, W_gateup, nullptr, tmp, 1, K, 2 * I, 0, s)) return rc;
+    return launch_swiglu_bf16(tmp, out_bf16, 1, I, s);
+  }
+  return launch_gemm_bf16_swiglu(in_bf16, W_gateup, out_bf16, tmp, M, K, I, s);
+}
+
 int orator_linear(const float* in_f32, const uint16_t* W_bf16, const float* bias, float* out,
                   int M, int K, int N, int act, void* stream) {
   if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;

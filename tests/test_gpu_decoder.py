@@ -76,6 +76,32 @@ def test_linear_pre_prompt_tiles(M, K, N):
     assert np.all(np.abs(got - ref) <= bound), np.max(np.abs(got - ref) / bound)
 
 
+@pytest.mark.parametrize("M,K,I", [(2048, 2048, 6144), (503, 2048, 6144), (300, 1024, 6000),
+                                   (5, 512, 1000), (1, 512, 300)])
+def test_linear_pre_swiglu_equals_three_calls(M, K, I):
+    """The gate|up GEMM with SwiGLU + bf16 cast in its epilogue is bit-identical to LinearPre
+    on the fused [gate; up] weight, SwiGLU and F32ToBf16 (asr_text_decoder.cu:547-552): the
+    fused tile (2048 / 503 rows), a ragged one (300 rows, I = 6000: 64-column tiles cut at
+    the edge), the short-grid path (5 rows) and the GEMV path (1 row)."""
+    from orator_amd import asr_ops
+    r = SplitMix64(M + 3 * K + I)
+    x = orc.to_bf16(r.normal((M, K)))
+    W = orc.to_bf16(r.normal((2 * I, K), 0.05))
+    xd, Wd = up(x), up(W)
+    gu = empty((M, 2 * I), np.float32)
+    say("linear_pre_swiglu", M, K, I)
+    asr_gemm.LinearPre(xd, Wd, None, gu, M, K, 2 * I, 0)
+    g_u = down(gu, (M, 2 * I))
+    act = empty((M * I,), np.float32)
+    asr_ops.SwiGLU(up(np.ascontiguousarray(g_u[:, :I])), up(np.ascontiguousarray(g_u[:, I:])),
+                   act, M * I)
+    want = empty((M * I,), np.uint16)
+    asr_ops.F32ToBf16(act, want, M * I)
+    got = empty((M * I,), np.uint16)
+    asr_gemm.LinearPreSwiGLU(xd, Wd, got, M, K, I)
+    np.testing.assert_array_equal(down(got, (M, I), np.uint16), down(want, (M, I), np.uint16))
+
+
 @pytest.mark.parametrize("M", [1, 33])
 def test_linear_f32_input_casts_rne(M):
     """Linear == F32ToBf16 + LinearPre (the cast is round-to-nearest-even, bit-exact)."""
