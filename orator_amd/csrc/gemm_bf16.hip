@@ -15,12 +15,13 @@
 // tile is loaded into registers during the current step and stored to the other buffer
 // before the step's last MFMAs, the next 16-deep fragments are read from LDS under the
 // current ones' MFMAs, one barrier per step.  Rows past M / N load the last valid row (their
-// outputs are never stored) and k chunks past K are zeroed by a mask, so the loads carry no
-// branches.  128 x 128 tiles when they give every CU a workgroup, else 128 x 64, with K split
-// over workgroups when even those leave CUs idle.  (Measured alternatives: 256 x 256 and
-// 256 x 128 tiles with 8 waves, one workgroup per CU, were 25-55 % slower at the decoder's
-// prompt shapes: their grids quantize badly on 256 CUs and their epilogue is not overlapped;
-// K = 32 steps with 3-4 workgroups per CU were 10-35 % slower.)
+// outputs are never stored) and k chunks past K are zeroed by a mask on the last step, so the
+// loads carry no branches.  128 x 128 tiles when they give every CU two workgroups, else
+// 128 x 64, with K split over workgroups when even those leave CUs idle.  (Measured
+// alternatives: 256 x 256 and 256 x 128 tiles with 8 waves, one workgroup per CU, were
+// 25-55 % slower at the decoder's prompt shapes: their grids quantize badly on 256 CUs and
+// their epilogue is not overlapped; K = 32 steps with 3-4 workgroups per CU were 10-35 %
+// slower.)
 #include <stdlib.h>
 
 #include <algorithm>
@@ -372,9 +373,9 @@ int launch_gemm_bf16_swiglu(const uint16_t* in, const uint16_t* W, uint16_t* out
   return check_launch("gemm_bf16_nt_kernel (swiglu)");
 }
 
-// Tile shape by grid size: 128 x 128 when that grid gives every CU a workgroup, else 128 x 64;
-// when even that leaves CUs idle and K is long, K is split over workgroups (partials reduced
-// in a fixed order: deterministic).  Measured at the 503-row prompt shapes: 128 x 64 unsplit
+// Tile shape by grid size: 128 x 128 when that grid gives every CU two workgroups, else
+// 128 x 64; when even that leaves CUs idle and K is long, K is split over workgroups (partials
+// reduced in a fixed order: deterministic).  Measured at the 503-row prompt shapes: 128 x 64 unsplit
 // beats a K split whenever its grid covers the CUs (qkv, 21.7 vs 23.7 us); below that, splits
 // to two workgroups per CU beat one (down projection, 28.4 vs 36.8 us).
 int launch_gemm_bf16_nt(const uint16_t* in, const uint16_t* W, const float* bias, float* out,
@@ -384,7 +385,9 @@ int launch_gemm_bf16_nt(const uint16_t* in, const uint16_t* W, const float* bias
   auto tiles = [&](int bm, int bn) {
     return static_cast<long>((M + bm - 1) / bm) * ((N + bn - 1) / bn);
   };
-  if (tiles(128, 128) >= cus)
+  // 128 x 128 only when every CU gets two of them (one workgroup per CU leaves its epilogue
+  // exposed: the decoder's 2048 x 2048 -> 2048 projections ran 2 % faster on 128 x 64)
+  if (tiles(128, 128) >= 2 * cus)
     return launch_tile<128, 128, 2, 2, 2>(in, W, bias, out, M, K, N, act, accumulate, 1, s);
   // when even 128 x 64 tiles leave CUs idle, split K until the grid gives every CU two
   // workgroups (K / 512 splits at most)
