@@ -644,12 +644,8 @@ int launch_dh_g(const DecodeArgs& args, int B, int split, hipStream_t stream) {
   if constexpr (G == 4) {
     return launch_split<DH, G, 256, KV>(args, B, stream);
   } else {
-    switch (split) {
-      case 128: return launch_split<DH, G, 128, KV>(args, B, stream);
-      case 512: return launch_split<DH, G, 512, KV>(args, B, stream);
-      case 1024: return launch_split<DH, G, 1024, KV>(args, B, stream);
-      default: return launch_split<DH, G, 256, KV>(args, B, stream);
-    }
+    if (split == 128) return launch_split<DH, G, 128, KV>(args, B, stream);
+    return launch_split<DH, G, 256, KV>(args, B, stream);
   }
 }
 
@@ -665,17 +661,6 @@ int launch_kv(const DecodeArgs& args, int B, int Dh, int G, int split, hipStream
   return launch_dh_g<64, 4, KV>(args, B, split, stream);
 }
 
-// Tuning override (read once): ORATOR_DECODE_SPLIT in {128,256,512,1024} fixes the
-// split length instead of the occupancy heuristic.
-int split_override() {
-  static const int v = [] {
-    const char* e = getenv("ORATOR_DECODE_SPLIT");
-    const int x = e ? atoi(e) : 0;
-    return (x == 128 || x == 256 || x == 512 || x == 1024) ? x : 0;
-  }();
-  return v;
-}
-
 }  // namespace
 
 // Split length: 128 keys (one 32-key chunk per wave, 117 VGPRs, 4 waves/SIMD), measured
@@ -683,13 +668,11 @@ int split_override() {
 // single stream by 6-23%.  G = 4 keeps 4 heads of state per lane and runs 256-key splits.
 int choose_split(int /*B*/, int /*Hkv*/, int G, int /*capacity*/) {
   if (G == 4) return 256;  // the only G = 4 instantiation (launch_dh_g)
-  if (split_override()) return split_override();
   return 128;
 }
 
 size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity) {
-  int split = 128;  // the shortest split choose_split() returns
-  if (split_override()) split = split_override();
+  const int split = 128;  // the shortest split choose_split() returns
   const size_t max_splits = (static_cast<size_t>(capacity) + split - 1) / split;
   return static_cast<size_t>(B) * Hq * max_splits * (Dh + 2) * sizeof(float);
 }

@@ -590,24 +590,12 @@ int launch_g(PrefillArgs& args, bool precise, hipStream_t stream) {
   // MI355X: RW = 2 is faster at 2048 tokens x 8 kv heads, RW = 4 at 4096.
   const int cus = device_cu_count();
   const int blocks4 = (args.Tq + 4 * (32 / G) - 1) / (4 * (32 / G));
-  int rw = static_cast<long>(blocks4) * args.Hkv >= 2L * (cus > 0 ? cus : 256) ? 4 : 2;
-  // Tuning override (read once): ORATOR_PREFILL_RW in {2, 4} fixes the row-wave count.
-  static const int rw_override = [] {
-    const char* e = std::getenv("ORATOR_PREFILL_RW");
-    const int v = e ? std::atoi(e) : 0;
-    return v == 2 || v == 4 ? v : 0;
-  }();
-  if (rw_override) rw = rw_override;
+  const int rw = static_cast<long>(blocks4) * args.Hkv >= 2L * (cus > 0 ? cus : 256) ? 4 : 2;
   const int BT = rw * (32 / G);
   args.n_tblocks = (args.Tq + BT - 1) / BT;
   // Pairs of blocks (heavy n-1-i with light i) per workgroup once there are at least two
   // blocks per CU: one workgroup per CU instead of two back to back, and one prologue less.
-  static const int pair_override = [] {
-    const char* e = std::getenv("ORATOR_PREFILL_PAIR");
-    return e ? std::atoi(e) : -1;
-  }();
   args.paired = static_cast<long>(args.n_tblocks) * args.Hkv >= 2L * (cus > 0 ? cus : 256);
-  if (pair_override == 0 || pair_override == 1) args.paired = pair_override;
   return precise ? launch_rw<G, true>(args, rw, stream) : launch_rw<G, false>(args, rw, stream);
 }
 
