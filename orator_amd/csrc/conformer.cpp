@@ -6,7 +6,10 @@
 //                           BatchNorm(eval)+SiLU, pointwise C
 //   x += 0.5 FFN2(LN(x));  x = LN_out(x)
 // The projections run on the fp32 MFMA SGEMM; the attention core is either the reference
-// decomposition in fp32 (attn_mode 0) or the fused fp16 MFMA kernel (attn_mode 1).
+// decomposition in fp32 (attn_mode 0) or the fused fp16 MFMA kernel (attn_mode 1).  Each
+// residual update x += s * (h W^T + b) is the last projection's epilogue (the same fp32
+// value, then one fused multiply-add, exact for s = 0.5 and 1), q/k/v are one grouped launch
+// sharing LN(x), and the closing LayerNorm writes x in place.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -23,7 +26,6 @@ int launch_glu_mask(const float* in, float* out, int T, int C, int valid, hipStr
 int launch_dwconv_bn_silu(const float* in, const float* w, const float* bias, const float* mean,
                           const float* var, const float* gamma, const float* beta, float* out,
                           int T, int C, int K, float eps, hipStream_t s);
-int launch_add_scaled(float* r, const float* x, float scale, long n, hipStream_t s);
 
 namespace {
 
@@ -33,15 +35,15 @@ struct Conformer {
   int D = 0, H = 0, Dff = 0, K = 0;
   OratorConformerWeights w{};
   int cap_t = 0;
-  float *ln = nullptr, *ff = nullptr, *tmp = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
-        *p = nullptr, *ctx = nullptr, *pw1 = nullptr, *glu = nullptr, *dw = nullptr;
+  float *ln = nullptr, *ff = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *p = nullptr,
+        *ctx = nullptr, *pw1 = nullptr, *glu = nullptr, *dw = nullptr;
 
   ~Conformer() { release(); }
 
   void release() {
-    for (float* b : {ln, ff, tmp, q, k, v, p, ctx, pw1, glu, dw})
+    for (float* b : {ln, ff, q, k, v, p, ctx, pw1, glu, dw})
       if (b) (void)hipFree(b);
-    ln = ff = tmp = q = k = v = p = ctx = pw1 = glu = dw = nullptr;
+    ln = ff = q = k = v = p = ctx = pw1 = glu = dw = nullptr;
     cap_t = 0;
   }
 
@@ -50,9 +52,8 @@ struct Conformer {
     release();
     const size_t t = T, P = 2 * t - 1;
     const std::pair<float**, size_t> bufs[] = {
-        {&ln, t * D},  {&ff, t * Dff}, {&tmp, t * D},     {&q, t * D},     {&k, t * D},
-        {&v, t * D},   {&p, P * D},    {&ctx, t * D},     {&pw1, 2 * t * D}, {&glu, t * D},
-        {&dw, t * D}};
+        {&ln, t * D}, {&ff, t * Dff},     {&q, t * D},   {&k, t * D},  {&v, t * D},
+        {&p, P * D},  {&ctx, t * D},      {&pw1, 2 * t * D}, {&glu, t * D}, {&dw, t * D}};
     for (const auto& [ptr, n] : bufs)
       if (int rc = check_hip(hipMalloc(reinterpret_cast<void**>(ptr), n * sizeof(float)),
                              "conformer scratch"))
@@ -66,20 +67,25 @@ struct Conformer {
     return orator_sgemm(in, W, b, out, M, Kd, N, act, s);
   }
 
+  int qkv(int T, hipStream_t s) {
+    const float* const W[3] = {w.q_w, w.k_w, w.v_w};
+    const float* const b[3] = {w.q_b, w.k_b, w.v_b};
+    float* const out[3] = {q, k, v};
+    return launch_sgemm_group3(ln, W, b, out, T, D, D, s);
+  }
+
   int ffn(float* x, int T, const float* nw, const float* nb, const float* w1, const float* b1,
           const float* w2, const float* b2, hipStream_t s) {
     int rc = 0;
     (rc = launch_layer_norm(x, nw, nb, ln, T, D, kEps, s)) ||
         (rc = linear(ln, w1, b1, ff, T, D, Dff, 1, s)) ||  // SiLU
-        (rc = linear(ff, w2, b2, tmp, T, Dff, D, 0, s)) ||
-        (rc = launch_add_scaled(x, tmp, 0.5f, static_cast<long>(T) * D, s));
+        (rc = launch_sgemm_residual(ff, w2, b2, x, T, Dff, D, 0.5f, s));
     return rc;
   }
 
   int forward(float* x, int T, int valid, const float* pos_emb, int attn_mode, hipStream_t s) {
     if (int rc = grow(T)) return rc;
     const int P = 2 * T - 1, Dk = D / H;
-    const long TD = static_cast<long>(T) * D;
     const float scale = 1.0f / std::sqrt(static_cast<float>(Dk));
     int rc = 0;
     // FFN1
@@ -87,9 +93,7 @@ struct Conformer {
       return rc;
     // MHSA
     (rc = launch_layer_norm(x, w.norm_att_w, w.norm_att_b, ln, T, D, kEps, s)) ||
-        (rc = linear(ln, w.q_w, w.q_b, q, T, D, D, 0, s)) ||
-        (rc = linear(ln, w.k_w, w.k_b, k, T, D, D, 0, s)) ||
-        (rc = linear(ln, w.v_w, w.v_b, v, T, D, D, 0, s)) ||
+        (rc = qkv(T, s)) ||
         (rc = linear(pos_emb, w.pos_w, nullptr, p, P, D, D, 0, s));
     if (rc) return rc;
     rc = attn_mode == 1
@@ -97,8 +101,7 @@ struct Conformer {
                                             valid, scale, 0, s)
              : orator_relpos_attention(q, k, v, p, w.pos_bias_u, w.pos_bias_v, ctx, T, H, Dk,
                                        valid, scale, s);
-    (rc) || (rc = linear(ctx, w.out_w, w.out_b, tmp, T, D, D, 0, s)) ||
-        (rc = launch_add_scaled(x, tmp, 1.0f, TD, s));
+    (rc) || (rc = launch_sgemm_residual(ctx, w.out_w, w.out_b, x, T, D, D, 1.0f, s));
     if (rc) return rc;
     // Conv module
     (rc = launch_layer_norm(x, w.norm_conv_w, w.norm_conv_b, ln, T, D, kEps, s)) ||
@@ -106,14 +109,11 @@ struct Conformer {
         (rc = launch_glu_mask(pw1, glu, T, D, valid, s)) ||
         (rc = launch_dwconv_bn_silu(glu, w.dw_w, w.dw_b, w.bn_mean, w.bn_var, w.bn_w, w.bn_b, dw,
                                     T, D, K, kEps, s)) ||
-        (rc = linear(dw, w.pw2_w, w.pw2_b, tmp, T, D, D, 0, s)) ||
-        (rc = launch_add_scaled(x, tmp, 1.0f, TD, s));
+        (rc = launch_sgemm_residual(dw, w.pw2_w, w.pw2_b, x, T, D, D, 1.0f, s));
     if (rc) return rc;
     // FFN2, norm_out
     (rc = ffn(x, T, w.norm_ff2_w, w.norm_ff2_b, w.ff2_w1, w.ff2_b1, w.ff2_w2, w.ff2_b2, s)) ||
-        (rc = launch_layer_norm(x, w.norm_out_w, w.norm_out_b, ln, T, D, kEps, s)) ||
-        (rc = check_hip(hipMemcpyAsync(x, ln, TD * sizeof(float), hipMemcpyDeviceToDevice, s),
-                        "conformer out"));
+        (rc = launch_layer_norm(x, w.norm_out_w, w.norm_out_b, x, T, D, kEps, s));
     return rc;
   }
 };

@@ -1,6 +1,7 @@
 // The Conformer layer's non-attention passes (src/model/conformer_layer.cu:28-76,207-246):
 // LayerNorm, GLU (fused with the padding-row mask that follows it), the depthwise time
-// convolution fused with the BatchNorm (eval) + SiLU after it, and the scaled residual add.
+// convolution fused with the BatchNorm (eval) + SiLU after it.  (The scaled residual add is the
+// epilogue of the projection before it: launch_sgemm_residual.)
 // Each keeps the reference's per-element arithmetic; the fusions only drop the HBM round trips
 // between passes.  All tensors are [T, C] fp32, C the channel count (d_model).
 #include "common.hpp"
@@ -10,28 +11,60 @@ namespace orator_hip {
 namespace {
 
 // LayerNormKernel (conformer_layer.cu:28-66): mean, then the mean square deviation, both over
-// the row, inv = rsqrt(var + eps), y = (x - mean) inv g + b.  One wave per row.
-__global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict__ in,
+// the row, inv = rsqrt(var + eps), y = (x - mean) inv g + b.  One wave per row; lane l owns
+// elements l, l + 64, ... and sums them in that order, then the wave sum.  PER > 0 (C <= 64 PER)
+// holds the row in registers, so all of a lane's loads are in flight together; PER = 0 re-reads
+// the row from cache, for any C.  Both give the same bits.  `out` may be `in` (each lane reads
+// its own elements before writing them).
+template <int PER>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float* in,
                                                          const float* __restrict__ g,
-                                                         const float* __restrict__ b,
-                                                         float* __restrict__ out, int T, int C,
-                                                         float eps) {
+                                                         const float* __restrict__ b, float* out,
+                                                         int T, int C, float eps) {
 #pragma clang fp contract(off)
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= T) return;
   const float* x = in + static_cast<long>(row) * C;
   float* y = out + static_cast<long>(row) * C;
-  float s = 0.0f;
-  for (int c = lane; c < C; c += 64) s += x[c];
-  const float mean = wave_sum(s) / static_cast<float>(C);
-  float sq = 0.0f;
-  for (int c = lane; c < C; c += 64) {
-    const float t = x[c] - mean;
-    sq += t * t;
+  if constexpr (PER > 0) {
+    float v[PER], gv[PER], bv[PER];  // the row, gamma and beta: one round of loads
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = min(lane + 64 * i, C - 1);
+      v[i] = x[c];
+      gv[i] = g[c];
+      bv[i] = b[c];
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (lane + 64 * i < C) s += v[i];
+    const float mean = wave_sum(s) / static_cast<float>(C);
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const float t = v[i] - mean;
+      if (lane + 64 * i < C) sq += t * t;
+    }
+    const float inv = rsqrtf(wave_sum(sq) / static_cast<float>(C) + eps);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = lane + 64 * i;
+      if (c < C) y[c] = (v[i] - mean) * inv * gv[i] + bv[i];
+    }
+  } else {
+    float s = 0.0f;
+    for (int c = lane; c < C; c += 64) s += x[c];
+    const float mean = wave_sum(s) / static_cast<float>(C);
+    float sq = 0.0f;
+    for (int c = lane; c < C; c += 64) {
+      const float t = x[c] - mean;
+      sq += t * t;
+    }
+    const float inv = rsqrtf(wave_sum(sq) / static_cast<float>(C) + eps);
+    for (int c = lane; c < C; c += 64) y[c] = (x[c] - mean) * inv * g[c] + b[c];
   }
-  const float inv = rsqrtf(wave_sum(sq) / static_cast<float>(C) + eps);
-  for (int c = lane; c < C; c += 64) y[c] = (x[c] - mean) * inv * g[c] + b[c];
 }
 
 // GluKernel (:207-215) then MaskRowsKernel (:78-83): out[t,c] = a * sigmoid(b) for rows
@@ -77,13 +110,6 @@ __global__ __launch_bounds__(256) void dwconv_bn_silu_kernel(
 }
 
 // AddScaledKernel (:70-73): r += scale * x.
-__global__ __launch_bounds__(256) void add_scaled_kernel(float* __restrict__ r,
-                                                         const float* __restrict__ x,
-                                                         float scale, long n) {
-  const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) r[i] += scale * x[i];
-}
-
 unsigned blocks256(long n) { return static_cast<unsigned>((n + 255) / 256); }
 
 }  // namespace
@@ -91,8 +117,15 @@ unsigned blocks256(long n) { return static_cast<unsigned>((n + 255) / 256); }
 int launch_layer_norm(const float* in, const float* g, const float* b, float* out, int T, int C,
                       float eps, hipStream_t s) {
   if (T <= 0 || C <= 0) return ORATOR_OK;
-  hipLaunchKernelGGL(layer_norm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, in, g, b, out, T, C,
-                     eps);
+  const dim3 grid((T + 3) / 4), block(256);
+  if (C <= 256)
+    hipLaunchKernelGGL(layer_norm_kernel<4>, grid, block, 0, s, in, g, b, out, T, C, eps);
+  else if (C <= 512)
+    hipLaunchKernelGGL(layer_norm_kernel<8>, grid, block, 0, s, in, g, b, out, T, C, eps);
+  else if (C <= 1024)
+    hipLaunchKernelGGL(layer_norm_kernel<16>, grid, block, 0, s, in, g, b, out, T, C, eps);
+  else
+    hipLaunchKernelGGL(layer_norm_kernel<0>, grid, block, 0, s, in, g, b, out, T, C, eps);
   return check_launch("layer_norm_kernel");
 }
 
@@ -110,12 +143,6 @@ int launch_dwconv_bn_silu(const float* in, const float* w, const float* bias, co
   hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(blocks256(static_cast<long>(T) * C)), dim3(256),
                      0, s, in, w, bias, mean, var, gamma, beta, out, T, C, K, eps);
   return check_launch("dwconv_bn_silu_kernel");
-}
-
-int launch_add_scaled(float* r, const float* x, float scale, long n, hipStream_t s) {
-  if (n <= 0) return ORATOR_OK;
-  hipLaunchKernelGGL(add_scaled_kernel, dim3(blocks256(n)), dim3(256), 0, s, r, x, scale, n);
-  return check_launch("add_scaled_kernel");
 }
 
 }  // namespace orator_hip

@@ -146,4 +146,13 @@ int launch_sgemm(const float* in, const float* W, const float* bias, float* out,
                  int N, int act, int batch, long stride_in, long stride_w, long stride_out,
                  hipStream_t stream);
 
+// out[M][N] += res_scale * (in W^T + bias): a linear followed by the reference's AddScaledKernel
+// (src/model/conformer_layer.cu:70-76, used at :385, :448, :467, :475), folded into one launch.
+int launch_sgemm_residual(const float* in, const float* W, const float* bias, float* out, int M,
+                          int K, int N, float res_scale, hipStream_t stream);
+
+// out[g] = in W[g]^T + bias[g] for g = 0..2: three products of one shape sharing `in`, one launch.
+int launch_sgemm_group3(const float* in, const float* const W[3], const float* const bias[3],
+                        float* const out[3], int M, int K, int N, hipStream_t stream);
+
 }  // namespace orator_hip

@@ -51,10 +51,19 @@ struct SgemmArgs {
   int batch, splits;  // blockIdx.z = split * batch + batch entry
   long s_in, s_w, s_out;
   bool vec;  // K % 32 == 0 and 16-byte aligned operands: 16-byte loads
+  // Grouped products (group > 0): `group` problems share `in`; problem z uses weight Wg[z],
+  // bias bg[z] and output og[z] (batch = group, blockIdx.z selects the problem).
+  int group;
+  const float* Wg[3];
+  const float* bg[3];
+  float* og[3];
+  // Residual update (residual != 0): out = out + res_scale * (in W^T + bias), act 0.
+  int residual;
+  float res_scale;
 };
 
 // Epilogues: raw split-K partials, out = acc (no bias, act 0), and out = act(acc + bias)
-// through LDS.
+// or the residual update out += res_scale * (acc + bias) through LDS.
 constexpr int kSEpiPartial = 0, kSEpiStore = 1, kSEpiAct = 2;
 
 template <int BM, int BN, int WGM, int WGN, int MINW, bool VEC, int EPI>
@@ -78,7 +87,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
   const int batch = blockIdx.z % a.batch;
   const int split = blockIdx.z / a.batch;
   const float* A = a.in + batch * a.s_in;
-  const float* B = a.W + batch * a.s_w;
+  const float* B = a.group ? a.Wg[batch] : a.W + batch * a.s_w;
   const int M = a.M, N = a.N, K = a.K;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -186,7 +195,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
   if constexpr (EPI != kSEpiAct) {
     float* C = EPI == kSEpiPartial
                    ? a.part + (static_cast<long>(split) * a.batch + batch) * M * N
-                   : a.out + batch * a.s_out;
+                   : (a.group ? a.og[batch] : a.out + batch * a.s_out);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = n0 + wn * TN + 32 * j + fr;
@@ -210,15 +219,26 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
         sC[wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)][wn * TN + 32 * j + fr] =
             acc[i][j][e];
   __syncthreads();
-  float* C = a.out + batch * a.s_out;
+  float* C = a.group ? a.og[batch] : a.out + batch * a.s_out;
+  const float* bias = a.group ? a.bg[batch] : a.bias;
   constexpr int TPRo = BN / 4, RPIo = NT / TPRo, PASSES = BM / RPIo;
   const int orow = tid / TPRo, ocol = 4 * (tid % TPRo);
   const int n = n0 + ocol;
   const bool vec_out = (N % 4) == 0 && ((reinterpret_cast<uintptr_t>(C)) & 15) == 0;
   float bv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (a.bias) {
+  if (bias) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) bv[q] = a.bias[min(n + q, N - 1)];
+    for (int q = 0; q < 4; ++q) bv[q] = bias[min(n + q, N - 1)];
+  }
+  // the residual's old values, all loaded before the first store
+  float old[PASSES][4];
+  if (a.residual) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const float* src = C + static_cast<long>(min(m0 + RPIo * p + orow, M - 1)) * N;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) old[p][q] = src[min(n + q, N - 1)];
+    }
   }
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
@@ -227,7 +247,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
     const float4 c = *reinterpret_cast<const float4*>(&sC[r][ocol]);
     float v[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = apply_act(v[q] + bv[q], a.act);
+    for (int q = 0; q < 4; ++q) {
+      v[q] = apply_act(v[q] + bv[q], a.act);
+      if (a.residual) v[q] = fmaf(a.res_scale, v[q], old[p][q]);
+    }
     if (m >= M) continue;
     float* dst = C + static_cast<long>(m) * N + n;
     if (vec_out && n + 3 < N) {
@@ -245,7 +268,8 @@ __global__ __launch_bounds__(256) void sgemm_splitk_reduce_kernel(const float* _
                                                                   int splits, int batch,
                                                                   const float* __restrict__ bias,
                                                                   float* __restrict__ out, int M,
-                                                                  int N, int act, long s_out) {
+                                                                  int N, int act, long s_out,
+                                                                  int residual, float res_scale) {
   const long MN = static_cast<long>(M) * N;
   const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= MN * batch) return;
@@ -253,7 +277,9 @@ __global__ __launch_bounds__(256) void sgemm_splitk_reduce_kernel(const float* _
   const long per_split = MN * batch;
   float v = part[i];
   for (int z = 1; z < splits; ++z) v += part[z * per_split + i];
-  out[b * s_out + r] = apply_act(v + (bias ? bias[r % N] : 0.0f), act);
+  v = apply_act(v + (bias ? bias[r % N] : 0.0f), act);
+  if (residual) v = fmaf(res_scale, v, out[b * s_out + r]);
+  out[b * s_out + r] = v;
 }
 
 template <int BM, int BN, int WGM, int WGN, int MINW, bool VEC>
@@ -277,7 +303,7 @@ int launch_sg(SgemmArgs a, int batch, int splits, hipStream_t s) {
   if (splits > 1)
     hipLaunchKernelGGL((sgemm_nt_kernel<BM, BN, WGM, WGN, MINW, VEC, kSEpiPartial>), grid, block,
                        0, s, a);
-  else if (a.bias || a.act)
+  else if (a.bias || a.act || a.residual || a.group)
     hipLaunchKernelGGL((sgemm_nt_kernel<BM, BN, WGM, WGN, MINW, VEC, kSEpiAct>), grid, block, 0,
                        s, a);
   else
@@ -288,8 +314,25 @@ int launch_sg(SgemmArgs a, int batch, int splits, hipStream_t s) {
   const long total = MN * batch;
   hipLaunchKernelGGL(sgemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
                      dim3(256), 0, s, a.part, splits, batch, a.bias, a.out, a.M, a.N, a.act,
-                     batch > 1 ? a.s_out : MN);
+                     batch > 1 ? a.s_out : MN, a.residual, a.res_scale);
   return check_launch("sgemm_splitk_reduce");
+}
+
+// 64 x 64 tiles, 4 waves of one 32 x 32 block each, four workgroups per CU.  K is split over
+// workgroups only when the grid leaves more than half the CUs idle (up to two workgroups per
+// CU, K / 256 splits at most).  Measured at the Conformer's shapes: 717 x 2048 -> 512 takes
+// 27.7 us with 6 splits against 45.9 unsplit; 1433 x 512 -> 512 (184 tiles) 13.6 unsplit
+// against 19.1 with 2 splits.  Grouped products are never split.
+int run_sgemm(SgemmArgs a, int batch, hipStream_t stream) {
+  const int M = a.M, N = a.N, K = a.K;
+  const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const long t = static_cast<long>((M + 63) / 64) * ((N + 63) / 64) * batch;
+  int splits = 1;
+  if (2 * t <= cus && K >= 512 && !a.group)
+    splits = static_cast<int>(std::min<long>((2 * cus + t - 1) / t, K / 256));
+  if (static_cast<long>(batch) * splits > 65535) splits = 1;
+  if (a.vec) return launch_sg<64, 64, 2, 2, 4, true>(a, batch, splits, stream);
+  return launch_sg<64, 64, 2, 2, 4, false>(a, batch, splits, stream);
 }
 
 }  // namespace
@@ -315,19 +358,49 @@ int launch_sgemm(const float* in, const float* W, const float* bias, float* out,
   a.s_out = batch > 1 ? stride_out : 0;
   a.vec = (K % kSK) == 0 && ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W) |
                             (batch > 1 ? (stride_in | stride_w) * 4 : 0)) & 15) == 0;
-  // 64 x 64 tiles, 4 waves of one 32 x 32 block each, four workgroups per CU.  K is split over
-  // workgroups only when the grid leaves more than half the CUs idle (up to two workgroups per
-  // CU, K / 256 splits at most).  Measured at the Conformer's shapes: 717 x 2048 -> 512 takes
-  // 27.7 us with 6 splits against 45.9 unsplit; 1433 x 512 -> 512 (184 tiles) 13.6 unsplit
-  // against 19.1 with 2 splits.
-  const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  const long t = static_cast<long>((M + 63) / 64) * ((N + 63) / 64) * batch;
-  int splits = 1;
-  if (2 * t <= cus && K >= 512)
-    splits = static_cast<int>(std::min<long>((2 * cus + t - 1) / t, K / 256));
-  if (static_cast<long>(batch) * splits > 65535) splits = 1;
-  if (a.vec) return launch_sg<64, 64, 2, 2, 4, true>(a, batch, splits, stream);
-  return launch_sg<64, 64, 2, 2, 4, false>(a, batch, splits, stream);
+  return run_sgemm(a, batch, stream);
+}
+
+int launch_sgemm_residual(const float* in, const float* W, const float* bias, float* out, int M,
+                          int K, int N, float res_scale, hipStream_t stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return ORATOR_OK;
+  if (!in || !W || !out) return fail(ORATOR_ERR_INVALID, "sgemm: null pointer");
+  SgemmArgs a{};
+  a.in = in;
+  a.W = W;
+  a.bias = bias;
+  a.out = out;
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.residual = 1;
+  a.res_scale = res_scale;
+  a.vec = (K % kSK) == 0 &&
+          ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15) == 0;
+  return run_sgemm(a, 1, stream);
+}
+
+int launch_sgemm_group3(const float* in, const float* const W[3], const float* const bias[3],
+                        float* const out[3], int M, int K, int N, hipStream_t stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return ORATOR_OK;
+  if (!in) return fail(ORATOR_ERR_INVALID, "sgemm: null pointer");
+  SgemmArgs a{};
+  a.in = in;
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.group = 3;
+  uintptr_t align = reinterpret_cast<uintptr_t>(in);
+  for (int g = 0; g < 3; ++g) {
+    if (!W[g] || !out[g]) return fail(ORATOR_ERR_INVALID, "sgemm: null pointer");
+    a.Wg[g] = W[g];
+    a.bg[g] = bias[g];
+    a.og[g] = out[g];
+    align |= reinterpret_cast<uintptr_t>(W[g]);
+  }
+  a.W = a.Wg[0];
+  a.vec = (K % kSK) == 0 && (align & 15) == 0;
+  return run_sgemm(a, 3, stream);
 }
 
 }  // namespace orator_hip

@@ -45,3 +45,30 @@ def test_conformer_layer_vs_oracle(T, valid, mode):
     err = rel_err(got, ref, 0.05)
     print(f"T={T} valid={valid} mode={mode}: {err:.2e} (floor 1e-3: {rel_err(got, ref, 1e-3):.2e})")
     assert err <= tol
+
+
+@pytest.mark.parametrize("T,valid,D,H,mode", [(200, 150, 256, 4, 0), (200, 150, 256, 4, 1),
+                                              (61, 61, 1152, 9, 0)])
+def test_conformer_layer_other_widths(T, valid, D, H, mode):
+    """d_model 256 and 1152 take the LayerNorm's other row forms (4 elements per lane in
+    registers; the re-reading loop above 1024) and other projection shapes; same bars as above."""
+    Dff, K = 4 * D, 9
+    r = SplitMix64(1000 + D + mode)
+    W = conformer_weights(r, D, H, Dff, K)
+    x = r.normal((T, D))
+    pe = orc.build_pos_emb(T, D)
+    ref = orc.conformer_layer(x, T, valid, pe, W, H)
+    tol = 2e-4
+    if mode == 1:
+        predicted = rel_err(fp16_model.conformer_layer_f16_core(x, T, valid, pe, W, H), ref, 0.05)
+        tol = 1.5 * predicted + 2e-4
+    layer = ConformerLayer({k: up(v) for k, v in W.items()}, D, H, Dff, K)
+    dx = up(x)
+    say("conformer layer", T, valid, D, mode)
+    layer.Forward(dx, T, valid, up(pe), attn_mode=mode)
+    got = down(dx, (T, D))
+    layer.close()
+    err = rel_err(got, ref, 0.05)
+    print(f"T={T} D={D} mode={mode}: {err:.2e} (floor 1e-3: {rel_err(got, ref, 1e-3):.2e}), "
+          f"bar {tol:.2e}")
+    assert err <= tol
