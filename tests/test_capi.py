@@ -137,3 +137,24 @@ def test_noalloc_decode_rejects_sizes_past_static_scratch():
     assert b"16 MiB" in lib.orator_last_error()
     assert lib.orator_gqa_decode_paged_noalloc(FAKE, FAKE, FAKE, None, 8, 16, FAKE, FAKE, 1, 16, 8,
                                                128, 0.1, None) == _lib.ORATOR_ERR_INVALID
+
+
+def test_prefill_validation():
+    """orator_gqa_prefill_ex rejects, before touching the device: a paged cache past the
+    16384 keys its LDS page-row table holds, a page size that is not a power of two >= 16, a
+    capacity beyond max_pages * page_size, group sizes and head sizes that are not built."""
+    lib = _lib.lib()
+    PF32 = 0
+
+    def call(page_table, max_pages, page_size, Hq, Hkv, Dh, cap):
+        return lib.orator_gqa_prefill_ex(FAKE, None, FAKE, FAKE, page_table, max_pages, page_size,
+                                         FAKE, 4, Hq, Hkv, Dh, FAKE, cap, 0.1, PF32, None)
+
+    assert call(FAKE, 1025, 16, 16, 8, 128, 16400) == _lib.ORATOR_ERR_UNSUPPORTED
+    assert b"16384" in lib.orator_last_error()
+    assert call(FAKE, 64, 24, 16, 8, 128, 1024) == _lib.ORATOR_ERR_INVALID
+    assert call(FAKE, 64, 8, 16, 8, 128, 512) == _lib.ORATOR_ERR_INVALID
+    assert call(FAKE, 16, 32, 16, 8, 128, 1024) == _lib.ORATOR_ERR_CAPACITY
+    assert call(None, 0, 0, 64, 8, 128, 1024) == _lib.ORATOR_ERR_UNSUPPORTED  # group size 8
+    assert call(None, 0, 0, 16, 8, 64, 1024) == _lib.ORATOR_ERR_UNSUPPORTED   # Dh 64
+    assert call(None, 0, 0, 12, 8, 128, 1024) == _lib.ORATOR_ERR_INVALID      # Hq % Hkv

@@ -154,3 +154,34 @@ def test_append_paged_unmapped_page_is_not_written(bad):
                truth=t64.decode_paged(q, kp_ref, vp_ref, ref_table, ps, pos, scale))
     np.testing.assert_array_equal(down(dk, kp.shape, np.uint16), kp)
     np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp)
+
+
+@pytest.mark.parametrize("ps", [32, 128])
+def test_append_paged_page_sizes(ps):
+    """Pages of 32 and 128 keys: the appended row lands in the right page and offset, and the
+    output matches the oracle's write-then-decode."""
+    Hq, Hkv, Dh = 16, 8, 128
+    lens = [1, ps, ps + 1, 2000, 4097]
+    r = SplitMix64(ps + 11)
+    B = len(lens)
+    max_pages = max((n + ps - 1) // ps for n in lens)
+    n_pages = B * max_pages + 2
+    kp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    vp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    table = np.array(r.uniform(n_pages).argsort(), np.int32)[:B * max_pages].reshape(B, max_pages)
+    q, kn, vn = r.normal((B, Hq, Dh)), r.normal((B, Hkv, Dh)), r.normal((B, Hkv, Dh))
+    pos = np.array(lens, np.int32) - 1
+    scale = 1.0 / math.sqrt(Dh)
+    kp_ref, vp_ref = kp.copy(), vp.copy()
+    for b in range(B):
+        orc.kv_write_paged(kn[b][None], vn[b][None], kp_ref, vp_ref, table[b], ps, int(pos[b]))
+    ref = orc.gqa_decode_paged(q, kp_ref, vp_ref, table, ps, pos, scale, threads=8)
+    dk, dv = up(kp), up(vp)
+    dout = empty((B, Hq, Dh), np.float32)
+    say("append paged page size", ps)
+    da.GqaDecodeAttnAppendPaged(up(q), up(kn), up(vn), dk, dv, up(table), max_pages, ps, n_pages,
+                                up(pos), dout, B, Hq, Hkv, Dh, scale)
+    check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+               truth=t64.decode_paged(q, kp_ref, vp_ref, table, ps, pos, scale))
+    np.testing.assert_array_equal(down(dk, kp.shape, np.uint16), kp_ref)
+    np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp_ref)

@@ -164,3 +164,34 @@ def test_kv_write_paged_bit_exact():
                          up(pos0))
     np.testing.assert_array_equal(down(dkp, kp.shape, np.uint16), kp)
     np.testing.assert_array_equal(down(dvp, vp.shape, np.uint16), vp)
+
+
+@pytest.mark.parametrize("ps", [32, 64, 256])
+def test_decode_paged_page_sizes(ps):
+    """Pages of 32, 64 and 256 keys (every power of two >= 16 is accepted): ragged streams
+    through random page tables, against the oracle."""
+    Hq, Hkv, Dh = 16, 8, 128
+    lens = [17, 1000, 2049, 4097]
+    q, kp, vp, table, pos = _paged_case(ps + 5, lens, ps=ps)
+    B, max_pages = table.shape
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_decode_paged(q, kp, vp, table, ps, pos, scale, threads=8)
+    dout = empty((B, Hq, Dh), np.float32)
+    say("decode paged page size", ps)
+    da.GqaDecodeAttnPaged(up(q), up(kp), up(vp), up(table), max_pages, ps, up(pos), dout, B, Hq,
+                          Hkv, Dh, scale)
+    check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+               truth=t64.decode_paged(q, kp, vp, table, ps, pos, scale))
+
+
+def test_decode_contiguous_16k_context():
+    """A 16384-key context (128 splits, 8 merge batches): against the oracle."""
+    Hq, Hkv, Dh, S = 16, 8, 128, 16384
+    q, kc, vc = _contig_case(16384, S, S)
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_decode(q, kc, vc, S - 1, scale)
+    dout = empty((Hq, Dh), np.float32)
+    say("decode 16k")
+    da.GqaDecodeAttn(up(q), up(kc), up(vc), dout, Hq, Hkv, Dh, up(np.array([S - 1], np.int32)), S,
+                     scale)
+    check_fp32(down(dout, (Hq, Dh)), ref, TOL, truth=t64.decode(q, kc, vc, S - 1, scale))

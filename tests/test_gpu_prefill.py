@@ -137,6 +137,54 @@ def test_prefill_paged_matches_contiguous(mode):
     np.testing.assert_array_equal(a, b)
 
 
+def _paged_copy(kc, vc, ps, seed):
+    cap, Hkv, Dh = kc.shape
+    n_pages = cap // ps
+    perm = np.array(SplitMix64(seed).uniform(n_pages).argsort(), np.int32)
+    kp = np.empty((n_pages, ps, Hkv, Dh), np.uint16)
+    vp = np.empty_like(kp)
+    kp[perm] = kc.reshape(n_pages, ps, Hkv, Dh)
+    vp[perm] = vc.reshape(n_pages, ps, Hkv, Dh)
+    return kp, vp, perm
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("ps", [32, 128])
+def test_prefill_paged_page_sizes(ps, mode):
+    """Pages of 32 and 128 keys through a permuted table: the same bits as the contiguous
+    cache, and the oracle's result."""
+    T, pos0, Hkv, Dh, cap = 300, 100, 8, 128, 512
+    q, kc, vc = _layer_inputs(17 + ps, T, pos0, cap=cap)
+    kp, vp, perm = _paged_copy(kc, vc, ps, ps)
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_prefill(q, kc, vc, pos0, scale, threads=8)
+    say("prefill paged page size", ps, mode)
+    a = _run(q, kc, vc, pos0, cap, mode, Hkv)
+    b = _run(q, kc, vc, pos0, cap, mode, Hkv, page=(kp, vp, perm, ps))
+    np.testing.assert_array_equal(a, b)
+    _check(b, ref, mode, t64.prefill(q, kc, vc, pos0, scale))
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_prefill_paged_at_the_16k_key_limit(mode):
+    """The last 64 prompt rows of a full 16384-key paged cache (the largest a paged cache may
+    hold: the kernel's LDS page-row table): queries at 16320..16383 against the oracle, and
+    the same bits as the contiguous cache."""
+    T, pos0, Hkv, Dh, ps = 64, 16320, 8, 128, 16
+    cap = pos0 + T
+    q, kc, vc = _layer_inputs(16384, T, pos0, cap=cap)
+    kp, vp, perm = _paged_copy(kc, vc, ps, 5)
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_prefill(q, kc, vc, pos0, scale, threads=8)
+    say("prefill paged 16k", mode)
+    a = _run(q, kc, vc, pos0, cap, mode, Hkv)
+    b = _run(q, kc, vc, pos0, cap, mode, Hkv, page=(kp, vp, perm, ps))
+    np.testing.assert_array_equal(a, b)
+    # outputs over 16K keys are ~0.01: at the 1e-3 floor the fp32 sums' rounding shows, so the
+    # device is held to the oracle's own distance from the fp64 value there
+    _check(b, ref, mode, t64.prefill(q, kc, vc, pos0, scale))
+
+
 def test_prefill_bf16_q_input():
     T, Hkv, Dh = 96, 8, 128
     q, kc, vc = _layer_inputs(13, T, 0)
