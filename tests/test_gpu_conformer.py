@@ -54,7 +54,7 @@ def _relpos_inputs(r, T, H, Dk):
 
 
 @pytest.mark.parametrize("T,valid", [(1, 1), (2, 2), (3, 2), (126, 125), (717, 717), (400, 333),
-                                     (5, 0), (70, 0)])
+                                     (5, 0), (70, 0), (1500, 1400)])
 def test_relpos_fp32_vs_oracle(T, valid):
     """Config-4 shape (T = 717: 340 chunk + 1 right context + 188 FIFO + 188 speaker cache),
     the NeMo verification shape (T = 126, valid = 125, tools/verify/cc/verify_conformer.cc),
@@ -85,7 +85,7 @@ def _to_f16_bits(x):
 
 @pytest.mark.parametrize("T,valid,in_f16", [(717, 717, True), (717, 700, False), (126, 125, True),
                                              (1, 1, True), (33, 20, True), (300, 300, False),
-                                             (40, 0, True), (70, 0, False)])
+                                             (40, 0, True), (70, 0, False), (1500, 1500, True)])
 def test_relpos_fused_vs_oracle(T, valid, in_f16):
     """Fused fp16-MFMA rel-pos attention (fp16 inputs N(0,1)).  fp16
     operands with fp32 accumulation: max abs error <= 2e-2 on unit-scale outputs (the
