@@ -552,7 +552,11 @@ template <int DH>
 __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, int split_len,
                                                                 int Hq) {
   constexpr int kBatch = 17;
-  const int h = blockIdx.x;
+  // x = kv head + Hkv * (q head within the group): with 8 kv heads the workgroup of every q
+  // head runs on the XCD (workgroup index % 8) whose L2 the split kernel wrote its partials
+  // through (its kv head is its fastest grid index too)
+  const int G = Hq / a.Hkv;
+  const int h = (blockIdx.x % a.Hkv) * G + blockIdx.x / a.Hkv;
   const int b = blockIdx.y;
   const long bh = static_cast<long>(b) * Hq + h;
   const long base = bh * a.max_splits;
