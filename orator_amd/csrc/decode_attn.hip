@@ -552,9 +552,10 @@ template <int DH>
 __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, int split_len,
                                                                 int Hq) {
   constexpr int kBatch = 17;
-  // x = kv head + Hkv * (q head within the group): with 8 kv heads the workgroup of every q
-  // head runs on the XCD (workgroup index % 8) whose L2 the split kernel wrote its partials
-  // through (its kv head is its fastest grid index too)
+  // x = kv head + Hkv * (q head within the group): the kv head is the fastest grid index, as
+  // in the split kernel, so with 8 kv heads a head's merge runs on the XCD (workgroup index %
+  // 8) that ran its splits.  Measured 0.9 us per op faster than q-head order (B = 16, L = 4096,
+  // same box), though the partials are still fetched from memory either way.
   const int G = Hq / a.Hkv;
   const int h = (blockIdx.x % a.Hkv) * G + blockIdx.x / a.Hkv;
   const int b = blockIdx.y;
