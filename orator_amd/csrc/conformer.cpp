@@ -2,7 +2,7 @@
 // src/model/conformer_layer.cu:364-488), composed from this library's operators:
 //   x += 0.5 FFN1(LN(x))                                   FFN: Linear+SiLU, Linear
 //   x += MHSA(LN(x))        linear_q/k/v, linear_pos(pos_emb), rel-pos attention, linear_out
-//   x += Conv(LN(x))        pointwise 2C, GLU (+ padding-row mask), depthwise K,
+//   x += Conv(LN(x))        pointwise 2C + GLU (+ padding-row mask) in one launch, depthwise K,
 //                           BatchNorm(eval)+SiLU, pointwise C
 //   x += 0.5 FFN2(LN(x));  x = LN_out(x)
 // The projections run on the fp32 MFMA SGEMM; the attention core is either the reference
@@ -67,6 +67,15 @@ struct Conformer {
     return orator_sgemm(in, W, b, out, M, Kd, N, act, s);
   }
 
+  // pointwise_conv1 + GLU + padding-row mask: one launch when the product takes 16-byte
+  // loads, else the product then the GLU pass (the same values either way)
+  int pw1_glu(int T, int valid, hipStream_t s) {
+    const int rc = launch_sgemm_glu(ln, w.pw1_w, w.pw1_b, glu, T, D, D, valid, s);
+    if (rc != ORATOR_ERR_UNSUPPORTED) return rc;
+    if (int r = linear(ln, w.pw1_w, w.pw1_b, pw1, T, D, 2 * D, 0, s)) return r;
+    return launch_glu_mask(pw1, glu, T, D, valid, s);
+  }
+
   int qkv(int T, hipStream_t s) {
     const float* const W[3] = {w.q_w, w.k_w, w.v_w};
     const float* const b[3] = {w.q_b, w.k_b, w.v_b};
@@ -105,8 +114,7 @@ struct Conformer {
     if (rc) return rc;
     // Conv module
     (rc = launch_layer_norm(x, w.norm_conv_w, w.norm_conv_b, ln, T, D, kEps, s)) ||
-        (rc = linear(ln, w.pw1_w, w.pw1_b, pw1, T, D, 2 * D, 0, s)) ||
-        (rc = launch_glu_mask(pw1, glu, T, D, valid, s)) ||
+        (rc = pw1_glu(T, valid, s)) ||
         (rc = launch_dwconv_bn_silu(glu, w.dw_w, w.dw_b, w.bn_mean, w.bn_var, w.bn_w, w.bn_b, dw,
                                     T, D, K, kEps, s)) ||
         (rc = launch_sgemm_residual(dw, w.pw2_w, w.pw2_b, x, T, D, D, 1.0f, s));

@@ -151,6 +151,13 @@ int launch_sgemm(const float* in, const float* W, const float* bias, float* out,
 int launch_sgemm_residual(const float* in, const float* W, const float* bias, float* out, int M,
                           int K, int N, float res_scale, hipStream_t stream);
 
+// The Conformer conv module's pointwise_conv1 + GLU + padding-row mask in one launch
+// (src/model/conformer_layer.cu:455-458): W [2C][K] (value rows, then gate rows), out [M][C] =
+// a * (1 / (1 + __expf(-b))) of the biased value / gate outputs, 0 for rows >= valid.
+// ORATOR_ERR_UNSUPPORTED (nothing launched) unless K % 32 == 0 and in, W are 16-byte aligned.
+int launch_sgemm_glu(const float* in, const float* W, const float* bias, float* out, int M, int K,
+                     int C, int valid, hipStream_t stream);
+
 // out[g] = in W[g]^T + bias[g] for g = 0..2: three products of one shape sharing `in`, one launch.
 int launch_sgemm_group3(const float* in, const float* const W[3], const float* const bias[3],
                         float* const out[3], int M, int K, int N, hipStream_t stream);

@@ -60,11 +60,16 @@ struct SgemmArgs {
   // Residual update (residual != 0): out = out + res_scale * (in W^T + bias), act 0.
   int residual;
   float res_scale;
+  // GLU (the kSEpiGlu epilogue): W has 2 glu_c rows (value rows, then gate rows); out[m][c] =
+  // a * (1 / (1 + exp(-b))) with a, b the value and gate outputs (bias added), 0 for rows
+  // m >= glu_valid; out is [M][glu_c].
+  int glu_c, glu_valid;
 };
 
-// Epilogues: raw split-K partials, out = acc (no bias, act 0), and out = act(acc + bias)
-// or the residual update out += res_scale * (acc + bias) through LDS.
-constexpr int kSEpiPartial = 0, kSEpiStore = 1, kSEpiAct = 2;
+// Epilogues: raw split-K partials, out = acc (no bias, act 0), and through LDS out =
+// act(acc + bias) or the residual update out += res_scale * (acc + bias), or the GLU of a
+// tile's value and gate halves.
+constexpr int kSEpiPartial = 0, kSEpiStore = 1, kSEpiAct = 2, kSEpiGlu = 3;
 
 template <int BM, int BN, int WGM, int WGN, int MINW, bool VEC, int EPI>
 __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArgs a) {
@@ -105,7 +110,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
 #pragma unroll
   for (int i = 0; i < LA; ++i) arow[i] = A + static_cast<long>(min(m0 + RPI * i + lr, M - 1)) * K;
 #pragma unroll
-  for (int i = 0; i < LW; ++i) wrow[i] = B + static_cast<long>(min(n0 + RPI * i + lr, N - 1)) * K;
+  for (int i = 0; i < LW; ++i) {
+    if constexpr (EPI == kSEpiGlu) {  // tile rows: BN/2 value rows, then the matching gate rows
+      const int t = RPI * i + lr, c = blockIdx.x * (BN / 2) + (t % (BN / 2));
+      wrow[i] = B + static_cast<long>((t < BN / 2 ? 0 : a.glu_c) + min(c, a.glu_c - 1)) * K;
+    } else {
+      wrow[i] = B + static_cast<long>(min(n0 + RPI * i + lr, N - 1)) * K;
+    }
+  }
   float4 ra[LA], rw[LW];
   auto load_guarded = [&](const float* base, int row, int rows, int k) -> float4 {
     if (row >= rows) return make_float4(0.f, 0.f, 0.f, 0.f);
@@ -192,7 +204,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
   // of the block.  Plain stores and partials go straight out (nothing is loaded, so no store
   // waits); bias / activation go through LDS with the bias loaded before the first store
   // (stores count against the same wait counter as loads).
-  if constexpr (EPI != kSEpiAct) {
+  if constexpr (EPI == kSEpiPartial || EPI == kSEpiStore) {
     float* C = EPI == kSEpiPartial
                    ? a.part + (static_cast<long>(split) * a.batch + batch) * M * N
                    : (a.group ? a.og[batch] : a.out + batch * a.s_out);
@@ -219,6 +231,47 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
         sC[wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)][wn * TN + 32 * j + fr] =
             acc[i][j][e];
   __syncthreads();
+  if constexpr (EPI == kSEpiGlu) {
+    // columns [0, BN/2) of the tile are the value outputs of channels c0 .., [BN/2, BN) the
+    // gate outputs of the same channels; the same fp32 values and formula as a plain product
+    // followed by the GLU pass (its bias added, then a * (1 / (1 + exp(-b))))
+    constexpr int HB = BN / 2, TPRg = HB / 4, RPIg = NT / TPRg, PASSES_G = BM / RPIg;
+    const int Cg = a.glu_c, c0 = blockIdx.x * HB;
+    const int orow = tid / TPRg, j = 4 * (tid % TPRg);
+    float ba[4] = {0.f, 0.f, 0.f, 0.f}, bg[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.bias) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        ba[q] = a.bias[min(c0 + j + q, Cg - 1)];
+        bg[q] = a.bias[Cg + min(c0 + j + q, Cg - 1)];
+      }
+    }
+    const bool vec_out = (Cg % 4) == 0 && ((reinterpret_cast<uintptr_t>(a.out)) & 15) == 0;
+#pragma unroll
+    for (int p = 0; p < PASSES_G; ++p) {
+      const int r = RPIg * p + orow;
+      const int m = m0 + r;
+      const float4 va = *reinterpret_cast<const float4*>(&sC[r][j]);
+      const float4 vg = *reinterpret_cast<const float4*>(&sC[r][HB + j]);
+      const float av[4] = {va.x, va.y, va.z, va.w}, gv[4] = {vg.x, vg.y, vg.z, vg.w};
+      float o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float x = av[q] + ba[q], g = gv[q] + bg[q];
+        o[q] = m < a.glu_valid ? x * (1.0f / (1.0f + __expf(-g))) : 0.0f;
+      }
+      if (m >= M) continue;
+      float* dst = a.out + static_cast<long>(m) * Cg + c0 + j;
+      if (vec_out && c0 + j + 3 < Cg) {
+        *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (c0 + j + q < Cg) dst[q] = o[q];
+      }
+    }
+    return;
+  }
   float* C = a.group ? a.og[batch] : a.out + batch * a.s_out;
   const float* bias = a.group ? a.bg[batch] : a.bias;
   constexpr int TPRo = BN / 4, RPIo = NT / TPRo, PASSES = BM / RPIo;
@@ -378,6 +431,33 @@ int launch_sgemm_residual(const float* in, const float* W, const float* bias, fl
   a.vec = (K % kSK) == 0 &&
           ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15) == 0;
   return run_sgemm(a, 1, stream);
+}
+
+int launch_sgemm_glu(const float* in, const float* W, const float* bias, float* out, int M, int K,
+                     int C, int valid, hipStream_t stream) {
+  if (M <= 0 || C <= 0 || K <= 0) return ORATOR_OK;
+  if (!in || !W || !out) return fail(ORATOR_ERR_INVALID, "sgemm_glu: null pointer");
+  if ((K % kSK) != 0 ||
+      ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15) != 0)
+    return ORATOR_ERR_UNSUPPORTED;  // no 16-byte loads: the caller takes the two-pass path
+  SgemmArgs a{};
+  a.in = in;
+  a.W = W;
+  a.bias = bias;
+  a.out = out;
+  a.M = M;
+  a.K = K;
+  a.N = 2 * C;
+  a.k_split = K;
+  a.batch = 1;
+  a.splits = 1;
+  a.vec = true;
+  a.glu_c = C;
+  a.glu_valid = valid;
+  const dim3 grid((C + 31) / 32, (M + 63) / 64, 1);
+  hipLaunchKernelGGL((sgemm_nt_kernel<64, 64, 2, 2, 4, true, kSEpiGlu>), grid, dim3(256), 0, stream,
+                     a);
+  return check_launch("sgemm_nt_kernel (glu)");
 }
 
 int launch_sgemm_group3(const float* in, const float* const W[3], const float* const bias[3],
