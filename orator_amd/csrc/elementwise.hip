@@ -22,8 +22,10 @@ inline int blocks_for(long n, int per_block = kBlock) {
 
 // ------------------------------------------------------------------ RmsNorm ----
 // OUT = float: the reference's RmsNorm; OUT = uint16_t: RmsNorm then F32ToBf16 (RNE) of the
-// same fp32 values, in one pass.
-template <bool VEC, typename OUT = float>
+// same fp32 values, in one pass.  One wave per row; with VEC lane l takes float4 l, l + 64, ...
+// and sums their squares in that order.  PER > 0 (VEC, dim <= 256 PER): the row and the
+// weights are loaded once, all together, into registers; same arithmetic, same bits.
+template <bool VEC, typename OUT = float, int PER = 0>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ w,
                                                        OUT* out, int rows, int dim,
@@ -35,6 +37,39 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
   const float* xr = x + static_cast<long>(row) * dim;
   OUT* yr = out + static_cast<long>(row) * dim;
   float local = 0.0f;
+  if constexpr (PER > 0) {
+    float4 v[PER], g[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int d = min(lane * 4 + 256 * i, dim - 4);
+      v[i] = *reinterpret_cast<const float4*>(xr + d);
+      g[i] = *reinterpret_cast<const float4*>(w + d);
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (lane * 4 + 256 * i < dim) {
+        local += v[i].x * v[i].x;
+        local += v[i].y * v[i].y;
+        local += v[i].z * v[i].z;
+        local += v[i].w * v[i].w;
+      }
+    }
+    const float sum = wave_sum(local);
+    const float ms = sum / static_cast<float>(dim) + eps;
+    const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int d = lane * 4 + 256 * i;
+      if (d >= dim) continue;
+      const float4 y = make_float4(v[i].x * inv * g[i].x, v[i].y * inv * g[i].y,
+                                   v[i].z * inv * g[i].z, v[i].w * inv * g[i].w);
+      if constexpr (sizeof(OUT) == 4)
+        *reinterpret_cast<float4*>(yr + d) = y;
+      else
+        *reinterpret_cast<uint2*>(yr + d) = make_uint2(pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w));
+    }
+    return;
+  }
   if (VEC) {
     for (int d = lane * 4; d < dim; d += 256) {
       const float4 v = *reinterpret_cast<const float4*>(xr + d);
@@ -456,7 +491,18 @@ int launch_rms_norm_bf16(const float* x, const float* w, uint16_t* out, int rows
                          float eps, hipStream_t s) {
   if (rows <= 0 || dim <= 0) return ORATOR_OK;
   const dim3 grid(blocks_for(rows, 4));
-  if (dim % 4 == 0 && aligned16(x) && aligned16(w) && (reinterpret_cast<uintptr_t>(out) & 7u) == 0)
+  const bool vec =
+      dim % 4 == 0 && aligned16(x) && aligned16(w) && (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
+  if (vec && dim <= 512)
+    hipLaunchKernelGGL((rms_norm_kernel<true, uint16_t, 2>), grid, dim3(256), 0, s, x, w, out,
+                       rows, dim, eps);
+  else if (vec && dim <= 1024)
+    hipLaunchKernelGGL((rms_norm_kernel<true, uint16_t, 4>), grid, dim3(256), 0, s, x, w, out,
+                       rows, dim, eps);
+  else if (vec && dim <= 2048)
+    hipLaunchKernelGGL((rms_norm_kernel<true, uint16_t, 8>), grid, dim3(256), 0, s, x, w, out,
+                       rows, dim, eps);
+  else if (vec)
     hipLaunchKernelGGL((rms_norm_kernel<true, uint16_t>), grid, dim3(256), 0, s, x, w, out, rows,
                        dim, eps);
   else
@@ -571,7 +617,17 @@ int orator_rms_norm(const float* x, const float* weight, float* out, int rows, i
   if (!x || !weight || !out) return fail(ORATOR_ERR_INVALID, "rms_norm: null pointer");
   const bool vec = (dim % 4 == 0) && aligned16(x) && aligned16(weight) && aligned16(out);
   const dim3 grid(blocks_for(rows, 4));
-  if (vec)
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (vec && dim <= 512)
+    hipLaunchKernelGGL((rms_norm_kernel<true, float, 2>), grid, dim3(256), 0, s, x, weight, out,
+                       rows, dim, eps);
+  else if (vec && dim <= 1024)
+    hipLaunchKernelGGL((rms_norm_kernel<true, float, 4>), grid, dim3(256), 0, s, x, weight, out,
+                       rows, dim, eps);
+  else if (vec && dim <= 2048)
+    hipLaunchKernelGGL((rms_norm_kernel<true, float, 8>), grid, dim3(256), 0, s, x, weight, out,
+                       rows, dim, eps);
+  else if (vec)
     hipLaunchKernelGGL(rms_norm_kernel<true>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
                        x, weight, out, rows, dim, eps);
   else

@@ -25,7 +25,8 @@ def test_rmsnorm_fixture_and_oracle(golden):
     assert rel_err(got, orc.rms_norm(x, w, 1e-6), 1e-3) < 1e-5
 
 
-@pytest.mark.parametrize("rows,dim", [(16 * 503, 128), (8, 128), (3, 2048), (5, 130)])
+@pytest.mark.parametrize("rows,dim", [(16 * 503, 128), (8, 128), (3, 2048), (5, 130), (4, 512),
+                                      (7, 1024), (2, 4096)])
 def test_rmsnorm_qk_shapes_in_place(rows, dim):
     r = SplitMix64(rows + dim)
     x, w = r.normal((rows, dim)), r.normal((dim,))
