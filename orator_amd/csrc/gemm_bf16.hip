@@ -356,14 +356,16 @@ int launch_tile(const uint16_t* in, const uint16_t* W, const float* bias, float*
 
 // out[M][I] bf16 = bf16(silu(in W_gate^T) * (in W_up^T)), W = [gate; up] of 2I rows: the
 // gate|up projection with SwiGLU and the bf16 cast in its epilogue.  Grids too short for the
-// CUs (small M) take the plain GEMM (split K) and the standalone SwiGLU pass instead: the same
-// values either way.
+// CUs (small M) take the plain GEMM (split K) into `tmp` ([M][2I] fp32; the stream's workspace
+// when null) and the standalone SwiGLU pass instead: the same values either way.
 int launch_gemm_bf16_swiglu(const uint16_t* in, const uint16_t* W, uint16_t* out, float* tmp,
                             int M, int K, int I, hipStream_t s) {
   if (M <= 0 || K <= 0 || I <= 0) return ORATOR_OK;
   const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const long tiles = static_cast<long>((M + 127) / 128) * ((I + 63) / 64);
   if (tiles < cus) {
+    if (!tmp) tmp = static_cast<float*>(workspace(s, static_cast<size_t>(M) * 2 * I * sizeof(float)));
+    if (!tmp) return ORATOR_ERR_HIP;
     if (int rc = launch_gemm_bf16_nt(in, W, nullptr, tmp, M, K, 2 * I, 0, false, s)) return rc;
     return launch_swiglu_bf16(tmp, out, M, I, s);
   }

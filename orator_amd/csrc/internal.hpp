@@ -137,8 +137,8 @@ int launch_swiglu_bf16(const float* gu, uint16_t* out, int T, int I, hipStream_t
 int launch_gemm_bf16_nt(const uint16_t* in, const uint16_t* W, const float* bias, float* out,
                         int M, int K, int N, int act, bool accumulate, hipStream_t s);
 // The gate|up projection with SwiGLU and the bf16 cast in the GEMM epilogue (gemm_bf16.hip):
-// out[M][I] = bf16(silu(in W[0:I]^T) * (in W[I:2I]^T)); `tmp` ([M][2I] fp32) is used only
-// when the grid is too short for the fused kernel.
+// out[M][I] = bf16(silu(in W[0:I]^T) * (in W[I:2I]^T)); `tmp` ([M][2I] fp32, or null for the
+// stream's workspace) is used only when the grid is too short for the fused kernel.
 int launch_gemm_bf16_swiglu(const uint16_t* in, const uint16_t* W, uint16_t* out, float* tmp,
                             int M, int K, int I, hipStream_t s);
 

@@ -339,14 +339,15 @@ int orator_linear_pre_swiglu(const uint16_t* in_bf16, const uint16_t* W_gateup,
                             "linear_pre_swiglu"))
     return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  // the fp32 gate|up block is materialised only by the short-grid and M = 1 paths
-  float* tmp = static_cast<float*>(workspace(s, static_cast<size_t>(M) * 2 * I * sizeof(float)));
-  if (!tmp) return ORATOR_ERR_HIP;
+  // the fp32 gate|up block is materialised (in the stream's workspace) only by the M = 1 and
+  // short-grid paths
   if (M == 1) {
+    float* tmp = static_cast<float*>(workspace(s, 2 * static_cast<size_t>(I) * sizeof(float)));
+    if (!tmp) return ORATOR_ERR_HIP;
     if (int rc = launch_bf16_gemm(in_bf16, W_gateup, nullptr, tmp, 1, K, 2 * I, 0, s)) return rc;
     return launch_swiglu_bf16(tmp, out_bf16, 1, I, s);
   }
-  return launch_gemm_bf16_swiglu(in_bf16, W_gateup, out_bf16, tmp, M, K, I, s);
+  return launch_gemm_bf16_swiglu(in_bf16, W_gateup, out_bf16, nullptr, M, K, I, s);
 }
 
 int orator_linear(const float* in_f32, const uint16_t* W_bf16, const float* bias, float* out,
