@@ -77,8 +77,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
   constexpr int TM = BM / WGM, TN = BN / WGN;
   constexpr int FM = TM / 32, FN = TN / 32;
   constexpr int RPI = NT / 8;  // rows per load instruction (8 threads x 16 bytes per row)
-  constexpr int LA = BM / RPI, LW = BN / RPI;
-  static_assert(LA >= 1 && LW >= 1, "tile rows cover one load instruction");
+  // load instructions per thread per K step; a tile side that is not a multiple of RPI (96 x 64
+  // tiles: 48 rows per instruction) loads clamped rows past it and does not store them
+  constexpr int LA = (BM + RPI - 1) / RPI, LW = (BN + RPI - 1) / RPI;
   // LDS: the double-buffered tiles during the K loop, then (bias / activation epilogue) the
   // fp32 output tile, rows padded by 8 floats
   constexpr int kCLd = BN + 8;
@@ -151,9 +152,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < LA; ++i) put(&sA[buf][RPI * i + lr][0], ra[i]);
+    for (int i = 0; i < LA; ++i)
+      if (BM % RPI == 0 || RPI * i + lr < BM) put(&sA[buf][RPI * i + lr][0], ra[i]);
 #pragma unroll
-    for (int i = 0; i < LW; ++i) put(&sW[buf][RPI * i + lr][0], rw[i]);
+    for (int i = 0; i < LW; ++i)
+      if (BN % RPI == 0 || RPI * i + lr < BN) put(&sW[buf][RPI * i + lr][0], rw[i]);
   };
 
   f32x16_t acc[FM][FN];
@@ -375,7 +378,12 @@ int launch_sg(SgemmArgs a, int batch, int splits, hipStream_t s) {
 // workgroups only when the grid leaves more than half the CUs idle (up to two workgroups per
 // CU, K / 256 splits at most).  Measured at the Conformer's shapes: 717 x 2048 -> 512 takes
 // 27.7 us with 6 splits against 45.9 unsplit; 1433 x 512 -> 512 (184 tiles) 13.6 unsplit
-// against 19.1 with 2 splits.  Grouped products are never split.
+// against 19.1 with 2 splits.  Grouped products are never split.  Two tiles on one CU are
+// MFMA-bound together (each takes twice as long), so an unsplit grid that would give some CUs
+// two 64 x 64 tiles takes 96 x 64 tiles (6 waves) when that needs fewer rounds of work and K
+// is long enough for the tiles to be MFMA-bound: 717 x 512 -> 2048 (384 tiles -> 256) 28.3 ->
+// 24.5 us, -> 1536 (288 -> 192) 27.5 -> 23.5 us; at K = 64 (8 x 717 x 64 -> 717) 96-row tiles
+// were slower, 16.1 against 12.9 us.
 int run_sgemm(SgemmArgs a, int batch, hipStream_t stream) {
   const int M = a.M, N = a.N, K = a.K;
   const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
@@ -384,6 +392,14 @@ int run_sgemm(SgemmArgs a, int batch, hipStream_t stream) {
   if (2 * t <= cus && K >= 512 && !a.group)
     splits = static_cast<int>(std::min<long>((2 * cus + t - 1) / t, K / 256));
   if (static_cast<long>(batch) * splits > 65535) splits = 1;
+  if (splits == 1 && t > cus && K >= 256) {  // short K: latency-bound tiles, more is better
+    const long t96 = static_cast<long>((M + 95) / 96) * ((N + 63) / 64) * batch;
+    const long r64 = (t + cus - 1) / cus, r96 = (t96 + cus - 1) / cus;
+    if (2 * r64 > 3 * r96) {  // rounds of 64 x 64 work: r64 against 1.5 r96
+      if (a.vec) return launch_sg<96, 64, 3, 2, 2, true>(a, batch, 1, stream);
+      return launch_sg<96, 64, 3, 2, 2, false>(a, batch, 1, stream);
+    }
+  }
   if (a.vec) return launch_sg<64, 64, 2, 2, 4, true>(a, batch, splits, stream);
   return launch_sg<64, 64, 2, 2, 4, false>(a, batch, splits, stream);
 }

@@ -34,8 +34,12 @@ def test_sgemm_batched_reference_test(rows, inner, cols, batch):
 
 @pytest.mark.parametrize("M,K,N,act", [(7, 13, 9, 0), (717, 512, 512, 0), (65, 64, 130, 1),
                                        (100, 33, 70, 2), (5, 2048, 3, 3), (1433, 512, 512, 0),
-                                       (717, 512, 2048, 1), (2048, 512, 2048, 0)])
+                                       (717, 512, 2048, 1), (2048, 512, 2048, 0),
+                                       (717, 100, 1536, 0), (701, 512, 1530, 2)])
 def test_sgemm_bias_act_vs_oracle(M, K, N, act):
+    """Every tile form: 64 x 64 with and without a K split, 96 x 64 (grids that would give
+    CUs two 64 x 64 tiles: 717 x 512 -> 2048, and the ragged 717 x 100 -> 1536 (guarded loads)
+    and 701 x 512 -> 1530 (16-byte loads, ragged rows and columns))."""
     r = SplitMix64(M * 3 + K + N)
     a, w, bias = r.normal((M, K)), r.normal((N, K), 1.0 / math.sqrt(K)), r.normal((N,))
     dout = empty((M, N), np.float32)
