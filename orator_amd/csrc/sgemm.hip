@@ -375,10 +375,10 @@ int launch_sg(SgemmArgs a, int batch, int splits, hipStream_t s) {
 }
 
 // 64 x 64 tiles, 4 waves of one 32 x 32 block each, four workgroups per CU.  K is split over
-// workgroups only when the grid leaves more than half the CUs idle (up to two workgroups per
-// CU, K / 256 splits at most).  Measured at the Conformer's shapes: 717 x 2048 -> 512 takes
-// 27.7 us with 6 splits against 45.9 unsplit; 1433 x 512 -> 512 (184 tiles) 13.6 unsplit
-// against 19.1 with 2 splits.  Grouped products are never split.  Two tiles on one CU are
+// workgroups only when the grid leaves more than half the CUs idle.  Measured at the
+// Conformer's shapes: 717 x 2048 -> 512 takes 25 us with 8 splits against 45.9 unsplit;
+// 1433 x 512 -> 512 (184 tiles) 13.6 unsplit against 19.1 with 2 splits.  Grouped products
+// are never split.  Two tiles on one CU are
 // MFMA-bound together (each takes twice as long), so an unsplit grid that would give some CUs
 // two 64 x 64 tiles takes 96 x 64 tiles (6 waves) when that needs fewer rounds of work and K
 // is long enough for the tiles to be MFMA-bound: 717 x 512 -> 2048 (384 tiles -> 256) 28.3 ->
@@ -389,8 +389,20 @@ int run_sgemm(SgemmArgs a, int batch, hipStream_t stream) {
   const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const long t = static_cast<long>((M + 63) / 64) * ((N + 63) / 64) * batch;
   int splits = 1;
-  if (2 * t <= cus && K >= 512 && !a.group)
-    splits = static_cast<int>(std::min<long>((2 * cus + t - 1) / t, K / 256));
+  if (2 * t <= cus && K >= 512 && !a.group) {
+    // the split count with the least work per CU in whole rounds, ceil(t s / cus) / s (ties to
+    // fewer splits), K / 256 and 8 at most: 717 x 2048 -> 512 (96 tiles) takes 8 splits (768
+    // workgroups, 3 rounds of 1/8): 24.7-25.9 us, against 25.9-27.4 with 5 and 27.5-28.9 with 6
+    long best_num = 1, best_den = 1;  // 1 round of the whole K
+    for (long sp = 2; sp <= std::min<long>(8, K / 256); ++sp) {
+      const long rounds = (t * sp + cus - 1) / cus;
+      if (rounds * best_den < best_num * sp) {
+        best_num = rounds;
+        best_den = sp;
+      }
+    }
+    splits = static_cast<int>(best_den);
+  }
   if (static_cast<long>(batch) * splits > 65535) splits = 1;
   if (splits == 1 && t > cus && K >= 256) {  // short K: latency-bound tiles, more is better
     const long t96 = static_cast<long>((M + 95) / 96) * ((N + 63) / 64) * batch;
