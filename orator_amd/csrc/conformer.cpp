@@ -7,9 +7,10 @@
 //   x += 0.5 FFN2(LN(x));  x = LN_out(x)
 // The projections run on the fp32 MFMA SGEMM; the attention core is either the reference
 // decomposition in fp32 (attn_mode 0) or the fused fp16 MFMA kernel (attn_mode 1).  Each
-// residual update x += s * (h W^T + b) is the last projection's epilogue (the same fp32
-// value, then one fused multiply-add, exact for s = 0.5 and 1), q/k/v are one grouped launch
-// sharing LN(x), and the closing LayerNorm writes x in place.
+// residual update x += s * (h W^T + b) is the last projection's epilogue or split-K reduce
+// (the same fp32 value, then one fused multiply-add, exact for s = 0.5 and 1), and that reduce
+// also writes the next block's LayerNorm of x (the closing one in place); q/k/v are one grouped
+// launch sharing LN(x).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -20,8 +21,6 @@
 
 namespace orator_hip {
 
-int launch_layer_norm(const float* in, const float* g, const float* b, float* out, int T, int C,
-                      float eps, hipStream_t s);
 int launch_glu_mask(const float* in, float* out, int T, int C, int valid, hipStream_t s);
 int launch_dwconv_bn_silu(const float* in, const float* w, const float* bias, const float* mean,
                           const float* var, const float* gamma, const float* beta, float* out,
@@ -83,12 +82,13 @@ struct Conformer {
     return launch_sgemm_group3(ln, W, b, out, T, D, D, s);
   }
 
-  int ffn(float* x, int T, const float* nw, const float* nb, const float* w1, const float* b1,
-          const float* w2, const float* b2, hipStream_t s) {
+  // x += 0.5 FFN(ln) (ln = this block's LayerNorm of x), then next_out = the next block's
+  // LayerNorm of the updated x (ng, nb)
+  int ffn(float* x, int T, const float* w1, const float* b1, const float* w2, const float* b2,
+          const float* ng, const float* nb, float* next_out, hipStream_t s) {
     int rc = 0;
-    (rc = launch_layer_norm(x, nw, nb, ln, T, D, kEps, s)) ||
-        (rc = linear(ln, w1, b1, ff, T, D, Dff, 1, s)) ||  // SiLU
-        (rc = launch_sgemm_residual(ff, w2, b2, x, T, Dff, D, 0.5f, s));
+    (rc = linear(ln, w1, b1, ff, T, D, Dff, 1, s)) ||  // SiLU
+        (rc = launch_sgemm_residual_ln(ff, w2, b2, x, T, Dff, D, 0.5f, ng, nb, next_out, kEps, s));
     return rc;
   }
 
@@ -97,12 +97,14 @@ struct Conformer {
     const int P = 2 * T - 1, Dk = D / H;
     const float scale = 1.0f / std::sqrt(static_cast<float>(Dk));
     int rc = 0;
-    // FFN1
-    if ((rc = ffn(x, T, w.norm_ff1_w, w.norm_ff1_b, w.ff1_w1, w.ff1_b1, w.ff1_w2, w.ff1_b2, s)))
-      return rc;
+    // FFN1.  Its LayerNorm is the only separate one: every residual update below also writes
+    // the next block's LayerNorm of x (into `ln`, whose previous contents are consumed by then;
+    // the last one, norm_out, into x itself).
+    (rc = launch_layer_norm(x, w.norm_ff1_w, w.norm_ff1_b, ln, T, D, kEps, s)) ||
+        (rc = ffn(x, T, w.ff1_w1, w.ff1_b1, w.ff1_w2, w.ff1_b2, w.norm_att_w, w.norm_att_b, ln, s));
+    if (rc) return rc;
     // MHSA
-    (rc = launch_layer_norm(x, w.norm_att_w, w.norm_att_b, ln, T, D, kEps, s)) ||
-        (rc = qkv(T, s)) ||
+    (rc = qkv(T, s)) ||
         (rc = linear(pos_emb, w.pos_w, nullptr, p, P, D, D, 0, s));
     if (rc) return rc;
     rc = attn_mode == 1
@@ -110,19 +112,18 @@ struct Conformer {
                                             valid, scale, 0, s)
              : orator_relpos_attention(q, k, v, p, w.pos_bias_u, w.pos_bias_v, ctx, T, H, Dk,
                                        valid, scale, s);
-    (rc) || (rc = launch_sgemm_residual(ctx, w.out_w, w.out_b, x, T, D, D, 1.0f, s));
+    (rc) || (rc = launch_sgemm_residual_ln(ctx, w.out_w, w.out_b, x, T, D, D, 1.0f, w.norm_conv_w,
+                                           w.norm_conv_b, ln, kEps, s));
     if (rc) return rc;
     // Conv module
-    (rc = launch_layer_norm(x, w.norm_conv_w, w.norm_conv_b, ln, T, D, kEps, s)) ||
-        (rc = pw1_glu(T, valid, s)) ||
+    (rc = pw1_glu(T, valid, s)) ||
         (rc = launch_dwconv_bn_silu(glu, w.dw_w, w.dw_b, w.bn_mean, w.bn_var, w.bn_w, w.bn_b, dw,
                                     T, D, K, kEps, s)) ||
-        (rc = launch_sgemm_residual(dw, w.pw2_w, w.pw2_b, x, T, D, D, 1.0f, s));
+        (rc = launch_sgemm_residual_ln(dw, w.pw2_w, w.pw2_b, x, T, D, D, 1.0f, w.norm_ff2_w,
+                                       w.norm_ff2_b, ln, kEps, s));
     if (rc) return rc;
-    // FFN2, norm_out
-    (rc = ffn(x, T, w.norm_ff2_w, w.norm_ff2_b, w.ff2_w1, w.ff2_b1, w.ff2_w2, w.ff2_b2, s)) ||
-        (rc = launch_layer_norm(x, w.norm_out_w, w.norm_out_b, x, T, D, kEps, s));
-    return rc;
+    // FFN2, then norm_out in place
+    return ffn(x, T, w.ff2_w1, w.ff2_b1, w.ff2_w2, w.ff2_b2, w.norm_out_w, w.norm_out_b, x, s);
   }
 };
 

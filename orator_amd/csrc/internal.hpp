@@ -151,6 +151,17 @@ int launch_sgemm(const float* in, const float* W, const float* bias, float* out,
 int launch_sgemm_residual(const float* in, const float* W, const float* bias, float* out, int M,
                           int K, int N, float res_scale, hipStream_t stream);
 
+// launch_sgemm_residual, then ln_out = LayerNorm(out rows; ln_g, ln_b, eps) (conformer_layer.cu:
+// 28-66, the next block's norm), fused into the split-K reduce when K is split and N <= 1024
+// (else a LayerNorm pass); ln_out may be out.  Same bits as the two operations.
+int launch_sgemm_residual_ln(const float* in, const float* W, const float* bias, float* out,
+                             int M, int K, int N, float res_scale, const float* ln_g,
+                             const float* ln_b, float* ln_out, float eps, hipStream_t stream);
+
+// LayerNorm of T rows of C (conformer_ops.hip); out may be in.
+int launch_layer_norm(const float* in, const float* g, const float* b, float* out, int T, int C,
+                      float eps, hipStream_t s);
+
 // The Conformer conv module's pointwise_conv1 + GLU + padding-row mask in one launch
 // (src/model/conformer_layer.cu:455-458): W [2C][K] (value rows, then gate rows), out [M][C] =
 // a * (1 / (1 + __expf(-b))) of the biased value / gate outputs, 0 for rows >= valid.

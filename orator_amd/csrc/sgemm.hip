@@ -64,6 +64,13 @@ struct SgemmArgs {
   // a * (1 / (1 + exp(-b))) with a, b the value and gate outputs (bias added), 0 for rows
   // m >= glu_valid; out is [M][glu_c].
   int glu_c, glu_valid;
+  // LayerNorm of the updated rows (ln_g non-null; split-K reduce only): ln_out[m] =
+  // (x - mean) rsqrt(var + eps) g + b over the row's N values x = out[m] after the residual
+  // update; ln_out == out writes the normalised row only.
+  const float* ln_g;
+  const float* ln_b;
+  float* ln_out;
+  float ln_eps;
 };
 
 // Epilogues: raw split-K partials, out = acc (no bias, act 0), and through LDS out =
@@ -338,6 +345,67 @@ __global__ __launch_bounds__(256) void sgemm_splitk_reduce_kernel(const float* _
   out[b * s_out + r] = v;
 }
 
+// The split-K reduce with the residual update, then a LayerNorm of each updated row: one wave
+// per row, lane l holding columns l, l + 64, ... (N <= 64 PER).  Per element the same
+// arithmetic as sgemm_splitk_reduce_kernel (partials in split order, bias, residual fmaf);
+// the normalisation is layer_norm_kernel's (lane-order sums, the wave sum, contraction off),
+// so x and LN(x) carry the same bits as the reduce followed by the LayerNorm pass.
+constexpr int kMaxLnSplits = 8;  // the split count run_sgemm chooses is at most 8
+
+template <int PER, int MAXS>
+__global__ __launch_bounds__(256) void sgemm_splitk_reduce_ln_kernel(
+    const float* __restrict__ part, int splits, const float* __restrict__ bias, float* out,
+    int M, int N, float res_scale, const float* __restrict__ g, const float* __restrict__ b,
+    float* ln_out, float eps) {
+#pragma clang fp contract(off)
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const long MN = static_cast<long>(M) * N;
+  const long base = static_cast<long>(row) * N;
+  // every partial of the lane's columns is loaded at once (one memory round trip: a wave per
+  // row leaves few waves per CU); the sum keeps split order, terms past `splits` selected away
+  float p[PER][MAXS], old[PER], bv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int n = min(lane + 64 * i, N - 1);
+#pragma unroll
+    for (int z = 0; z < MAXS; ++z) p[i][z] = part[min(z, splits - 1) * MN + base + n];
+    old[i] = out[base + n];
+    bv[i] = bias ? bias[n] : 0.0f;
+  }
+  float v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    float x = p[i][0];
+#pragma unroll
+    for (int z = 1; z < MAXS; ++z) x = z < splits ? x + p[i][z] : x;
+    x = x + bv[i];
+    v[i] = fmaf(res_scale, x, old[i]);
+  }
+  const bool in_place = ln_out == out;
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    if (!in_place && lane + 64 * i < N) out[base + lane + 64 * i] = v[i];
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    if (lane + 64 * i < N) sum += v[i];
+  const float mean = wave_sum(sum) / static_cast<float>(N);
+  float sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const float t = v[i] - mean;
+    if (lane + 64 * i < N) sq += t * t;
+  }
+  const float inv = rsqrtf(wave_sum(sq) / static_cast<float>(N) + eps);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int n = lane + 64 * i;
+    if (n < N) ln_out[base + n] = (v[i] - mean) * inv * g[n] + b[n];
+  }
+}
+
 template <int BM, int BN, int WGM, int WGN, int MINW, bool VEC>
 int launch_sg(SgemmArgs a, int batch, int splits, hipStream_t s) {
   a.k_split = a.K;
@@ -366,12 +434,29 @@ int launch_sg(SgemmArgs a, int batch, int splits, hipStream_t s) {
     hipLaunchKernelGGL((sgemm_nt_kernel<BM, BN, WGM, WGN, MINW, VEC, kSEpiStore>), grid, block,
                        0, s, a);
   if (int rc = check_launch("sgemm_nt_kernel")) return rc;
-  if (splits == 1) return ORATOR_OK;
+  if (splits == 1) {
+    if (!a.ln_g) return ORATOR_OK;
+    return launch_layer_norm(a.out, a.ln_g, a.ln_b, a.ln_out, a.M, a.N, a.ln_eps, s);
+  }
+  if (a.ln_g && a.N <= 1024 && splits <= kMaxLnSplits) {  // batch 1, act 0, residual
+    const dim3 rgrid((a.M + 3) / 4);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, rgrid, dim3(256), 0, s, a.part, splits, a.bias, a.out, a.M, a.N,
+                         a.res_scale, a.ln_g, a.ln_b, a.ln_out, a.ln_eps);
+    };
+    if (a.N <= 512)
+      splits <= 2 ? go(sgemm_splitk_reduce_ln_kernel<8, 2>) : go(sgemm_splitk_reduce_ln_kernel<8, 8>);
+    else
+      splits <= 2 ? go(sgemm_splitk_reduce_ln_kernel<16, 2>) : go(sgemm_splitk_reduce_ln_kernel<16, 8>);
+    return check_launch("sgemm_splitk_reduce_ln");
+  }
   const long total = MN * batch;
   hipLaunchKernelGGL(sgemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
                      dim3(256), 0, s, a.part, splits, batch, a.bias, a.out, a.M, a.N, a.act,
                      batch > 1 ? a.s_out : MN, a.residual, a.res_scale);
-  return check_launch("sgemm_splitk_reduce");
+  if (int rc = check_launch("sgemm_splitk_reduce")) return rc;
+  if (!a.ln_g) return ORATOR_OK;
+  return launch_layer_norm(a.out, a.ln_g, a.ln_b, a.ln_out, a.M, a.N, a.ln_eps, s);
 }
 
 // 64 x 64 tiles, 4 waves of one 32 x 32 block each, four workgroups per CU.  K is split over
@@ -456,6 +541,31 @@ int launch_sgemm_residual(const float* in, const float* W, const float* bias, fl
   a.N = N;
   a.residual = 1;
   a.res_scale = res_scale;
+  a.vec = (K % kSK) == 0 &&
+          ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15) == 0;
+  return run_sgemm(a, 1, stream);
+}
+
+int launch_sgemm_residual_ln(const float* in, const float* W, const float* bias, float* out,
+                             int M, int K, int N, float res_scale, const float* ln_g,
+                             const float* ln_b, float* ln_out, float eps, hipStream_t stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return ORATOR_OK;
+  if (!in || !W || !out || !ln_g || !ln_b || !ln_out)
+    return fail(ORATOR_ERR_INVALID, "sgemm_residual_ln: null pointer");
+  SgemmArgs a{};
+  a.in = in;
+  a.W = W;
+  a.bias = bias;
+  a.out = out;
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.residual = 1;
+  a.res_scale = res_scale;
+  a.ln_g = ln_g;
+  a.ln_b = ln_b;
+  a.ln_out = ln_out;
+  a.ln_eps = eps;
   a.vec = (K % kSK) == 0 &&
           ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15) == 0;
   return run_sgemm(a, 1, stream);
