@@ -14,14 +14,19 @@
 //
 // Work split.  A workgroup is 8 wave64s: RW query-row waves (32 query columns each) times
 // KG = 8/RW key groups.  Key group g takes the 32-key tiles g, g+KG, g+2KG, ... of the
-// block's causal key range with its own double-buffered LDS tiles; the KG partial softmax
-// states are merged through LDS at the end.  Two waves per SIMD (<= 256 VGPRs each) let one
-// wave's softmax VALU run under the other's MFMAs.  The launcher picks
+// block's causal key range with its own LDS tiles; the KG partial softmax states are merged
+// through LDS at the end.  Two waves per SIMD (<= 256 VGPRs each) let one wave's softmax
+// VALU run under the other's MFMAs.  The launcher picks
 //  * RW = 4, KG = 2 (128 query rows share every K/V tile) when that still gives every CU
 //    two workgroups: a CU then pulls 32 B/clk of K/V at full MFMA rate, half of what its
 //    vector memory path sustains, and registers hold a prefetch two rounds ahead;
-//  * RW = 2, KG = 4 (64 rows per tile, 64 B/clk at full rate) for short prompts, which need
-//    the extra workgroups.
+//  * RW = 2, KG = 4 (64 rows per tile, 64 B/clk at full rate) when RW = 4 would not;
+//  * RW = 1, KG = 8 when even RW = 2 leaves CUs without a workgroup (T = 503 on 8 kv heads:
+//    256 workgroups instead of 128, at most two tiles per wave).  Such prompts are a chain of
+//    latencies, not a throughput problem: every wave is its own key group with a single
+//    buffer (no barrier per round), the loads of its first two tiles go out before the pos0
+//    read, and the workgroup's q is read once, row-contiguous, and staged in LDS (a lane per
+//    query row re-read by all 8 groups touched 64 cache lines per load instruction).
 //
 // Per tile and wave:
 //  * S^T = K Q^T: K tile rows are the MFMA A operand (ds_read_b128 from a padded,
@@ -88,10 +93,12 @@ struct PrefillArgs {
   float scale_log2e;      // > 0
 };
 
-// One key group's LDS: double-buffered K and V rows.
+// One key group's LDS: NB buffers of K and V rows (double-buffered for groups of several
+// waves, single for the one-wave groups of the short-prompt form).
+template <int NB>
 struct GroupTiles {
-  uint16_t k[2][kBN][kKRow];
-  uint16_t v[2][kBN][kVRow];
+  uint16_t k[NB][kBN][kKRow];
+  uint16_t v[NB][kBN][kVRow];
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
@@ -160,11 +167,18 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   constexpr int NP = kBN * 16 / GT;            // 16-byte chunks per thread per K (or V) tile
   constexpr int RPP = GT / 16;                 // tile rows covered by one pass of the group
   constexpr int DIST = (!PRECISE && RW == 4) ? 2 : 1;  // register prefetch distance (rounds)
-  constexpr int D = 4 / KG;                    // 32-dim output blocks each wave finalizes
+  constexpr int NB = RW == 1 ? 1 : 2;          // tile buffers per key group
+  constexpr int CS = 64 / KG;                  // accumulator values per lane each wave finalizes
+  using Tiles = GroupTiles<NB>;
+  // q staged once per workgroup through LDS (measured: a gain for the one-wave key groups and
+  // fp32 mode's three terms at RW = 2, a small loss for bf16 at RW = 2)
+  constexpr bool kStageQ = RW == 1 || (RW == 2 && PRECISE);
+  static_assert(!kStageQ || (PRECISE ? 3 : 1) * RW * 32 * kKRow * 2 <= KG * (int)sizeof(Tiles),
+                "q staging area fits in the tile buffers");
   static_assert(KG * RW == 8 && NP * RPP == kBN, "tile split");
-  static_assert(8 * (4 - D) * 16 * 64 * 4 + 8 * 2 * 64 * 4 <= KG * (int)sizeof(GroupTiles),
+  static_assert(8 * (KG - 1) * CS * 64 * 4 + 8 * 2 * 64 * 4 <= KG * (int)sizeof(Tiles),
                 "merge area reuses the tile buffers");
-  __shared__ __align__(16) unsigned char smem[KG * sizeof(GroupTiles)];
+  __shared__ __align__(16) unsigned char smem[KG * sizeof(Tiles)];
   __shared__ int row_lds[kMaxRowGroups];
 
   const int kvh = blockIdx.x % a.Hkv;
@@ -177,9 +191,51 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   const int gt = tid % GT;                                    // thread index within the group
   const int h2 = lane >> 5;   // which half of the 32x32 accumulator rows this lane holds
   const int col = lane & 31;  // this lane's query column
-  const int pos0 = *a.pos0p;
-  GroupTiles& tl = reinterpret_cast<GroupTiles*>(smem)[grp];
+  Tiles& tl = reinterpret_cast<Tiles*>(smem)[grp];
   const bool contiguous = a.page_table == nullptr;  // row of key k is k
+
+  // ---- tile loader (group-local tile j = key tile grp + KG*j) ----
+  // K and V rows ld_row + RPP*p (p < NP), one 16-byte chunk (dims 8*ld_chunk..) per thread;
+  // with the padded rows the LDS stores are conflict-free.
+  const long rs = static_cast<long>(a.Hkv) * kDh;  // elements between consecutive rows
+  const uint16_t* kbase = a.kpool + static_cast<long>(kvh) * kDh;
+  const uint16_t* vbase = a.vpool + static_cast<long>(kvh) * kDh;
+  const int ld_row = gt >> 4, ld_chunk = gt & 15;
+  const uint32_t lane_off = static_cast<uint32_t>((ld_row * rs + 8 * ld_chunk) * 2);  // bytes
+  const long rs2 = rs * 2;
+
+  // One-wave key groups over a contiguous cache issue the loads of their first two tiles
+  // before the pos0 read, for the tiles a block needs whatever pos0 is (keys below
+  // min(t_end, capacity)); rows are clamped to the capacity, and keys past the range a block
+  // needs are masked (scores) or zeroed (V) as always.  fp32 mode leaves V(1) for later
+  // (register budget).
+  u32x4_t kr[NP], vr[NP], kn[NP], vn[NP];
+  bool early0 = false, early1 = false;
+  if constexpr (RW == 1) {
+    if (contiguous) {
+      const int tb = a.n_tblocks - 1 - wi;  // RW = 1 grids are never paired
+      const int lb = min(min((tb + 1) * BT, a.Tq), a.capacity);
+      auto early_rows = [&](const uint16_t* base, int k0, u32x4_t (&r)[NP]) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+          r[p] = *reinterpret_cast<const u32x4_t*>(
+              base + static_cast<long>(min(k0 + RPP * p + ld_row, a.capacity - 1)) * rs +
+              8 * ld_chunk);
+      };
+      early0 = kBN * grp < lb;
+      early1 = kBN * (grp + KG) < lb;
+      if (early0) {
+        early_rows(kbase, kBN * grp, kr);
+        early_rows(vbase, kBN * grp, vr);
+      }
+      if (early1) {
+        early_rows(kbase, kBN * (grp + KG), kn);
+        if (!PRECISE) early_rows(vbase, kBN * (grp + KG), vn);
+      }
+    }
+  }
+  asm volatile("" ::: "memory");  // the loads above are issued before the pos0 read
+  const int pos0 = *a.pos0p;
 
   // One token block: keys, tiles, softmax state, output.  Returns after its output is
   // stored; every thread runs every barrier of it.
@@ -213,35 +269,65 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   // B operand per 16-dim k-step (dims 16ks + 8*h2 + e).  fp32 mode carries q as three bf16
   // terms hi + mid + lo (exact to fp32 rounding); bf16 mode uses hi only.
   uint4 qhi[8], qmid[8], qlo[8];
-  {
+  // Splits 8 fp32 q values into the bf16 terms (hi, mid, lo) this mode uses.
+  auto q_terms = [&](const float* src, uint4& hi, uint4& mid, uint4& lo) {
+    const float4 x0 = *reinterpret_cast<const float4*>(src);
+    const float4 x1 = *reinterpret_cast<const float4*>(src + 4);
+    float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    split8(xs, hi, mid);
+    if (PRECISE) split8(xs, mid, lo);
+  };
+  if constexpr (kStageQ) {
+    // The workgroup's RW*32 query columns are read once, with row-contiguous loads (a lane
+    // per 8 dims), and staged in LDS as bf16 terms ([term][column][kKRow]; the K tiles'
+    // padded rows, so the B-operand reads below are conflict-free), instead of every key
+    // group's waves loading them a row per lane.
+    uint16_t* qs = reinterpret_cast<uint16_t*>(smem);
+    for (int it = tid; it < RW * 32 * 16; it += kThreads) {
+      const int qc = it >> 4, qd = it & 15;  // column, 8-dim chunk
+      const int t = t_blk + (qc >> 5) * TW + (qc & 31) % TW;
+      const int h = kvh * G + (qc & 31) / TW;
+      uint4 hi = make_uint4(0, 0, 0, 0), mid = hi, lo = hi;
+      if (t < a.Tq) {
+        const long off = (static_cast<long>(t) * a.Hq + h) * kDh + 8 * qd;
+        if (a.q)
+          q_terms(a.q + off, hi, mid, lo);
+        else
+          hi = *reinterpret_cast<const uint4*>(a.q_bf16 + off);
+      }
+      *reinterpret_cast<uint4*>(qs + qc * kKRow + 8 * qd) = hi;
+      if (PRECISE) {
+        *reinterpret_cast<uint4*>(qs + (RW * 32 + qc) * kKRow + 8 * qd) = mid;
+        *reinterpret_cast<uint4*>(qs + (2 * RW * 32 + qc) * kKRow + 8 * qd) = lo;
+      }
+    }
+    lds_barrier();  // staged q and row_lds ready
+    const uint16_t* qrow = qs + (rw * 32 + col) * kKRow + 8 * h2;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      qhi[ks] = *reinterpret_cast<const uint4*>(qrow + 16 * ks);
+      qmid[ks] = qlo[ks] = make_uint4(0, 0, 0, 0);
+      if (PRECISE) {
+        qmid[ks] = *reinterpret_cast<const uint4*>(qrow + RW * 32 * kKRow + 16 * ks);
+        qlo[ks] = *reinterpret_cast<const uint4*>(qrow + 2 * RW * 32 * kKRow + 16 * ks);
+      }
+    }
+    lds_barrier();  // every wave has its q before the tiles overwrite the staging area
+  } else {
     const long qoff = (static_cast<long>(tq) * a.Hq + hq) * kDh + 8 * h2;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       qmid[ks] = qlo[ks] = make_uint4(0, 0, 0, 0);
-      if (!q_valid) {
+      if (!q_valid)
         qhi[ks] = make_uint4(0, 0, 0, 0);
-      } else if (a.q) {
-        const float4 x0 = *reinterpret_cast<const float4*>(a.q + qoff + 16 * ks);
-        const float4 x1 = *reinterpret_cast<const float4*>(a.q + qoff + 16 * ks + 4);
-        float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        split8(xs, qhi[ks], qmid[ks]);
-        if (PRECISE) split8(xs, qmid[ks], qlo[ks]);
-      } else {
+      else if (a.q)
+        q_terms(a.q + qoff + 16 * ks, qhi[ks], qmid[ks], qlo[ks]);
+      else
         qhi[ks] = *reinterpret_cast<const uint4*>(a.q_bf16 + qoff + 16 * ks);
-      }
     }
+    lds_barrier();  // row_lds ready
   }
-  lds_barrier();  // row_lds ready
 
-  // ---- tile loader (group-local tile j = key tile grp + KG*j) ----
-  // K and V rows ld_row + RPP*p (p < NP), one 16-byte chunk (dims 8*ld_chunk..) per thread;
-  // with the padded rows the LDS stores are conflict-free.
-  const long rs = static_cast<long>(a.Hkv) * kDh;  // elements between consecutive rows
-  const uint16_t* kbase = a.kpool + static_cast<long>(kvh) * kDh;
-  const uint16_t* vbase = a.vpool + static_cast<long>(kvh) * kDh;
-  const int ld_row = gt >> 4, ld_chunk = gt & 15;
-  const uint32_t lane_off = static_cast<uint32_t>((ld_row * rs + 8 * ld_chunk) * 2);  // bytes
-  const long rs2 = rs * 2;
   // Row of `key` (clamped to the last needed key, so every load stays in bounds).
   auto row_clamped = [&](int key) -> long {
     key = min(key, n_keys - 1);
@@ -363,42 +449,107 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
     }
   };
 
-  // Softmax of tile j (scores s) and O^T += V^T P^T from V buffer `buf` (fp32 mode).
+  // Softmax of tile j (scores s) and O^T += V^T P^T from V buffer `buf`, one 16-key k-step
+  // at a time (register pressure).
   auto softmax_pv = [&](f32x16_t s, int j, int buf) {
     const float mref = mask_and_rescale(s, j);
-    // B operand per 16-key k-step st (keys 16st + 8(e/4) + 4*h2 + e%4), each weight as
-    // hi + mid + lo bf16 terms: both remainders are exact in fp32, so the three terms carry
-    // the fp32 weight to ~2^-26 relative.  One k-step at a time (register pressure).
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(fmaf(s[8 * st + e], c, -mref));
-      uint32_t hw[4], mw[4], lw[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        hw[e] = cvt_bf16x2(pv[2 * e], pv[2 * e + 1]);
-        const float r0 = pv[2 * e] - bf16_lo(hw[e]), r1 = pv[2 * e + 1] - bf16_hi(hw[e]);
-        mw[e] = cvt_bf16x2(r0, r1);
-        lw[e] = cvt_bf16x2(r0 - bf16_lo(mw[e]), r1 - bf16_hi(mw[e]));
-        lsum += pv[2 * e] + pv[2 * e + 1];
-      }
-      const uint4 phi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-      const uint4 pmid = make_uint4(mw[0], mw[1], mw[2], mw[3]);
-      const uint4 plo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
       uint4 vf[4];
-      read_vf(buf, st, vf);
+      if constexpr (PRECISE) {
+        // B operand per k-step st (keys 16st + 8(e/4) + 4*h2 + e%4), each weight as
+        // hi + mid + lo bf16 terms: both remainders are exact in fp32, so the three terms
+        // carry the fp32 weight to ~2^-26 relative.
+        uint32_t hw[4], mw[4], lw[4];
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const bf16x8_t va = as_bf16x8(vf[dt]);
-        o[dt] = mfma32(va, as_bf16x8(plo), o[dt]);
-        o[dt] = mfma32(va, as_bf16x8(pmid), o[dt]);
-        o[dt] = mfma32(va, as_bf16x8(phi), o[dt]);
+        for (int e = 0; e < 4; ++e) {
+          hw[e] = cvt_bf16x2(pv[2 * e], pv[2 * e + 1]);
+          const float r0 = pv[2 * e] - bf16_lo(hw[e]), r1 = pv[2 * e + 1] - bf16_hi(hw[e]);
+          mw[e] = cvt_bf16x2(r0, r1);
+          lw[e] = cvt_bf16x2(r0 - bf16_lo(mw[e]), r1 - bf16_hi(mw[e]));
+          lsum += pv[2 * e] + pv[2 * e + 1];
+        }
+        const uint4 phi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        const uint4 pmid = make_uint4(mw[0], mw[1], mw[2], mw[3]);
+        const uint4 plo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        read_vf(buf, st, vf);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const bf16x8_t va = as_bf16x8(vf[dt]);
+          o[dt] = mfma32(va, as_bf16x8(plo), o[dt]);
+          o[dt] = mfma32(va, as_bf16x8(pmid), o[dt]);
+          o[dt] = mfma32(va, as_bf16x8(phi), o[dt]);
+        }
+      } else {
+        // bf16 weights, and the row sum of those bf16 values (the pipelined rounds' form)
+        uint32_t hw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hw[e] = cvt_bf16x2(pv[2 * e], pv[2 * e + 1]);
+          lsum = add_bf16x2(hw[e], lsum);
+        }
+        const uint4 phi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        read_vf(buf, st, vf);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] = mfma32(as_bf16x8(vf[dt]), as_bf16x8(phi), o[dt]);
       }
+      // one k-step's temporaries at a time (the one-wave key groups keep a tile in flight)
+      if constexpr (RW == 1) __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  if constexpr (!PRECISE) {
+  if constexpr (RW == 1) {
+    // Short prompts: every wave is a key group of its own with a single K and V buffer that
+    // no other wave touches, so the rounds need no workgroup barrier.  A wave's LDS
+    // instructions execute in issue order, so a tile may be stored over the previous one
+    // right after that one's reads; compiler fences keep the order.  A wave loads and
+    // computes its own tiles only.
+    //  * bf16 mode, round j: S of tile j, store K(j+1); softmax and PV of tile j, store
+    //    V(j+1); load tile j+2.  At most two tiles per wave (the prompts this form is chosen
+    //    for) are all loaded in the prologue: one memory latency.
+    //  * fp32 mode holds three q terms, so only K(j+1) is in flight during S of tile j and no
+    //    tile during the softmax and PV; V(j+1) is loaded after them.
+    if (my_tiles > 0 && !early0) {
+      load_k(0, kr);
+      load_v(0, vr);
+    }
+    if (my_tiles > 1 && !early1) {
+      load_k(1, kn);
+      if (!PRECISE) load_v(1, vn);
+    }
+    if (my_tiles > 0) {
+      store_k(0, kr);
+      store_v(0, vr, 0);
+    }
+    for (int j = 0; j < my_tiles; ++j) {
+      asm volatile("" ::: "memory");
+      const f32x16_t sj = qk(0);
+      asm volatile("" ::: "memory");
+      if constexpr (!PRECISE) {
+        if (j + 1 < my_tiles) store_k(0, kn);
+        softmax_pv(sj, j, 0);
+        asm volatile("" ::: "memory");
+        if (j + 1 < my_tiles) store_v(0, vn, j + 1);
+        if (j + 2 < my_tiles) {
+          load_k(j + 2, kn);
+          load_v(j + 2, vn);
+        }
+      } else {
+        if (j + 1 < my_tiles) store_k(0, kn);
+        softmax_pv(sj, j, 0);
+        asm volatile("" ::: "memory");
+        if (j + 1 < my_tiles) {
+          load_v(j + 1, vn);
+          store_v(0, vn, j + 1);
+        }
+        if (j + 2 < my_tiles) load_k(j + 2, kn);
+      }
+    }
+    lds_barrier();  // every wave's tiles are consumed before the merge reuses them
+  } else if constexpr (!PRECISE) {
     // Register prefetch sets: set (j % DIST) holds K(j+2), V(j+1) at the start of round j.
     u32x4_t kr[DIST][NP], vr[DIST][NP];
     // Phases of one bf16 round, in issue order: LDS stores of the prefetched K(j+2), V(j+1);
@@ -499,18 +650,19 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
     }
   }
 
-  // ---- merge the KG key groups through LDS.  Wave (grp, rw) finishes output dims
-  // [32*D*grp, 32*D*(grp+1)) of its query rows; every wave hands the other groups the
-  // 32-dim blocks they finish. ----
+  // ---- merge the KG key groups through LDS.  A lane's 64 accumulator values (block dt,
+  // element e: flat index 16*dt + e) form KG chunks of CS; wave (grp, rw) finishes chunk grp
+  // of its query columns, and hands every other chunk to the wave that finishes it. ----
   lsum = xor32_sum(lsum);
-  float* mo = reinterpret_cast<float*>(smem);  // [wave][4 - D blocks][16 values][64 lanes]
-  float* mml = mo + 8 * (4 - D) * 16 * 64;     // [wave][m, l][64 lanes]
+  float* mo = reinterpret_cast<float*>(smem);  // [wave][KG - 1 chunks][CS values][64 lanes]
+  float* mml = mo + 8 * (KG - 1) * CS * 64;    // [wave][m, l][64 lanes]
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-    if (dt / D == grp) continue;  // uniform
-    const int slot = dt < grp * D ? dt : dt - D;
+  for (int ch = 0; ch < KG; ++ch) {
+    if (ch == grp) continue;  // uniform
+    const int slot = ch < grp ? ch : ch - 1;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) mo[((wave * (4 - D) + slot) * 16 + e) * 64 + lane] = o[dt][e];
+    for (int i = 0; i < CS; ++i)
+      mo[((wave * (KG - 1) + slot) * CS + i) * 64 + lane] = o[(ch * CS + i) / 16][(ch * CS + i) % 16];
   }
   mml[(wave * 2) * 64 + lane] = m;
   mml[(wave * 2 + 1) * 64 + lane] = lsum;
@@ -530,43 +682,42 @@ __global__ __launch_bounds__(kThreads) void gqa_prefill_kernel(PrefillArgs a) {
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   if (q_valid) {
-  float* orow = a.out + (static_cast<long>(tq) * a.Hq + hq) * kDh + 4 * h2;
+    // this wave's own chunk, weighted, plus the other groups' weighted chunks in group order
+    float f[CS];
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    const int dt = grp * D + d;
-    // this wave's own block dt = grp * D + d
-    f32x16_t f;
-    if constexpr (KG == 2) {
-      f = grp ? o[2 + d] : o[d];
-    } else {
-      f = grp == 0 ? o[0] : grp == 1 ? o[1] : grp == 2 ? o[2] : o[3];
-    }
+    for (int ch = 0; ch < KG; ++ch)
+      if (ch == grp)
+#pragma unroll
+        for (int i = 0; i < CS; ++i) f[i] = o[(ch * CS + i) / 16][(ch * CS + i) % 16];
     float w_own = w[0];
 #pragma unroll
     for (int g = 1; g < KG; ++g)
       if (grp == g) w_own = w[g];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) f[e] *= w_own;
+    for (int i = 0; i < CS; ++i) f[i] *= w_own;
 #pragma unroll
     for (int g = 0; g < KG; ++g) {
       if (g == grp) continue;
-      const int slot = dt < g * D ? dt : dt - D;
-      const float* src = mo + ((g * RW + rw) * (4 - D) + slot) * 16 * 64 + lane;
+      const int slot = grp < g ? grp : grp - 1;
+      const float* src = mo + ((g * RW + rw) * (KG - 1) + slot) * CS * 64 + lane;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) f[e] += w[g] * src[e * 64];
+      for (int i = 0; i < CS; ++i) f[i] += w[g] * src[i * 64];
     }
+    // flat index 16*dt + 4*q4 + r holds dim 32*dt + 8*q4 + 4*h2 + r
+    float* orow = a.out + (static_cast<long>(tq) * a.Hq + hq) * kDh + 4 * h2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<float4*>(orow + 32 * dt + 8 * i) =
+    for (int i = 0; i < CS / 4; ++i) {
+      const int fl = grp * CS + 4 * i;
+      *reinterpret_cast<float4*>(orow + 32 * (fl / 16) + 2 * (fl % 16)) =
           make_float4(f[4 * i] * inv, f[4 * i + 1] * inv, f[4 * i + 2] * inv, f[4 * i + 3] * inv);
-  }
+    }
   }
   };  // run_block
 
   // Heaviest blocks first; paired: the heavy block n-1-i, then (after a barrier that frees
   // the merge area) the light block i, so every workgroup has about the same key count.
   run_block(a.n_tblocks - 1 - wi);
-  if (a.paired && wi < a.n_tblocks - 1 - wi) {
+  if (RW > 1 && a.paired && wi < a.n_tblocks - 1 - wi) {  // RW = 1 grids are never paired
     __syncthreads();
     run_block(wi);
   }
@@ -578,8 +729,10 @@ int launch_rw(const PrefillArgs& args, int rw, hipStream_t stream) {
   const dim3 grid(n_work * args.Hkv);
   if (rw == 4)
     hipLaunchKernelGGL((gqa_prefill_kernel<G, PRECISE, 4>), grid, dim3(kThreads), 0, stream, args);
-  else
+  else if (rw == 2)
     hipLaunchKernelGGL((gqa_prefill_kernel<G, PRECISE, 2>), grid, dim3(kThreads), 0, stream, args);
+  else
+    hipLaunchKernelGGL((gqa_prefill_kernel<G, PRECISE, 1>), grid, dim3(kThreads), 0, stream, args);
   return check_launch("gqa_prefill_kernel");
 }
 
@@ -588,14 +741,20 @@ int launch_g(PrefillArgs& args, bool precise, hipStream_t stream) {
   // 128 query rows per K/V tile when that still gives every CU two workgroups (heaviest-
   // first dispatch needs the second one to even out the causal triangle); measured on
   // MI355X: RW = 2 is faster at 2048 tokens x 8 kv heads, RW = 4 at 4096.
-  const int cus = device_cu_count();
+  // Prompts too short to give every CU an RW = 2 workgroup take RW = 1 (8 one-wave key
+  // groups): twice the workgroups, half the rounds per workgroup.
+  const int cus_q = device_cu_count();
+  const int cus = cus_q > 0 ? cus_q : 256;
   const int blocks4 = (args.Tq + 4 * (32 / G) - 1) / (4 * (32 / G));
-  const int rw = static_cast<long>(blocks4) * args.Hkv >= 2L * (cus > 0 ? cus : 256) ? 4 : 2;
+  const int blocks2 = (args.Tq + 2 * (32 / G) - 1) / (2 * (32 / G));
+  const int rw = static_cast<long>(blocks4) * args.Hkv >= 2L * cus ? 4
+                 : static_cast<long>(blocks2) * args.Hkv < cus     ? 1
+                                                                    : 2;
   const int BT = rw * (32 / G);
   args.n_tblocks = (args.Tq + BT - 1) / BT;
   // Pairs of blocks (heavy n-1-i with light i) per workgroup once there are at least two
   // blocks per CU: one workgroup per CU instead of two back to back, and one prologue less.
-  args.paired = static_cast<long>(args.n_tblocks) * args.Hkv >= 2L * (cus > 0 ? cus : 256);
+  args.paired = rw > 1 && static_cast<long>(args.n_tblocks) * args.Hkv >= 2L * cus;
   return precise ? launch_rw<G, true>(args, rw, stream) : launch_rw<G, false>(args, rw, stream);
 }
 
