@@ -180,6 +180,8 @@ constexpr int kVRowH = 64 + 32;  // row-major V tile row (halves): 192 bytes, so
                                  // of a half-wave's transposing read start 48 banks apart
 constexpr int kRtRow = 64 + 2;   // R^T row (floats): the diagonal band reads [c][jl - c + 31]
                                  // then fall on distinct banks across the 32 columns
+constexpr int kStRow = 64 + 8;   // staged K / P / q row (halves): 144 bytes, so the A-fragment
+                                 // reads of 16 lanes (rows r, 16 bytes each) hit distinct banks
 
 __device__ __forceinline__ f16x8_t as_f16x8(uint4 u) { return __builtin_bit_cast(f16x8_t, u); }
 
@@ -240,12 +242,20 @@ struct RelPosArgs {
 
 template <typename IN>
 __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs a) {
-  __shared__ __align__(16) uint16_t v_lds[kRpWaves][32][kVRowH];
-  // R^T during the key loop, then the waves' partial outputs [wave][dim][query] for the merge
-  __shared__ float rt_lds[kRpWaves][32][kRtRow];
+  // Each wave's LDS area holds, per key tile, first the tile's K rows and P window (row-major,
+  // padded; the MFMA A fragments are read back from them), then the V tile and R^T; after the
+  // key loop its R^T part holds the wave's partial output [dim][query] for the merge.  Before
+  // the loop the workgroup's (q + u), (q + v) rows are staged at the start of the areas.
+  constexpr int kVBytes = 32 * kVRowH * 2;
+  constexpr int kWaveBytes = kVBytes + 32 * kRtRow * 4;
+  static_assert((32 + 64) * kStRow * 2 <= kWaveBytes, "K / P staging fits a wave's area");
+  static_assert(2 * 32 * kStRow * 2 <= kRpWaves * kWaveBytes, "q staging fits");
+  static_assert(kRpDk * 33 * 4 <= kWaveBytes - kVBytes, "the merge area fits a wave's R^T area");
+  __shared__ __align__(16) unsigned char lds[kRpWaves * kWaveBytes];
   __shared__ float mo_lds[kRpWaves][2][32];
-  static_assert(kRpDk * 33 <= 32 * kRtRow, "the merge area fits a wave's R^T area");
-  auto o_lds = [&](int w, int d, int c) -> float& { return (&rt_lds[w][0][0])[d * 33 + c]; };
+  auto o_lds = [&](int w, int d, int c) -> float& {
+    return reinterpret_cast<float*>(lds + w * kWaveBytes + kVBytes)[d * 33 + c];
+  };
 
   const int h = blockIdx.x % a.H;
   const int i0 = (blockIdx.x / a.H) * 32;
@@ -258,25 +268,44 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
   const IN* vp = static_cast<const IN*>(a.v);
   const IN* pp = static_cast<const IN*>(a.p);
 
-  // (q_i + u) and (q_i + v) of this lane's query column, B operand per 16-dim k-step
+  unsigned char* wl = lds + wave * kWaveBytes;
+  uint16_t* const kst = reinterpret_cast<uint16_t*>(wl);  // staged K rows [32][kStRow]
+  uint16_t* const pst = kst + 32 * kStRow;                 // staged P window [64][kStRow]
+  uint16_t* const vt = reinterpret_cast<uint16_t*>(wl);   // V tile [32][kVRowH]
+  float* const rt = reinterpret_cast<float*>(wl + kVBytes);  // R^T [32][kRtRow]
+
+  // (q_i + u) and (q_i + v) of the workgroup's 32 queries, formed once with row-contiguous
+  // loads (8 lanes per row), staged in LDS ([2][32][kStRow]), and read back as this lane's B
+  // operand per 16-dim k-step.  (A lane per query row, in every wave, touched a cache line
+  // per lane and load.)
   const int qi = i0 + col;
   const bool q_ok = qi < T;
   uint4 qu[4], qv[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int d0 = 16 * ks + 8 * h2;
-    if (!q_ok) {
-      qu[ks] = qv[ks] = make_uint4(0, 0, 0, 0);
-      continue;
-    }
-    float x[8];
-    load8_f(qp + qi * rs + h * kRpDk + d0, x);
-    const float* ub = a.u + h * kRpDk + d0;
-    const float* vb = a.vb + h * kRpDk + d0;
-    qu[ks] = make_uint4(pack_h2(x[0] + ub[0], x[1] + ub[1]), pack_h2(x[2] + ub[2], x[3] + ub[3]),
+  {
+    uint16_t* qst = reinterpret_cast<uint16_t*>(lds);
+    for (int it = tid; it < 32 * 8; it += 64 * kRpWaves) {
+      const int c = it >> 3, d0 = 8 * (it & 7);
+      uint4 hu = make_uint4(0, 0, 0, 0), hv = hu;
+      if (i0 + c < T) {
+        float x[8];
+        load8_f(qp + (i0 + c) * rs + h * kRpDk + d0, x);
+        const float* ub = a.u + h * kRpDk + d0;
+        const float* vb = a.vb + h * kRpDk + d0;
+        hu = make_uint4(pack_h2(x[0] + ub[0], x[1] + ub[1]), pack_h2(x[2] + ub[2], x[3] + ub[3]),
                         pack_h2(x[4] + ub[4], x[5] + ub[5]), pack_h2(x[6] + ub[6], x[7] + ub[7]));
-    qv[ks] = make_uint4(pack_h2(x[0] + vb[0], x[1] + vb[1]), pack_h2(x[2] + vb[2], x[3] + vb[3]),
+        hv = make_uint4(pack_h2(x[0] + vb[0], x[1] + vb[1]), pack_h2(x[2] + vb[2], x[3] + vb[3]),
                         pack_h2(x[4] + vb[4], x[5] + vb[5]), pack_h2(x[6] + vb[6], x[7] + vb[7]));
+      }
+      *reinterpret_cast<uint4*>(qst + c * kStRow + d0) = hu;
+      *reinterpret_cast<uint4*>(qst + (32 + c) * kStRow + d0) = hv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      qu[ks] = *reinterpret_cast<const uint4*>(qst + col * kStRow + 16 * ks + 8 * h2);
+      qv[ks] = *reinterpret_cast<const uint4*>(qst + (32 + col) * kStRow + 16 * ks + 8 * h2);
+    }
+    __syncthreads();  // the tiles below overwrite the staging area
   }
 
   f32x16_t o[2];
@@ -288,35 +317,31 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
   const int n_tiles = (a.valid + 31) / 32;
   const int P = 2 * T - 1;
 
-  // One tile's global operands: V rows (for the V LDS copy), K and the two P windows in
-  // MFMA A layout (zeros outside [0, T) / [0, P)).  The next tile's operands are loaded
-  // before the current one is processed.
+  // One tile's global operands, row-contiguous (8 lanes per 128-byte row): V and K rows
+  // j0 .. j0+31 and the P window base .. base+63 (zeros outside [0, T) / [0, P)).  The next
+  // tile's operands are loaded before the current one is processed.
   struct Tile {
-    uint4 v[4], k[4], p0[4], p1[4];
+    uint4 v[4], k[4], p[8];
   };
   const int dcv = lane & 7, rv = lane >> 3;
   auto load_tile = [&](Tile& t, int n) {
     const int j0 = 32 * n;
+    const int base = T - 1 - (i0 + 31) + j0;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int j = j0 + 8 * it + rv;
       t.v[it] = j < T ? load8_h(vp + j * rs + h * kRpDk + 8 * dcv) : make_uint4(0, 0, 0, 0);
+      t.k[it] = j < T ? load8_h(kp + j * rs + h * kRpDk + 8 * dcv) : make_uint4(0, 0, 0, 0);
     }
-    const int jk = j0 + col;
-    const int base = T - 1 - (i0 + 31) + j0;
-    const int pr0 = base + col, pr1 = base + 32 + col;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int d0 = 16 * ks + 8 * h2;
-      t.k[ks] = jk < T ? load8_h(kp + jk * rs + h * kRpDk + d0) : make_uint4(0, 0, 0, 0);
-      t.p0[ks] = (pr0 >= 0 && pr0 < P) ? load8_h(pp + static_cast<long>(pr0) * rs + h * kRpDk + d0)
-                                      : make_uint4(0, 0, 0, 0);
-      t.p1[ks] = (pr1 >= 0 && pr1 < P) ? load8_h(pp + static_cast<long>(pr1) * rs + h * kRpDk + d0)
-                                      : make_uint4(0, 0, 0, 0);
+    for (int it = 0; it < 8; ++it) {
+      const int pr = base + 8 * it + rv;
+      t.p[it] = (pr >= 0 && pr < P) ? load8_h(pp + static_cast<long>(pr) * rs + h * kRpDk + 8 * dcv)
+                                    : make_uint4(0, 0, 0, 0);
     }
   };
   const int tg = lane >> 4, ts = lane & 15;
-  const uint16_t* vsrc0 = &v_lds[wave][4 * (tg >> 1) + (ts >> 2)][16 * (tg & 1) + 4 * (ts & 3)];
+  const uint16_t* vsrc0 = vt + (4 * (tg >> 1) + (ts >> 2)) * kVRowH + 16 * (tg & 1) + 4 * (ts & 3);
   // tile n + W's operands are in flight while tile n is processed
   Tile cur, nxt;
   if (wave < n_tiles) load_tile(cur, wave);
@@ -324,27 +349,45 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
     if (n + kRpWaves < n_tiles) load_tile(nxt, n + kRpWaves);
     const int j0 = 32 * n;
     wave_lds_sync();  // the previous tile's LDS reads precede this tile's writes
+    // K rows and the P window -> wave-private LDS; MFMA A fragments (row j0 + col / base +
+    // col / base + 32 + col, dims 16 ks + 8 h2) read back conflict-free
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+      *reinterpret_cast<uint4*>(kst + (8 * it + rv) * kStRow + 8 * dcv) = cur.k[it];
+#pragma unroll
+    for (int it = 0; it < 8; ++it)
+      *reinterpret_cast<uint4*>(pst + (8 * it + rv) * kStRow + 8 * dcv) = cur.p[it];
+    wave_lds_sync();
+    uint4 kf[4], pf0[4], pf1[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int d0 = 16 * ks + 8 * h2;
+      kf[ks] = *reinterpret_cast<const uint4*>(kst + col * kStRow + d0);
+      pf0[ks] = *reinterpret_cast<const uint4*>(pst + col * kStRow + d0);
+      pf1[ks] = *reinterpret_cast<const uint4*>(pst + (32 + col) * kStRow + d0);
+    }
+    wave_lds_sync();  // the fragments are read before V and R^T overwrite the staging
     // V tile -> wave-private LDS, row-major (one 16-byte store per row piece); the PV
     // operand V^T is read back with transposing reads
 #pragma unroll
     for (int it = 0; it < 4; ++it)
-      *reinterpret_cast<uint4*>(&v_lds[wave][8 * it + rv][8 * dcv]) = cur.v[it];
+      *reinterpret_cast<uint4*>(vt + (8 * it + rv) * kVRowH + 8 * dcv) = cur.v[it];
     // AC^T and R = P_window (q + v)^T
     f32x16_t s, r0, r1;
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[e] = r0[e] = r1[e] = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(cur.k[ks]), as_f16x8(qu[ks]), s, 0, 0, 0);
-      r0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(cur.p0[ks]), as_f16x8(qv[ks]), r0, 0, 0, 0);
-      r1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(cur.p1[ks]), as_f16x8(qv[ks]), r1, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(kf[ks]), as_f16x8(qu[ks]), s, 0, 0, 0);
+      r0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(pf0[ks]), as_f16x8(qv[ks]), r0, 0, 0, 0);
+      r1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(pf1[ks]), as_f16x8(qv[ks]), r1, 0, 0, 0);
     }
     // R^T -> LDS; the lane's accumulator rows are 8i + 4*h2 + j (+32 for r1), column = col
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int rr = 8 * (e >> 2) + 4 * h2 + (e & 3);
-      rt_lds[wave][col][rr] = r0[e];
-      rt_lds[wave][col][32 + rr] = r1[e];
+      rt[col * kRtRow + rr] = r0[e];
+      rt[col * kRtRow + 32 + rr] = r1[e];
     }
     wave_lds_sync();  // R^T and V written by all lanes before any lane reads them
     // scores: (AC + BD) * scale, key mask j >= valid, padding query columns masked
@@ -352,7 +395,7 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
-      const float bd = rt_lds[wave][col][jl - col + 31];
+      const float bd = rt[col * kRtRow + jl - col + 31];
       const float sc = a.uniform ? 0.0f : (s[e] + bd) * a.scale_log2e;
       const float x = (q_ok && j0 + jl < a.valid) ? sc : -INFINITY;
       s[e] = x;
