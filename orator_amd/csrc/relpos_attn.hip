@@ -391,15 +391,29 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
     }
     wave_lds_sync();  // R^T and V written by all lanes before any lane reads them
     // scores: (AC + BD) * scale, key mask j >= valid, padding query columns masked
+    // (the uniform case is decided once per tile: as a per-element select it became a branch
+    // around every band read, 16 serialized LDS round trips)
     float tmax = -INFINITY;
+    if (a.uniform) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
-      const float bd = rt[col * kRtRow + jl - col + 31];
-      const float sc = a.uniform ? 0.0f : (s[e] + bd) * a.scale_log2e;
-      const float x = (q_ok && j0 + jl < a.valid) ? sc : -INFINITY;
-      s[e] = x;
-      tmax = fmaxf(tmax, x);
+      for (int e = 0; e < 16; ++e) {
+        const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
+        const float x = (q_ok && j0 + jl < a.valid) ? 0.0f : -INFINITY;
+        s[e] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    } else {
+      float bd[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        bd[e] = rt[col * kRtRow + 8 * (e >> 2) + 4 * h2 + (e & 3) - col + 31];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
+        const float x = (q_ok && j0 + jl < a.valid) ? (s[e] + bd[e]) * a.scale_log2e : -INFINITY;
+        s[e] = x;
+        tmax = fmaxf(tmax, x);
+      }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float mn = fmaxf(m, tmax);
