@@ -96,13 +96,13 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_bf16_kernel(
 // (AddResidualKernel) into the store.  PAIR computes the fused gate|up projection's rows n and
 // N + n in the same wave and stores silu(gate) * up (the SwiGLU that follows it, :424), N
 // outputs from 2N weight rows.  The per-element arithmetic is the standalone kernels'; only
-// the order of the RMSNorm sum of squares differs.  The first batch of weight loads (U
-// 16-byte chunks per lane and row: U = 4 holds a 2048-wide row, 12 a 6144-wide one) is
-// issued before the row is built, so the prologue hides under the HBM latency; longer rows
-// ping-pong two batches.
+// the order of the RMSNorm sum of squares differs.  The row's loads, then the first batch of
+// weight loads (U 16-byte chunks per lane and row: U = 4 holds a 2048-wide row, 12 a 6144-wide
+// one), are issued before the row is built, so the prologue runs under the weights' HBM
+// latency; longer rows ping-pong two batches.
 template <int MODE, int R, bool ACC, int U, bool PAIR>
-__global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict__ x,
-                                                         const float* __restrict__ aux, float eps,
+__global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const float* aux,
+                                                         float eps,
                                                          const uint16_t* __restrict__ W,
                                                          float* __restrict__ out, int K, int N) {
 #pragma clang fp contract(off)
@@ -122,14 +122,32 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict
     const long row = PAIR && r >= RO ? static_cast<long>(N) + o : o;
     wr[r] = reinterpret_cast<const u32x4_t*>(W + row * K);
   }
+  // The input row (and the RMSNorm gain or the SwiGLU up values) is read into registers
+  // before the first batch of weight loads: loads return in issue order, so the row issued
+  // after the weights would wait out their HBM latency before the prologue could start.
+  constexpr int NX = U == 4 ? 2 : 6;  // float4 per thread held: K <= 2048 / 6144 (then the loop)
+  constexpr bool kAux = MODE == kGemvInRmsNorm || MODE == kGemvInSwiglu;
+  // Both the row and the weights are loaded without branches (indices clamped in range; the
+  // values past the end are never used): a branch per load leaves the wait before the
+  // prologue unable to count the loads in flight, and it then waits for the weights too.
+  float4 xr[NX], ar[NX];
+#pragma unroll
+  for (int i = 0; i < NX; ++i) {
+    const int d = min(4 * tid + 1024 * i, K - 4);
+    xr[i] = *reinterpret_cast<const float4*>(x + d);
+    if constexpr (kAux) ar[i] = *reinterpret_cast<const float4*>(aux + d);
+  }
+
+  // the row's loads go out before the weights' (x and aux are not __restrict__, so this
+  // fence also keeps the compiler from sinking them to their uses)
+  asm volatile("" ::: "memory");
   u32x4_t A[U][R], Bb[U][R];
   auto load = [&](u32x4_t(&dst)[U][R], int base) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = base + 64 * u + lane;
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-        dst[u][r] = c < nchunk ? __builtin_nontemporal_load(wr[r] + c) : u32x4_t{0, 0, 0, 0};
+      for (int r = 0; r < R; ++r) dst[u][r] = __builtin_nontemporal_load(wr[r] + min(c, nchunk - 1));
     }
   };
   load(A, 0);
@@ -137,7 +155,18 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict
   // ---- the bf16 input row, in LDS ----
   if constexpr (MODE == kGemvInRmsNorm) {
     float local = 0.0f;
-    for (int d = 4 * tid; d < K; d += 1024) {
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const int d = 4 * tid + 1024 * i;
+      if (d < K) {
+        const float4 v = xr[i];
+        local += v.x * v.x;
+        local += v.y * v.y;
+        local += v.z * v.z;
+        local += v.w * v.w;
+      }
+    }
+    for (int d = 4 * tid + 1024 * NX; d < K; d += 1024) {
       const float4 v = *reinterpret_cast<const float4*>(x + d);
       local += v.x * v.x;
       local += v.y * v.y;
@@ -150,18 +179,19 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict
     const float sum = (red[0] + red[1]) + (red[2] + red[3]);
     const float ms = sum / static_cast<float>(K) + eps;
     const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
-    for (int d = 4 * tid; d < K; d += 1024) {
-      const float4 v = *reinterpret_cast<const float4*>(x + d);
-      const float4 g = *reinterpret_cast<const float4*>(aux + d);
+    auto put = [&](int d, float4 v, float4 g) {
       *reinterpret_cast<uint2*>(xs + d) =
           make_uint2(pack_bf16x2(v.x * inv * g.x, v.y * inv * g.y),
                      pack_bf16x2(v.z * inv * g.z, v.w * inv * g.w));
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < NX; ++i)
+      if (4 * tid + 1024 * i < K) put(4 * tid + 1024 * i, xr[i], ar[i]);
+    for (int d = 4 * tid + 1024 * NX; d < K; d += 1024)
+      put(d, *reinterpret_cast<const float4*>(x + d), *reinterpret_cast<const float4*>(aux + d));
   } else {
-    for (int d = 4 * tid; d < K; d += 1024) {
-      const float4 v = *reinterpret_cast<const float4*>(x + d);
+    auto put = [&](int d, float4 v, float4 u) {
       if constexpr (MODE == kGemvInSwiglu) {
-        const float4 u = *reinterpret_cast<const float4*>(aux + d);
         *reinterpret_cast<uint2*>(xs + d) =
             make_uint2(pack_bf16x2((v.x / (1.0f + expf(-v.x))) * u.x,
                                    (v.y / (1.0f + expf(-v.y))) * u.y),
@@ -171,7 +201,13 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* __restrict
         *reinterpret_cast<uint2*>(xs + d) =
             make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
       }
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < NX; ++i)
+      if (4 * tid + 1024 * i < K) put(4 * tid + 1024 * i, xr[i], ar[i]);
+    for (int d = 4 * tid + 1024 * NX; d < K; d += 1024)
+      put(d, *reinterpret_cast<const float4*>(x + d),
+          kAux ? *reinterpret_cast<const float4*>(aux + d) : make_float4(0.0f, 0.0f, 0.0f, 0.0f));
   }
   lds_barrier();
 
