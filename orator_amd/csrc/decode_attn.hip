@@ -117,6 +117,9 @@ __device__ __forceinline__ int stream_key0(const DecodeArgs& a, int b) {
 // (capacity - 1 at most) and depend on nothing loaded, so the two reads go out together at
 // entry; a row past the stream's keys is never dereferenced (the chunk loads clamp to the
 // last valid key).  Called with wave-uniform arguments: no workgroup-wide table, no barrier.
+// A readable zero word: the address the entry load of a lane uses when its value is not needed.
+__device__ int g_decode_zero[1] = {0};  // never written
+
 __device__ __forceinline__ void chunk_rows(const DecodeArgs& a, int b, int key0, int c, long& r0,
                                            long& r1) {
   const int lim = a.capacity - 1;
@@ -364,12 +367,31 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: wave-level branches
-  // the stream's position and the pool rows of the wave's first chunk (keys w0, w0 + 16):
-  // independent uniform loads, issued together before anything else
-  const int pos_b = a.pos_mode == 0 ? a.pos[b] : 0;
+  // The stream's position (lane 0) and the page-table entries of the wave's first chunk (keys
+  // w0, w0 + 16; lanes 1, 2) in one vector load, one wait: as separate uniform loads behind
+  // the branches for absent arrays, each got a wait of its own before the next was issued.
+  // Table indices are clamped into the table (capacity - 1 at most).
+  const int lim = a.capacity - 1;
+  const int wj0 = min(t0 + wave * TPW, lim) & ~15, wj1 = min(t0 + wave * TPW + 16, lim) & ~15;
+  const bool paged = a.page_table != nullptr;
+  const int* ptb = a.page_table + static_cast<long>(b) * a.max_pages;
+  const int* esrc = g_decode_zero;
+  if (lane == 0 && a.pos_mode == 0) esrc = a.pos + b;
+  if (lane == 1 && paged) esrc = ptb + (wj0 >> a.page_shift);
+  if (lane == 2 && paged) esrc = ptb + (wj1 >> a.page_shift);
+  const int eld = *esrc;
+  const int pos_b = a.pos_mode == 0 ? __builtin_amdgcn_readlane(eld, 0) : 0;
   const int key0 = stream_key0(a, b);
   long wr0, wr1;
-  chunk_rows(a, b, key0, t0 + wave * TPW, wr0, wr1);
+  if (paged) {
+    const int msk = (1 << a.page_shift) - 1;
+    // long arithmetic: an unmapped page (< 0) yields a negative row, never a wrapped one
+    wr0 = static_cast<long>(__builtin_amdgcn_readlane(eld, 1)) * (1L << a.page_shift) + (wj0 & msk);
+    wr1 = static_cast<long>(__builtin_amdgcn_readlane(eld, 2)) * (1L << a.page_shift) + (wj1 & msk);
+  } else {
+    wr0 = wj0 + key0;
+    wr1 = wj1 + key0;
+  }
   int S = stream_keys(a, b, pos_b);
   if (S <= 0) {  // no keys: the reference's 1/sum guard yields zeros
     if (split == 0)
