@@ -602,7 +602,14 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
   };
   Batch A, Bb;
   load(A, 0);
-  const int S = stream_keys(a, b, a.pos_mode == 0 ? a.pos[b] : 0);
+  // the stream's position, read by lane 0 of each wave in a vector load that every thread
+  // issues (the others read a zero word): as a uniform load behind the branch for an absent
+  // position array, it and the pointer it needs cost two round trips before the batch's row
+  // loads
+  const int* psrc = ((d & 63) == 0 && a.pos_mode == 0) ? a.pos + b : g_decode_zero;
+  const int pos_ld = *psrc;
+  asm volatile("" ::: "memory");  // keeps the batch's loads here, ahead of the early return
+  const int S = stream_keys(a, b, a.pos_mode == 0 ? __builtin_amdgcn_readlane(pos_ld, 0) : 0);
   const int n_splits = (S + split_len - 1) / split_len;
   if (n_splits <= 1) return;  // written directly by the split kernel
   auto fold = [&](const Batch& x, int s0) {
