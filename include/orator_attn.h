@@ -367,8 +367,9 @@ int orator_relpos_attention(const float* q, const float* k, const float* v, cons
                             int H, int Dk, int valid_len, float scale, void* stream);
 
 /* Same attention core, fused on fp16 MFMA (one launch, no [H,T,2T-1] BD matrix): inputs
- * fp16 bits (in_f16 = 1) or fp32 rounded to fp16 on load (in_f16 = 0); biases and output
- * fp32; Dk = 64.  Max abs error ~1e-3 on unit-scale outputs (fp16 operands, fp32 accumulate). */
+ * fp16 bits (in_f16 = 1), fp32 rounded to fp16 on load (in_f16 = 0), or q fp32 and k, v, p
+ * fp16 bits (in_f16 = 2: the same result as in_f16 = 0 on the fp32 rows k, v, p round to);
+ * biases and output fp32; Dk = 64.  Max abs error ~1e-3 on unit-scale outputs (fp16 operands, fp32 accumulate). */
 int orator_relpos_attention_fast(const void* q, const void* k, const void* v, const void* p,
                                  const float* pos_bias_u, const float* pos_bias_v, float* out,
                                  int T, int H, int Dk, int valid_len, float scale, int in_f16,

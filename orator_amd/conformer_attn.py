@@ -21,13 +21,15 @@ def RelPosAttention(q, k, v, p, pos_bias_u, pos_bias_v, out, T: int, H: int, Dk:
 
 
 def RelPosAttentionFast(q, k, v, p, pos_bias_u, pos_bias_v, out, T: int, H: int, Dk: int,
-                        valid_len: int, scale: float | None = None, in_f16: bool = True,
+                        valid_len: int, scale: float | None = None, in_f16: bool | int = True,
                         stream=None) -> None:
-    """Fused fp16-MFMA form of RelPosAttention (inputs fp16 bits, or fp32 if in_f16=False)."""
+    """Fused fp16-MFMA form of RelPosAttention: inputs fp16 bits (in_f16 True or 1), fp32
+    (False or 0), or q fp32 with k, v, p fp16 bits (2)."""
     if scale is None:
         scale = 1.0 / math.sqrt(Dk)
+    mode = 2 if in_f16 == 2 and not isinstance(in_f16, bool) else int(bool(in_f16))
     call("orator_relpos_attention_fast", ptr(q), ptr(k), ptr(v), ptr(p), ptr(pos_bias_u),
-         ptr(pos_bias_v), ptr(out), T, H, Dk, valid_len, scale, int(bool(in_f16)), _sh(stream))
+         ptr(pos_bias_v), ptr(out), T, H, Dk, valid_len, scale, mode, _sh(stream))
 
 
 def BuildPosEmb(T: int, d_model: int) -> np.ndarray:

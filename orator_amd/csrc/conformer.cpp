@@ -75,11 +75,14 @@ struct Conformer {
     return launch_glu_mask(pw1, glu, T, D, valid, s);
   }
 
-  int qkv(int T, hipStream_t s) {
+  // q, k, v projections in one launch; with the fused core (f16_kv) k and v are written as
+  // the fp16 values that core would round them to on load, and q stays fp32 (q + u and q + v
+  // are formed in fp32 before their one rounding)
+  int qkv(int T, bool f16_kv, hipStream_t s) {
     const float* const W[3] = {w.q_w, w.k_w, w.v_w};
     const float* const b[3] = {w.q_b, w.k_b, w.v_b};
-    float* const out[3] = {q, k, v};
-    return launch_sgemm_group3(ln, W, b, out, T, D, D, s);
+    void* const out[3] = {q, k, v};
+    return launch_sgemm_group3(ln, W, b, out, T, D, D, f16_kv ? 6 : 0, s);
   }
 
   // x += 0.5 FFN(ln) (ln = this block's LayerNorm of x), then next_out = the next block's
@@ -103,13 +106,14 @@ struct Conformer {
     (rc = launch_layer_norm(x, w.norm_ff1_w, w.norm_ff1_b, ln, T, D, kEps, s)) ||
         (rc = ffn(x, T, w.ff1_w1, w.ff1_b1, w.ff1_w2, w.ff1_b2, w.norm_att_w, w.norm_att_b, ln, s));
     if (rc) return rc;
-    // MHSA
-    (rc = qkv(T, s)) ||
-        (rc = linear(pos_emb, w.pos_w, nullptr, p, P, D, D, 0, s));
+    // MHSA (the fused core reads k, v and p as fp16: half the bytes written and read)
+    (rc = qkv(T, attn_mode == 1, s)) ||
+        (rc = attn_mode == 1 ? launch_sgemm_f16_out(pos_emb, w.pos_w, p, P, D, D, s)
+                             : linear(pos_emb, w.pos_w, nullptr, p, P, D, D, 0, s));
     if (rc) return rc;
     rc = attn_mode == 1
              ? orator_relpos_attention_fast(q, k, v, p, w.pos_bias_u, w.pos_bias_v, ctx, T, H, Dk,
-                                            valid, scale, 0, s)
+                                            valid, scale, 2, s)
              : orator_relpos_attention(q, k, v, p, w.pos_bias_u, w.pos_bias_v, ctx, T, H, Dk,
                                        valid, scale, s);
     (rc) || (rc = launch_sgemm_residual_ln(ctx, w.out_w, w.out_b, x, T, D, D, 1.0f, w.norm_conv_w,

@@ -170,7 +170,14 @@ int launch_sgemm_glu(const float* in, const float* W, const float* bias, float* 
                      int C, int valid, hipStream_t stream);
 
 // out[g] = in W[g]^T + bias[g] for g = 0..2: three products of one shape sharing `in`, one launch.
+// out[g] is fp32, or fp16 (each fp32 result rounded to nearest even) where bit g of h16_mask is set.
 int launch_sgemm_group3(const float* in, const float* const W[3], const float* const bias[3],
-                        float* const out[3], int M, int K, int N, hipStream_t stream);
+                        void* const out[3], int M, int K, int N, int h16_mask,
+                        hipStream_t stream);
+
+// out[M][N] = fp16(in W^T), the fp32 product rounded to nearest even once per element (never
+// split over K): the values an fp16 consumer would round from launch_sgemm's fp32 output.
+int launch_sgemm_f16_out(const float* in, const float* W, void* out, int M, int K, int N,
+                         hipStream_t stream);
 
 }  // namespace orator_hip

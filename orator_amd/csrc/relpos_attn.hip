@@ -240,7 +240,8 @@ struct RelPosArgs {
   int uniform;  // every key masked (valid_len <= 0): all T scores equal, softmax = mean of V
 };
 
-template <typename IN>
+// QT: the q rows' type; IN: the k, v and p rows' type (fp32 or fp16 bits).
+template <typename QT, typename IN>
 __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs a) {
   // Each wave's LDS area holds, per key tile, first the tile's K rows and P window (row-major,
   // padded; the MFMA A fragments are read back from them), then the V tile and R^T; after the
@@ -263,7 +264,7 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
   const int col = lane & 31, h2 = lane >> 5;
   const int T = a.T, H = a.H;
   const long rs = static_cast<long>(H) * kRpDk;  // elements per token row
-  const IN* qp = static_cast<const IN*>(a.q);
+  const QT* qp = static_cast<const QT*>(a.q);
   const IN* kp = static_cast<const IN*>(a.k);
   const IN* vp = static_cast<const IN*>(a.v);
   const IN* pp = static_cast<const IN*>(a.p);
@@ -499,6 +500,8 @@ int orator_relpos_attention_fast(const void* q, const void* k, const void* v, co
   if (!q || !k || !v || !p || !pos_bias_u || !pos_bias_v || !out)
     return fail(ORATOR_ERR_INVALID, "relpos_attention_fast: null pointer");
   if (Dk != kRpDk) return fail(ORATOR_ERR_UNSUPPORTED, "relpos_attention_fast: Dk must be 64");
+  if (in_f16 < 0 || in_f16 > 2)
+    return fail(ORATOR_ERR_INVALID, "relpos_attention_fast: in_f16 must be 0, 1 or 2");
   // The reference masks keys >= valid_len with a finite -1e30 (conformer_layer.cu:140-143):
   // with no valid key every score is the same and the softmax averages V over all T keys.
   const bool none_valid = valid_len <= 0;
@@ -506,12 +509,15 @@ int orator_relpos_attention_fast(const void* q, const void* k, const void* v, co
                   none_valid ? T : (valid_len > T ? T : valid_len), scale * 1.4426950408889634f,
                   none_valid ? 1 : 0};
   const dim3 grid(((T + 31) / 32) * H);
-  if (in_f16)
-    hipLaunchKernelGGL(relpos_fused_kernel<_Float16>, grid, dim3(64 * kRpWaves), 0,
-                       static_cast<hipStream_t>(stream), args);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (in_f16 == 1)
+    hipLaunchKernelGGL((relpos_fused_kernel<_Float16, _Float16>), grid, dim3(64 * kRpWaves), 0, s,
+                       args);
+  else if (in_f16 == 2)
+    hipLaunchKernelGGL((relpos_fused_kernel<float, _Float16>), grid, dim3(64 * kRpWaves), 0, s,
+                       args);
   else
-    hipLaunchKernelGGL(relpos_fused_kernel<float>, grid, dim3(64 * kRpWaves), 0,
-                       static_cast<hipStream_t>(stream), args);
+    hipLaunchKernelGGL((relpos_fused_kernel<float, float>), grid, dim3(64 * kRpWaves), 0, s, args);
   return check_launch("relpos_fused_kernel");
 }
 

@@ -71,6 +71,9 @@ struct SgemmArgs {
   const float* ln_b;
   float* ln_out;
   float ln_eps;
+  // fp16 outputs: bit z set stores problem z's output (group products; bit 0 otherwise) as
+  // fp16, each value rounded to nearest even once; unsplit products without residual only.
+  int h16;
 };
 
 // Epilogues: raw split-K partials, out = acc (no bias, act 0), and through LDS out =
@@ -214,6 +217,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
   // of the block.  Plain stores and partials go straight out (nothing is loaded, so no store
   // waits); bias / activation go through LDS with the bias loaded before the first store
   // (stores count against the same wait counter as loads).
+  const bool h16 = (a.h16 >> (a.group ? batch : 0)) & 1;
   if constexpr (EPI == kSEpiPartial || EPI == kSEpiStore) {
     float* C = EPI == kSEpiPartial
                    ? a.part + (static_cast<long>(split) * a.batch + batch) * M * N
@@ -227,7 +231,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-          if (m < M) C[static_cast<long>(m) * N + n] = acc[i][j][e];
+          if (m >= M) continue;
+          if (EPI == kSEpiStore && h16)
+            reinterpret_cast<_Float16*>(C)[static_cast<long>(m) * N + n] =
+                static_cast<_Float16>(acc[i][j][e]);
+          else
+            C[static_cast<long>(m) * N + n] = acc[i][j][e];
         }
     }
     return;
@@ -315,6 +324,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
       if (a.residual) v[q] = fmaf(a.res_scale, v[q], old[p][q]);
     }
     if (m >= M) continue;
+    if (h16) {
+      _Float16* dst = reinterpret_cast<_Float16*>(C) + static_cast<long>(m) * N + n;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n + q < N) dst[q] = static_cast<_Float16>(v[q]);
+      continue;
+    }
     float* dst = C + static_cast<long>(m) * N + n;
     if (vec_out && n + 3 < N) {
       *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
@@ -474,7 +490,7 @@ int run_sgemm(SgemmArgs a, int batch, hipStream_t stream) {
   const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const long t = static_cast<long>((M + 63) / 64) * ((N + 63) / 64) * batch;
   int splits = 1;
-  if (2 * t <= cus && K >= 512 && !a.group) {
+  if (2 * t <= cus && K >= 512 && !a.group && !a.h16) {
     // the split count with the least work per CU in whole rounds, ceil(t s / cus) / s (ties to
     // fewer splits), K / 256 and 8 at most: 717 x 2048 -> 512 (96 tiles) takes 8 splits (768
     // workgroups, 3 rounds of 1/8): 24.7-25.9 us, against 25.9-27.4 with 5 and 27.5-28.9 with 6
@@ -599,7 +615,8 @@ int launch_sgemm_glu(const float* in, const float* W, const float* bias, float* 
 }
 
 int launch_sgemm_group3(const float* in, const float* const W[3], const float* const bias[3],
-                        float* const out[3], int M, int K, int N, hipStream_t stream) {
+                        void* const out[3], int M, int K, int N, int h16_mask,
+                        hipStream_t stream) {
   if (M <= 0 || N <= 0 || K <= 0) return ORATOR_OK;
   if (!in) return fail(ORATOR_ERR_INVALID, "sgemm: null pointer");
   SgemmArgs a{};
@@ -608,17 +625,35 @@ int launch_sgemm_group3(const float* in, const float* const W[3], const float* c
   a.K = K;
   a.N = N;
   a.group = 3;
+  a.h16 = h16_mask & 7;
   uintptr_t align = reinterpret_cast<uintptr_t>(in);
   for (int g = 0; g < 3; ++g) {
     if (!W[g] || !out[g]) return fail(ORATOR_ERR_INVALID, "sgemm: null pointer");
     a.Wg[g] = W[g];
     a.bg[g] = bias[g];
-    a.og[g] = out[g];
+    a.og[g] = static_cast<float*>(out[g]);
     align |= reinterpret_cast<uintptr_t>(W[g]);
   }
   a.W = a.Wg[0];
   a.vec = (K % kSK) == 0 && (align & 15) == 0;
   return run_sgemm(a, 3, stream);
+}
+
+int launch_sgemm_f16_out(const float* in, const float* W, void* out, int M, int K, int N,
+                         hipStream_t stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return ORATOR_OK;
+  if (!in || !W || !out) return fail(ORATOR_ERR_INVALID, "sgemm: null pointer");
+  SgemmArgs a{};
+  a.in = in;
+  a.W = W;
+  a.out = static_cast<float*>(out);
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.h16 = 1;
+  a.vec = (K % kSK) == 0 &&
+          ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15) == 0;
+  return run_sgemm(a, 1, stream);
 }
 
 }  // namespace orator_hip

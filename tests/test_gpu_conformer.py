@@ -113,3 +113,23 @@ def test_relpos_fused_vs_oracle(T, valid, in_f16):
     print(f"T={T} valid={valid}: max abs {err:.2e}, fp16 model predicts {predicted:.2e}")
     assert err <= 2e-2
     assert err <= 2.0 * predicted + 2e-5
+
+
+@pytest.mark.parametrize("T,valid", [(717, 529), (33, 20), (70, 0), (1, 1)])
+def test_relpos_fused_mixed_inputs_match_fp32(T, valid):
+    """in_f16 = 2 (q fp32; k, v, p fp16 bits, what the Conformer layer's fused mode feeds) gives
+    bit for bit the in_f16 = 0 result on the fp32 rows those fp16 values round from: both round
+    k, v, p to nearest even once and form q + u, q + v in fp32."""
+    H, Dk = 8, 64
+    r = SplitMix64(T * 29 + valid)
+    q, k, v, p, u, vb = _relpos_inputs(r, T, H, Dk)
+    scale = 1.0 / math.sqrt(Dk)
+    say("relpos fused mixed", T, valid)
+    d32, dmix = empty(q.shape, np.float32), empty(q.shape, np.float32)
+    ca.RelPosAttentionFast(up(q), up(k), up(v), up(p), up(u), up(vb), d32, T, H, Dk, valid,
+                           scale, in_f16=0)
+    ca.RelPosAttentionFast(up(q), *(up(_to_f16_bits(x)) for x in (k, v, p)), up(u), up(vb),
+                           dmix, T, H, Dk, valid, scale, in_f16=2)
+    a, b = down(d32, q.shape), down(dmix, q.shape)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
