@@ -78,7 +78,7 @@ struct SgemmArgs {
 
 // Epilogues: raw split-K partials, out = acc (no bias, act 0), and through LDS out =
 // act(acc + bias) or the residual update out += res_scale * (acc + bias), or the GLU of a
-// tile's value and gate halves.
+// tile's value and gate halves.  out = acc and out = act(acc + bias) may be stored as fp16 (h16).
 constexpr int kSEpiPartial = 0, kSEpiStore = 1, kSEpiAct = 2, kSEpiGlu = 3;
 
 template <int BM, int BN, int WGM, int WGN, int MINW, bool VEC, int EPI>
@@ -217,7 +217,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
   // of the block.  Plain stores and partials go straight out (nothing is loaded, so no store
   // waits); bias / activation go through LDS with the bias loaded before the first store
   // (stores count against the same wait counter as loads).
-  const bool h16 = (a.h16 >> (a.group ? batch : 0)) & 1;
   if constexpr (EPI == kSEpiPartial || EPI == kSEpiStore) {
     float* C = EPI == kSEpiPartial
                    ? a.part + (static_cast<long>(split) * a.batch + batch) * M * N
@@ -232,7 +231,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
         for (int e = 0; e < 16; ++e) {
           const int m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
           if (m >= M) continue;
-          if (EPI == kSEpiStore && h16)
+          if (EPI == kSEpiStore && (a.h16 & 1))  // ungrouped: bit 0
             reinterpret_cast<_Float16*>(C)[static_cast<long>(m) * N + n] =
                 static_cast<_Float16>(acc[i][j][e]);
           else
@@ -293,10 +292,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
   }
   float* C = a.group ? a.og[batch] : a.out + batch * a.s_out;
   const float* bias = a.group ? a.bg[batch] : a.bias;
+  const bool h16 = (a.h16 >> (a.group ? batch : 0)) & 1;
   constexpr int TPRo = BN / 4, RPIo = NT / TPRo, PASSES = BM / RPIo;
   const int orow = tid / TPRo, ocol = 4 * (tid % TPRo);
   const int n = n0 + ocol;
   const bool vec_out = (N % 4) == 0 && ((reinterpret_cast<uintptr_t>(C)) & 15) == 0;
+  const bool vec_h16 = (N % 4) == 0 && ((reinterpret_cast<uintptr_t>(C)) & 7) == 0;
   float bv[4] = {0.f, 0.f, 0.f, 0.f};
   if (bias) {
 #pragma unroll
@@ -326,9 +327,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void sgemm_nt_kernel(SgemmArg
     if (m >= M) continue;
     if (h16) {
       _Float16* dst = reinterpret_cast<_Float16*>(C) + static_cast<long>(m) * N + n;
+      if (vec_h16 && n + 3 < N) {
+        typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+        const h4_t hv = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]),
+                         static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+        *reinterpret_cast<h4_t*>(dst) = hv;
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (n + q < N) dst[q] = static_cast<_Float16>(v[q]);
+        for (int q = 0; q < 4; ++q)
+          if (n + q < N) dst[q] = static_cast<_Float16>(v[q]);
+      }
       continue;
     }
     float* dst = C + static_cast<long>(m) * N + n;
