@@ -27,6 +27,7 @@ int check_launch(const char* what);
 // Slots are independent blocks: kWsGemm holds the split-K partials of the GEMMs, which may run
 // while a caller's slot-0 buffer (e.g. the bf16 cast of a Linear input) is being read.
 constexpr int kWsGemm = 1;
+constexpr int kWsMha = 2;  // key-split partials of the small-head masked MHA
 void* workspace(hipStream_t stream, size_t bytes, int slot = 0);
 // Frees every workspace block of `stream` (all threads, current and retired) after the
 // stream's queued work; for the owner of a stream about to be destroyed.

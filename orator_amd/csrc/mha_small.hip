@@ -8,7 +8,10 @@
 // matrix: one workgroup owns 64 queries of one head, one query per lane; its waves (16 for
 // Dk <= 32, 8 above: 717 queries x 8 heads is only 96 workgroups, so the keys are split
 // finely to occupy the SIMDs) split the keys, each keeps an online softmax (a running max per
-// 8-key block), and the partials are merged in LDS.  K and V rows are wave-uniform, so they arrive through scalar
+// 8-key block), and the partials are merged in LDS.  When those workgroups leave CUs idle,
+// the keys are also split over grid z (Z workgroups per query tile and head): each writes its
+// unnormalised (max, sum, P.V) to a workspace and a second kernel merges the Z partials per
+// (query, head) (717 x 8 heads on 256 CUs: Z = 2, half the keys per workgroup).  K and V rows are wave-uniform, so they arrive through scalar
 // loads and feed the FMAs as scalar operands: the kernel is VALU-bound at ~2 Dk FMAs per
 // (query, key), with no LDS traffic in the key loop.
 #include "common.hpp"
@@ -31,7 +34,9 @@ __global__ __launch_bounds__(kQ * kWaves) void mha_small_kernel(const float* __r
                                                                 const float* __restrict__ k,
                                                                 const float* __restrict__ v,
                                                                 float* __restrict__ out, int T,
-                                                                int H, int valid, float scale) {
+                                                                int H, int valid, float scale,
+                                                                int nsplit,
+                                                                float* __restrict__ ws) {
   __shared__ float part[kWaves][kQ][DK + 2];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -44,8 +49,9 @@ __global__ __launch_bounds__(kQ * kWaves) void mha_small_kernel(const float* __r
   // softmax is uniform over all T keys, which score 0 reproduces.
   const bool uniform = valid <= 0;
   const int nk = uniform ? T : min(valid, T);
-  const int per = ((nk + kWaves - 1) / kWaves + kKB - 1) / kKB * kKB;
-  const int j0 = min(wave * per, nk);
+  const int ranges = nsplit * kWaves;  // key ranges of one query tile: (split z, wave)
+  const int per = ((nk + ranges - 1) / ranges + kKB - 1) / kKB * kKB;
+  const int j0 = min((static_cast<int>(blockIdx.z) * kWaves + wave) * per, nk);
   const int j1 = min(j0 + per, nk);
 
   float qr[DK];
@@ -123,6 +129,15 @@ __global__ __launch_bounds__(kQ * kWaves) void mha_small_kernel(const float* __r
     for (int d = 0; d < DK; ++d) o[d] = fmaf(c, pw[2 + d], o[d]);
   }
   if (i >= T) return;
+  if (nsplit > 1) {
+    // ws[z][h][c][i], c = max, sum, P.V[0..DK): consecutive lanes write consecutive floats
+    float* wp = ws + (static_cast<long>(blockIdx.z) * H + h) * (DK + 2) * T + i;
+    wp[0] = M;
+    wp[T] = L;
+#pragma unroll
+    for (int d = 0; d < DK; ++d) wp[static_cast<long>(2 + d) * T] = o[d];
+    return;
+  }
   const float inv = 1.0f / L;
   float* op = out + i * hs + static_cast<long>(h) * DK;
 #pragma unroll
@@ -131,11 +146,65 @@ __global__ __launch_bounds__(kQ * kWaves) void mha_small_kernel(const float* __r
         make_float4(o[d] * inv, o[d + 1] * inv, o[d + 2] * inv, o[d + 3] * inv);
 }
 
+// out[i][h] = sum_z c_z o_z / sum_z c_z l_z, c_z = exp(m_z - max_z m_z) (0 for a split with no
+// keys, m_z = -inf): the Z key-split partials of one (query, head), one thread each.
 template <int DK>
-void launch(const float* q, const float* k, const float* v, float* out, int T, int H, int valid,
-            float scale, hipStream_t s) {
-  hipLaunchKernelGGL(mha_small_kernel<DK>, dim3((T + kQ - 1) / kQ, H), dim3(kQ * mha_waves<DK>()),
-                     0, s, q, k, v, out, T, H, valid, scale);
+__global__ __launch_bounds__(256) void mha_small_merge_kernel(const float* __restrict__ ws,
+                                                              float* __restrict__ out, int T,
+                                                              int H, int nsplit) {
+  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= static_cast<long>(T) * H) return;
+  const int i = static_cast<int>(idx % T), h = static_cast<int>(idx / T);
+  const long zs = static_cast<long>(H) * (DK + 2) * T;  // floats between splits
+  const float* wp = ws + static_cast<long>(h) * (DK + 2) * T + i;
+  float M = -INFINITY;
+  for (int z = 0; z < nsplit; ++z) M = fmaxf(M, wp[z * zs]);
+  float L = 0.0f, o[DK];
+#pragma unroll
+  for (int d = 0; d < DK; ++d) o[d] = 0.0f;
+  for (int z = 0; z < nsplit; ++z) {
+    const float* pz = wp + z * zs;
+    const float m = pz[0];
+    const float c = m == -INFINITY ? 0.0f : __expf(m - M);
+    L = fmaf(c, pz[T], L);
+#pragma unroll
+    for (int d = 0; d < DK; ++d) o[d] = fmaf(c, pz[static_cast<long>(2 + d) * T], o[d]);
+  }
+  const float inv = 1.0f / L;
+  float* op = out + (static_cast<long>(i) * H + h) * DK;
+#pragma unroll
+  for (int d = 0; d < DK; d += 4)
+    *reinterpret_cast<float4*>(op + d) =
+        make_float4(o[d] * inv, o[d + 1] * inv, o[d + 2] * inv, o[d + 3] * inv);
+}
+
+template <int DK>
+int launch(const float* q, const float* k, const float* v, float* out, int T, int H, int valid,
+           float scale, hipStream_t s) {
+  constexpr int kWaves = mha_waves<DK>();
+  // Key splits over grid z: as many as the CUs take one workgroup each (the merge area holds
+  // a CU's LDS to one workgroup), at most 8, and at least one 8-key block per wave each.
+  const int tiles = (T + kQ - 1) / kQ;
+  const long wgs = static_cast<long>(tiles) * H;
+  const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const int nk = valid <= 0 ? T : (valid < T ? valid : T);
+  long z = std::min<long>(8, cus / wgs);
+  z = std::min<long>(z, nk / (kWaves * kKB));
+  const int nsplit = z > 1 ? static_cast<int>(z) : 1;
+  float* ws = nullptr;
+  if (nsplit > 1) {
+    ws = static_cast<float*>(
+        workspace(s, static_cast<size_t>(nsplit) * H * (DK + 2) * T * sizeof(float), kWsMha));
+    if (!ws) return ORATOR_ERR_HIP;
+  }
+  hipLaunchKernelGGL(mha_small_kernel<DK>, dim3(tiles, H, nsplit), dim3(kQ * kWaves), 0, s, q, k,
+                     v, out, T, H, valid, scale, nsplit, ws);
+  if (nsplit == 1) return check_launch("mha_small_kernel");
+  if (int rc = check_launch("mha_small_kernel")) return rc;
+  hipLaunchKernelGGL(mha_small_merge_kernel<DK>,
+                     dim3(static_cast<unsigned>((static_cast<long>(T) * H + 255) / 256)),
+                     dim3(256), 0, s, ws, out, T, H, nsplit);
+  return check_launch("mha_small_merge_kernel");
 }
 
 }  // namespace
@@ -156,10 +225,9 @@ int orator_masked_mha(const float* q, const float* k, const float* v, float* out
     return fail(ORATOR_ERR_INVALID, "masked_mha: q, k, v, out must be 16-byte aligned");
   if (H > 65535) return fail(ORATOR_ERR_UNSUPPORTED, "masked_mha: at most 65535 heads");
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (Dk == 24) launch<24>(q, k, v, out, T, H, valid_len, scale, s);
-  else if (Dk == 32) launch<32>(q, k, v, out, T, H, valid_len, scale, s);
-  else launch<64>(q, k, v, out, T, H, valid_len, scale, s);
-  return check_launch("mha_small_kernel");
+  if (Dk == 24) return launch<24>(q, k, v, out, T, H, valid_len, scale, s);
+  if (Dk == 32) return launch<32>(q, k, v, out, T, H, valid_len, scale, s);
+  return launch<64>(q, k, v, out, T, H, valid_len, scale, s);
 }
 
 }  // extern "C"

@@ -23,7 +23,8 @@ FLOOR, TOL = 0.05, 1e-4
 @pytest.mark.parametrize("T,H,Dk,valid", [(1, 8, 24, 1), (7, 8, 24, 7), (65, 8, 24, 50),
                                            (717, 8, 24, 717), (717, 8, 24, 600),
                                            (376, 8, 24, 0), (300, 4, 32, 299),
-                                           (200, 8, 64, 1000)])
+                                           (200, 8, 64, 1000), (1024, 1, 24, 1000),
+                                           (2000, 1, 32, 0)])
 def test_masked_mha_vs_oracle(T, H, Dk, valid):
     r = SplitMix64(T * 11 + Dk + valid)
     q, k, v = r.normal((T, H, Dk)), r.normal((T, H, Dk)), r.normal((T, H, Dk))
