@@ -147,12 +147,14 @@ __global__ __launch_bounds__(kQ * kWaves) void mha_small_kernel(const float* __r
 }
 
 // out[i][h] = sum_z c_z o_z / sum_z c_z l_z, c_z = exp(m_z - max_z m_z) (0 for a split with no
-// keys, m_z = -inf): the Z key-split partials of one (query, head), one thread each.
+// keys, m_z = -inf): the Z key-split partials of one (query, head), one thread each; one wave
+// per workgroup, so the ~90 workgroups of T = 717 x 8 heads spread their loads over as many
+// CUs.
 template <int DK>
-__global__ __launch_bounds__(256) void mha_small_merge_kernel(const float* __restrict__ ws,
+__global__ __launch_bounds__(64) void mha_small_merge_kernel(const float* __restrict__ ws,
                                                               float* __restrict__ out, int T,
                                                               int H, int nsplit) {
-  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long idx = static_cast<long>(blockIdx.x) * 64 + threadIdx.x;
   if (idx >= static_cast<long>(T) * H) return;
   const int i = static_cast<int>(idx % T), h = static_cast<int>(idx / T);
   const long zs = static_cast<long>(H) * (DK + 2) * T;  // floats between splits
@@ -202,8 +204,8 @@ int launch(const float* q, const float* k, const float* v, float* out, int T, in
   if (nsplit == 1) return check_launch("mha_small_kernel");
   if (int rc = check_launch("mha_small_kernel")) return rc;
   hipLaunchKernelGGL(mha_small_merge_kernel<DK>,
-                     dim3(static_cast<unsigned>((static_cast<long>(T) * H + 255) / 256)),
-                     dim3(256), 0, s, ws, out, T, H, nsplit);
+                     dim3(static_cast<unsigned>((static_cast<long>(T) * H + 63) / 64)),
+                     dim3(64), 0, s, ws, out, T, H, nsplit);
   return check_launch("mha_small_merge_kernel");
 }
 
