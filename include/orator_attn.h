@@ -68,6 +68,10 @@ int orator_event_elapsed_ms(float* ms, void* start, void* stop);
 /* Pre-sizes the library workspace of `stream` (split-K decode partials, rel-pos fp32
  * intermediates) so that later calls do not allocate, e.g. before hipGraph capture. */
 int orator_workspace_reserve(size_t bytes, void* stream);
+/* Diagnostics (no reference counterpart): the library workspace blocks currently held (current
+ * and retired, every device, stream and thread) and their bytes, after freeing the retired
+ * blocks whose stream work has completed.  Either pointer may be NULL. */
+int orator_workspace_stats(size_t* blocks, size_t* bytes);
 /* Measurement hook (this thread; no reference counterpart): the next decode call records the
  * HIP events `start` before its split kernel, `split_end` after it and `stop` after the split
  * merge, on the launch stream, so the operation and its split kernel can be timed without
@@ -99,7 +103,9 @@ int orator_argmax_banned(const float* logits, int n, int ban0, int ban1, int* ou
  * (Dh 64 / 128 with Hq/Hkv in {1,2,4} run on the split-K kernel, the rest on a generic one). */
 int orator_gqa_attention(const float* q, const float* k, const float* v, float* out, int T, int Hq,
                          int Hkv, int Dh, float scale, int causal);
-/* asr_gemm::F32ToBf16 / Bf16ToF32 (include/model/asr_gemm.h:23-25; src/model/asr_gemm.cu:45-57). */
+/* asr_gemm::F32ToBf16 / Bf16ToF32 (include/model/asr_gemm.h:23-25; src/model/asr_gemm.cu:45-57).
+ * Any n; operands at their natural alignment (16-byte fp32 and 8-byte bf16 addresses take the
+ * 4-wide accesses). */
 int orator_f32_to_bf16(const float* in, uint16_t* out, long n, void* stream);
 int orator_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream);
 
@@ -226,21 +232,25 @@ int orator_masked_mha(const float* q, const float* k, const float* v, float* out
 /* asr_gemm::LinearPre (include/model/asr_gemm.h:33-38, src/model/asr_gemm.cu:175-208):
  * out[M,N] fp32 = act(in[M,K] W[N,K]^T + bias), in and W bf16, fp32 accumulation; act 0 none,
  * 1 exact-erf GELU, 2 ReLU; bias may be NULL.  M == 1 runs a streaming GEMV, M > 1 an MFMA
- * GEMM.  K % 8 == 0, in and W 16-byte aligned. */
+ * GEMM.  Any K >= 1 and any 2-byte aligned in / W, as the reference (asr_gemm.cu:188-214,
+ * gemm.cuh:461-501): K % 8 == 0 with 16-byte aligned in and W takes the 16-byte-load kernels,
+ * anything else the GEMM with element loads (M == 1 included). */
 int orator_linear_pre(const uint16_t* in_bf16, const uint16_t* W_bf16, const float* bias,
                       float* out, int M, int K, int N, int act, void* stream);
 /* The decoder MLP's gate|up projection with SwiGLU and the bf16 cast folded into the GEMM's
  * epilogue: asr_gemm::LinearPre on the fused [gate; up] weight (2I rows), asr_ops::SwiGLU and
  * F32ToBf16 (src/model/asr_text_decoder.cu:547-552, :424-428) in one launch.  out_bf16[M,I] =
  * bf16_rne(silu(g) * u), g = in . W[0:I]^T, u = in . W[I:2I]^T, the same values as the three
- * separate calls.  K % 8 == 0, I % 4 == 0.  No reference counterpart as one entry. */
+ * separate calls.  I % 4 == 0; any K (K % 8 != 0 or unaligned operands run the plain GEMM
+ * into workspace, then the SwiGLU pass).  No reference counterpart as one entry. */
 int orator_linear_pre_swiglu(const uint16_t* in_bf16, const uint16_t* W_gateup,
                              uint16_t* out_bf16, int M, int K, int I, void* stream);
 /* asr_gemm::Linear (asr_gemm.h:27-31, asr_gemm.cu:160-167): the same with fp32 `in`, cast to
  * bf16 (round to nearest even) into library workspace first. */
 int orator_linear(const float* in_f32, const uint16_t* W_bf16, const float* bias, float* out,
                   int M, int K, int N, int act, void* stream);
-/* gemm::LaunchBf16Gemm (include/model/gemm.cuh:484-501): the MFMA GEMM for any M >= 1. */
+/* gemm::LaunchBf16Gemm (include/model/gemm.cuh:484-501): the MFMA GEMM for any M >= 1, any
+ * K >= 1, 2-byte aligned operands (as orator_linear_pre). */
 int orator_bf16_gemm(const uint16_t* in_bf16, const uint16_t* W_bf16, const float* bias,
                      float* out, int M, int K, int N, int act, void* stream);
 

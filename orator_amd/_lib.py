@@ -106,6 +106,7 @@ SIGNATURES: dict[str, list] = {
     "orator_event_record": [_p, _p],
     "orator_event_elapsed_ms": [C.POINTER(_f), _p, _p],
     "orator_workspace_reserve": [_sz, _p],
+    "orator_workspace_stats": [C.POINTER(_sz), C.POINTER(_sz)],
     "orator_time_next_decode": [_p, _p, _p],
     # asr_ops family
     "orator_rms_norm": [_p, _p, _p, _i, _i, _f, _p],

@@ -184,26 +184,30 @@ __global__ __launch_bounds__(256) void swiglu_bf16_kernel(const float* __restric
 }
 
 // -------------------------------------------------------------------- casts ----
+// VEC: 16-byte fp32 side and 8-byte bf16 side (4 elements per access); otherwise element
+// accesses (operands at their natural alignment only).
+template <bool VEC>
 __global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ in,
                                                           uint16_t* __restrict__ out, long n) {
   const long i = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
-  if (i + 3 < n) {
+  if (VEC && i + 3 < n) {
     const float4 v = *reinterpret_cast<const float4*>(in + i);
     *reinterpret_cast<uint2*>(out + i) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
   } else {
-    for (long k = i; k < n; ++k) out[k] = f32_to_bf16(in[k]);
+    for (long k = i; k < n && k < i + 4; ++k) out[k] = f32_to_bf16(in[k]);
   }
 }
 
+template <bool VEC>
 __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __restrict__ in,
                                                           float* __restrict__ out, long n) {
   const long i = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
-  if (i + 3 < n) {
+  if (VEC && i + 3 < n) {
     const uint2 v = *reinterpret_cast<const uint2*>(in + i);
     *reinterpret_cast<float4*>(out + i) =
         make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
   } else {
-    for (long k = i; k < n; ++k) out[k] = bf16_to_f32(in[k]);
+    for (long k = i; k < n && k < i + 4; ++k) out[k] = bf16_to_f32(in[k]);
   }
 }
 
@@ -670,20 +674,30 @@ int orator_swiglu(const float* gate, const float* up, float* out, int n, void* s
 int orator_f32_to_bf16(const float* in, uint16_t* out, long n, void* stream) {
   if (n <= 0) return ORATOR_OK;
   if (!in || !out) return fail(ORATOR_ERR_INVALID, "f32_to_bf16: null pointer");
-  if (!aligned16(in) || (reinterpret_cast<uintptr_t>(out) & 7u))
-    return fail(ORATOR_ERR_INVALID, "f32_to_bf16: in must be 16-byte and out 8-byte aligned");
-  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(blocks_for((n + 3) / 4)), dim3(kBlock), 0,
-                     static_cast<hipStream_t>(stream), in, out, n);
+  if ((reinterpret_cast<uintptr_t>(in) & 3u) || (reinterpret_cast<uintptr_t>(out) & 1u))
+    return fail(ORATOR_ERR_INVALID, "f32_to_bf16: in must be 4-byte and out 2-byte aligned");
+  const bool vec = aligned16(in) && (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
+  if (vec)
+    hipLaunchKernelGGL(f32_to_bf16_kernel<true>, dim3(blocks_for((n + 3) / 4)), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), in, out, n);
+  else
+    hipLaunchKernelGGL(f32_to_bf16_kernel<false>, dim3(blocks_for((n + 3) / 4)), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), in, out, n);
   return check_launch("f32_to_bf16");
 }
 
 int orator_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream) {
   if (n <= 0) return ORATOR_OK;
   if (!in || !out) return fail(ORATOR_ERR_INVALID, "bf16_to_f32: null pointer");
-  if ((reinterpret_cast<uintptr_t>(in) & 7u) || !aligned16(out))
-    return fail(ORATOR_ERR_INVALID, "bf16_to_f32: in must be 8-byte and out 16-byte aligned");
-  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(blocks_for((n + 3) / 4)), dim3(kBlock), 0,
-                     static_cast<hipStream_t>(stream), in, out, n);
+  if ((reinterpret_cast<uintptr_t>(in) & 1u) || (reinterpret_cast<uintptr_t>(out) & 3u))
+    return fail(ORATOR_ERR_INVALID, "bf16_to_f32: in must be 2-byte and out 4-byte aligned");
+  const bool vec = (reinterpret_cast<uintptr_t>(in) & 7u) == 0 && aligned16(out);
+  if (vec)
+    hipLaunchKernelGGL(bf16_to_f32_kernel<true>, dim3(blocks_for((n + 3) / 4)), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), in, out, n);
+  else
+    hipLaunchKernelGGL(bf16_to_f32_kernel<false>, dim3(blocks_for((n + 3) / 4)), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), in, out, n);
   return check_launch("bf16_to_f32");
 }
 

@@ -53,7 +53,7 @@ __device__ __forceinline__ float gb_act(float v, int act) {
 // bf16(silu(gate) * up) for its BN/2 columns of the [M][I] bf16 output.
 constexpr int kEpiPartial = 0, kEpiStore = 1, kEpiAccumulate = 2, kEpiAct = 3, kEpiSwiglu = 4;
 
-template <int BM, int BN, int WGM, int WGN, int MINW, int EPI>
+template <int BM, int BN, int WGM, int WGN, int MINW, int EPI, bool GEN = false>
 __global__ __launch_bounds__(64 * WGM * WGN, MINW) void gemm_bf16_nt_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ W,
     const float* __restrict__ bias, float* __restrict__ C, int M, int K, int N, int act,
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void gemm_bf16_nt_kernel(
   // split-K: workgroup z covers k in [z * k_split, (z + 1) * k_split) (k_split a multiple of
   // kBK) and leaves its raw partial sums in part[z]
   const int kb = blockIdx.z * k_split;
-  const int k_lim = min(K - kb, k_split);  // a multiple of 8
+  const int k_lim = min(K - kb, k_split);  // a multiple of 8 unless GEN
   const int n_k = (k_lim + kBK - 1) / kBK;
   A += kb;
   W += kb;
@@ -123,16 +123,35 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void gemm_bf16_nt_kernel(
   gb_u32x4_t ra[LA], rw[LW];
   uint32_t keep = 0;  // mask of the chunk in flight; applied at the LDS store, and only on the
                       // last K step when k_lim is not a multiple of kBK (a uniform branch)
+  // GEN (any K, rows at any 2-byte alignment): the chunk's 8 elements are loaded one by one,
+  // elements past k_lim read as zero, so nothing is masked at the store.
+  auto load8 = [&](const uint16_t* row, int kk) {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = kk + 2 * e < k_lim ? row[kk + 2 * e] : 0u;
+      const uint32_t hi = kk + 2 * e + 1 < k_lim ? row[kk + 2 * e + 1] : 0u;
+      w[e] = lo | (hi << 16);
+    }
+    return gb_u32x4_t{w[0], w[1], w[2], w[3]};
+  };
   auto load = [&](int k0) {
     const int kk = k0 + 8 * lc;
-    const int kc = min(kk, k_lim - 8);
-    keep = kk < k_lim ? 0xffffffffu : 0u;
+    if constexpr (GEN) {
 #pragma unroll
-    for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const gb_u32x4_t*>(arow[i] + kc);
+      for (int i = 0; i < LA; ++i) ra[i] = load8(arow[i], kk);
 #pragma unroll
-    for (int i = 0; i < LW; ++i) rw[i] = *reinterpret_cast<const gb_u32x4_t*>(wrow[i] + kc);
+      for (int i = 0; i < LW; ++i) rw[i] = load8(wrow[i], kk);
+    } else {
+      const int kc = min(kk, k_lim - 8);
+      keep = kk < k_lim ? 0xffffffffu : 0u;
+#pragma unroll
+      for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const gb_u32x4_t*>(arow[i] + kc);
+#pragma unroll
+      for (int i = 0; i < LW; ++i) rw[i] = *reinterpret_cast<const gb_u32x4_t*>(wrow[i] + kc);
+    }
   };
-  const bool ragged = (k_lim % kBK) != 0;
+  const bool ragged = !GEN && (k_lim % kBK) != 0;
   auto store = [&](int buf, bool masked) {
     if (masked) {
 #pragma unroll
@@ -318,7 +337,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   out[i] = accumulate ? out[i] + v : v;
 }
 
-template <int BM, int BN, int WGM, int WGN, int MINW>
+template <int BM, int BN, int WGM, int WGN, int MINW, bool GEN>
 int launch_tile(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
                 int K, int N, int act, bool accumulate, int splits, hipStream_t s) {
   const int k_split = splits > 1 ? ((K + splits - 1) / splits + kBK - 1) / kBK * kBK : K;
@@ -334,17 +353,17 @@ int launch_tile(const uint16_t* in, const uint16_t* W, const float* bias, float*
   const dim3 block(64 * WGM * WGN);
   const int acc = accumulate ? 1 : 0;
   if (splits > 1)
-    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiPartial>), grid, block, 0,
-                       s, in, W, bias, out, M, K, N, act, acc, part, k_split);
+    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiPartial, GEN>), grid,
+                       block, 0, s, in, W, bias, out, M, K, N, act, acc, part, k_split);
   else if (act != 0 || (bias && !accumulate))
-    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiAct>), grid, block, 0, s,
-                       in, W, bias, out, M, K, N, act, acc, part, k_split);
-  else if (accumulate)
-    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiAccumulate>), grid, block,
+    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiAct, GEN>), grid, block,
                        0, s, in, W, bias, out, M, K, N, act, acc, part, k_split);
+  else if (accumulate)
+    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiAccumulate, GEN>), grid,
+                       block, 0, s, in, W, bias, out, M, K, N, act, acc, part, k_split);
   else
-    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiStore>), grid, block, 0,
-                       s, in, W, bias, out, M, K, N, act, acc, part, k_split);
+    hipLaunchKernelGGL((gemm_bf16_nt_kernel<BM, BN, WGM, WGN, MINW, kEpiStore, GEN>), grid, block,
+                       0, s, in, W, bias, out, M, K, N, act, acc, part, k_split);
   if (int rc = check_launch("gemm_bf16_nt_kernel")) return rc;
   if (splits == 1) return ORATOR_OK;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((MN + 255) / 256)),
@@ -376,12 +395,14 @@ int launch_gemm_bf16_swiglu(const uint16_t* in, const uint16_t* W, uint16_t* out
 }
 
 // Tile shape by grid size: 128 x 128 when that grid gives every CU two workgroups, else
-// 128 x 64; when even that leaves CUs idle and K is long, K is split over workgroups (partials
+// 128 x 64 (always for `generic`: K not a multiple of 8 or rows not 16-byte aligned, loaded
+// element by element); when even that leaves CUs idle and K is long, K is split over workgroups (partials
 // reduced in a fixed order: deterministic).  Measured at the 503-row prompt shapes: 128 x 64 unsplit
 // beats a K split whenever its grid covers the CUs (qkv, 21.7 vs 23.7 us); below that, splits
 // to two workgroups per CU beat one (down projection, 28.4 vs 36.8 us).
 int launch_gemm_bf16_nt(const uint16_t* in, const uint16_t* W, const float* bias, float* out,
-                        int M, int K, int N, int act, bool accumulate, hipStream_t s) {
+                        int M, int K, int N, int act, bool accumulate, hipStream_t s,
+                        bool generic) {
   if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;
   const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
   auto tiles = [&](int bm, int bn) {
@@ -389,15 +410,19 @@ int launch_gemm_bf16_nt(const uint16_t* in, const uint16_t* W, const float* bias
   };
   // 128 x 128 only when every CU gets two of them (one workgroup per CU leaves its epilogue
   // exposed: the decoder's 2048 x 2048 -> 2048 projections ran 2 % faster on 128 x 64)
-  if (tiles(128, 128) >= 2 * cus)
-    return launch_tile<128, 128, 2, 2, 2>(in, W, bias, out, M, K, N, act, accumulate, 1, s);
+  if (!generic && tiles(128, 128) >= 2 * cus)
+    return launch_tile<128, 128, 2, 2, 2, false>(in, W, bias, out, M, K, N, act, accumulate, 1, s);
   // when even 128 x 64 tiles leave CUs idle, split K until the grid gives every CU two
   // workgroups (K / 512 splits at most)
   const long t = tiles(128, 64);
   int splits = 1;
   if (t < cus)
     splits = static_cast<int>(std::min<long>((2 * cus + t - 1) / t, std::max(1, K / 512)));
-  return launch_tile<128, 64, 4, 1, 2>(in, W, bias, out, M, K, N, act, accumulate, splits, s);
+  if (generic)
+    return launch_tile<128, 64, 4, 1, 2, true>(in, W, bias, out, M, K, N, act, accumulate, splits,
+                                               s);
+  return launch_tile<128, 64, 4, 1, 2, false>(in, W, bias, out, M, K, N, act, accumulate, splits,
+                                              s);
 }
 
 }  // namespace orator_hip

@@ -20,9 +20,10 @@ int check_hip(hipError_t e, const char* what);
 // Checks hipGetLastError() after a launch.
 int check_launch(const char* what);
 
-// Device scratch owned by the library, one block per (device, stream, host thread), grown
-// on demand; a grown block's old memory is kept (queued work or a captured graph may still
-// read it) until workspace_release(stream).  Returns nullptr on failure (the error is
+// Device scratch owned by the library, one block per (device, stream, host thread, slot),
+// grown geometrically on demand.  A grown block's old memory is freed once the work queued
+// on the stream before the growth has finished (an event), or, if it was handed out during a
+// graph capture, at workspace_release(stream).  Returns nullptr on failure (the error is
 // recorded).
 // Slots are independent blocks: kWsGemm holds the split-K partials of the GEMMs, which may run
 // while a caller's slot-0 buffer (e.g. the bf16 cast of a Linear input) is being read.
@@ -134,9 +135,11 @@ int launch_rms_norm_bf16(const float* x, const float* w, uint16_t* out, int rows
 int launch_swiglu_bf16(const float* gu, uint16_t* out, int T, int I, hipStream_t s);
 
 // This library's bf16 GEMM (gemm_bf16.hip): out[M][N] (= or +=) act(in[M][K] W[N][K]^T +
-// bias), fp32 accumulation and output; K a multiple of 8, 16-byte aligned operands.
+// bias), fp32 accumulation and output.  K a multiple of 8 and 16-byte aligned operands, or
+// `generic`: any K, operands at any 2-byte alignment (element loads).
 int launch_gemm_bf16_nt(const uint16_t* in, const uint16_t* W, const float* bias, float* out,
-                        int M, int K, int N, int act, bool accumulate, hipStream_t s);
+                        int M, int K, int N, int act, bool accumulate, hipStream_t s,
+                        bool generic = false);
 // The gate|up projection with SwiGLU and the bf16 cast in the GEMM epilogue (gemm_bf16.hip):
 // out[M][I] = bf16(silu(in W[0:I]^T) * (in W[I:2I]^T)); `tmp` ([M][2I] fp32, or null for the
 // stream's workspace) is used only when the grid is too short for the fused kernel.

@@ -10,6 +10,8 @@
 //    instruction moves one contiguous 1 KB piece of a row, and the k loop is unrolled so a
 //    lane keeps 16 such loads in flight.  x (4-12 KB) is read through the caches.
 //  * M > 1 (prefill) is MFMA-bound: this library's bf16 GEMM (gemm_bf16.hip).
+//  * K not a multiple of 8, or operands not 16-byte aligned (the audio tower's first conv as
+//    a GEMM has K = 9, asr_audio_tower.cu:417-445): the GEMM with element loads, M = 1 too.
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -290,13 +292,18 @@ int launch_fused_mode(const float* x, const float* aux, float eps, const uint16_
   return launch_fused_u<MODE, ACC, 4>(x, aux, eps, W, out, K, N, pair, s);
 }
 
+// Argument checks shared by the bf16 linear entry points.  Returns the status; *generic is set
+// when K is not a multiple of 8 or `in` / W are not 16-byte aligned: the GEMM then loads
+// element by element (any K, as the reference's generic fallback, gemm.cuh:461-501; operands
+// need only the 2-byte alignment of their element type).
 int check_linear(const void* in, const uint16_t* W, const float* out, int K, int act,
-                 const char* who) {
+                 const char* who, bool* generic) {
   if (!in || !W || !out) return fail(ORATOR_ERR_INVALID, std::string(who) + ": null pointer");
   if (act < 0 || act > 2) return fail(ORATOR_ERR_INVALID, std::string(who) + ": act must be 0-2");
-  if (K % 8) return fail(ORATOR_ERR_UNSUPPORTED, std::string(who) + ": K must be a multiple of 8");
-  if ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15u)
-    return fail(ORATOR_ERR_INVALID, std::string(who) + ": in and W must be 16-byte aligned");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W);
+  if (al & 1u)
+    return fail(ORATOR_ERR_INVALID, std::string(who) + ": in and W must be 2-byte aligned");
+  *generic = (K % 8) != 0 || (al & 15u) != 0;
   return ORATOR_OK;
 }
 
@@ -305,14 +312,15 @@ int check_linear(const void* in, const uint16_t* W, const float* out, int K, int
 int launch_bf16_gemm(const uint16_t* in, const uint16_t* W, const float* bias, float* out, int M,
                      int K, int N, int act, hipStream_t stream) {
   if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;  // reference no-op
-  if (int rc = check_linear(in, W, out, K, act, "bf16_gemm")) return rc;
-  if (M == 1) {  // one row: the weight-streaming GEMV
+  bool generic = false;
+  if (int rc = check_linear(in, W, out, K, act, "bf16_gemm", &generic)) return rc;
+  if (M == 1 && !generic) {  // one row: the weight-streaming GEMV
     const int per_wg = kGemvRows * kGemvWaves;
     hipLaunchKernelGGL(gemv_bf16_kernel, dim3((N + per_wg - 1) / per_wg), dim3(64 * kGemvWaves), 0,
                        stream, in, W, bias, out, K, N, act);
     return check_launch("gemv_bf16_kernel");
   }
-  return launch_gemm_bf16_nt(in, W, bias, out, M, K, N, act, false, stream);
+  return launch_gemm_bf16_nt(in, W, bias, out, M, K, N, act, false, stream, generic);
 }
 
 int launch_gemv_fused(int mode, const float* x, const float* aux, float eps, const uint16_t* W,
@@ -350,8 +358,9 @@ int launch_linear_pre(const uint16_t* in, const uint16_t* W, const float* bias, 
 int launch_linear_pre_acc(const uint16_t* in, const uint16_t* W, float* out, int M, int K, int N,
                           float* tmp, hipStream_t stream) {
   if (M <= 0 || K <= 0 || N <= 0) return ORATOR_OK;
-  if (int rc = check_linear(in, W, out, K, 0, "linear_acc")) return rc;
-  if (M > 1) return launch_gemm_bf16_nt(in, W, nullptr, out, M, K, N, 0, true, stream);
+  bool generic = false;
+  if (int rc = check_linear(in, W, out, K, 0, "linear_acc", &generic)) return rc;
+  if (M > 1) return launch_gemm_bf16_nt(in, W, nullptr, out, M, K, N, 0, true, stream, generic);
   if (int rc = launch_bf16_gemm(in, W, nullptr, tmp, M, K, N, 0, stream)) return rc;
   return orator_add_residual(out, tmp, static_cast<long>(M) * N, stream);
 }
@@ -373,17 +382,19 @@ int orator_linear_pre_swiglu(const uint16_t* in_bf16, const uint16_t* W_gateup,
   if (M <= 0 || K <= 0 || I <= 0) return ORATOR_OK;
   if (!out_bf16) return fail(ORATOR_ERR_INVALID, "linear_pre_swiglu: null pointer");
   if (I % 4) return fail(ORATOR_ERR_UNSUPPORTED, "linear_pre_swiglu: I must be a multiple of 4");
+  bool generic = false;
   if (int rc = check_linear(in_bf16, W_gateup, reinterpret_cast<const float*>(out_bf16), K, 0,
-                            "linear_pre_swiglu"))
+                            "linear_pre_swiglu", &generic))
     return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  // the fp32 gate|up block is materialised (in the stream's workspace) only by the M = 1 and
-  // short-grid paths
-  if (M == 1) {
-    float* tmp = static_cast<float*>(workspace(s, 2 * static_cast<size_t>(I) * sizeof(float)));
+  // the fp32 gate|up block is materialised (in the stream's workspace) only by the M = 1,
+  // any-K and short-grid paths
+  if (M == 1 || generic) {
+    float* tmp =
+        static_cast<float*>(workspace(s, 2 * static_cast<size_t>(M) * I * sizeof(float)));
     if (!tmp) return ORATOR_ERR_HIP;
-    if (int rc = launch_bf16_gemm(in_bf16, W_gateup, nullptr, tmp, 1, K, 2 * I, 0, s)) return rc;
-    return launch_swiglu_bf16(tmp, out_bf16, 1, I, s);
+    if (int rc = launch_bf16_gemm(in_bf16, W_gateup, nullptr, tmp, M, K, 2 * I, 0, s)) return rc;
+    return launch_swiglu_bf16(tmp, out_bf16, M, I, s);
   }
   return launch_gemm_bf16_swiglu(in_bf16, W_gateup, out_bf16, nullptr, M, K, I, s);
 }

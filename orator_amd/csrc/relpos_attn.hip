@@ -158,8 +158,8 @@ int orator_relpos_attention(const float* q, const float* k, const float* v, cons
 
 // ===================================================================== fused fp16 path
 //
-// One workgroup = one (head, 32-query tile); its 4 wave64s split the key range (tiles of 32
-// keys, wave w takes tiles w, w+4, ...) and merge (max, sum, acc) through LDS at the end.
+// One workgroup = one (head, 32-query tile); its 8 wave64s split the key range (tiles of 32
+// keys, wave w takes tiles w, w+8, ...) and merge (max, sum, acc) through LDS at the end.
 // Per key tile and wave, on v_mfma_f32_32x32x16_f16 (S^T orientation, so the softmax
 // state is per lane = per query column):
 //   AC^T[j][i] = K[j] . (q_i + u)                  4 MFMAs

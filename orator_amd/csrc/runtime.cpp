@@ -1,6 +1,8 @@
 // Library runtime: error reporting, the per-(device, stream, thread) workspace and the small
 // device-plumbing surface of the C ABI (allocation, copies, streams, events).
 #include <hip/hip_runtime.h>
+#include <sys/syscall.h>
+#include <unistd.h>
 
 #include <cmath>
 #include <atomic>
@@ -23,10 +25,55 @@ int ws_sync(const void* stream) {
              ? 0
              : 1;
 }
-WorkspacePool& ws_pool() {
-  static WorkspacePool* pool = new WorkspacePool(ws_alloc, ws_free, ws_sync);  // never destroyed:
-  return *pool;  // blocks may be in use until the process ends
+// true while `stream` is being captured (or when that cannot be told: then nothing recorded
+// on it is trusted as a completion marker)
+bool ws_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return st != hipStreamCaptureStatusNone;
 }
+void* ws_record(int dev, const void* stream_p) {
+  hipStream_t stream = static_cast<hipStream_t>(const_cast<void*>(stream_p));
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+  if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+  hipEvent_t ev = nullptr;
+  if (!ws_capturing(stream) &&
+      hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess &&
+      hipEventRecord(ev, stream) != hipSuccess) {
+    (void)hipEventDestroy(ev);
+    ev = nullptr;
+  }
+  if (cur != dev) (void)hipSetDevice(cur);
+  (void)hipGetLastError();
+  return ev;
+}
+int ws_done(void* ev) {
+  const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(ev));
+  if (e == hipSuccess) return 1;
+  (void)hipGetLastError();
+  return e == hipErrorNotReady ? 0 : -1;
+}
+void ws_destroy(void* ev) { (void)hipEventDestroy(static_cast<hipEvent_t>(ev)); }
+WorkspacePool& ws_pool() {
+  // never destroyed: blocks may be in use until the process ends
+  static WorkspacePool* pool =
+      new WorkspacePool(ws_alloc, ws_free, ws_sync, ws_record, ws_done, ws_destroy);
+  return *pool;
+}
+// Retires a worker thread's blocks when it exits.  The process's main thread skips this: its
+// thread_local objects are destroyed at process exit, where no device call is made.
+struct WsThreadGuard {
+  bool armed = false;
+  ~WsThreadGuard() {
+    if (armed && static_cast<pid_t>(syscall(SYS_gettid)) != getpid())
+      ws_pool().thread_exit(std::this_thread::get_id());
+  }
+};
+thread_local WsThreadGuard g_ws_guard;
 thread_local hipEvent_t g_ev_start = nullptr, g_ev_split = nullptr, g_ev_stop = nullptr;
 }  // namespace
 
@@ -64,7 +111,9 @@ void* workspace(hipStream_t stream, size_t bytes, int slot) {
   int dev = 0;
   if (check_hip(hipGetDevice(&dev), "hipGetDevice") != ORATOR_OK) return nullptr;
   std::string err;
-  void* p = ws_pool().get(WsKey{dev, stream, std::this_thread::get_id(), slot}, bytes, &err);
+  g_ws_guard.armed = true;
+  void* p = ws_pool().get(WsKey{dev, stream, std::this_thread::get_id(), slot}, bytes,
+                          ws_capturing(stream), &err);
   if (!p) (void)fail(ORATOR_ERR_HIP, err);
   return p;
 }
@@ -212,6 +261,13 @@ int orator_time_next_decode(void* start, void* split_end, void* stop) {
 int orator_workspace_reserve(size_t bytes, void* stream) {
   return orator_hip::workspace(static_cast<hipStream_t>(stream), bytes) ? ORATOR_OK
                                                                         : ORATOR_ERR_HIP;
+}
+
+int orator_workspace_stats(size_t* blocks, size_t* bytes) {
+  orator_hip::ws_pool().reap();
+  if (blocks) *blocks = orator_hip::ws_pool().held_blocks();
+  if (bytes) *bytes = orator_hip::ws_pool().held_bytes();
+  return ORATOR_OK;
 }
 
 }  // extern "C"

@@ -33,6 +33,14 @@ def synchronize() -> None:
     call("orator_device_synchronize")
 
 
+def workspace_stats() -> tuple[int, int]:
+    """(blocks, bytes) of library workspace held now, after freeing retired blocks whose
+    stream work has completed."""
+    blocks, nbytes = C.c_size_t(0), C.c_size_t(0)
+    call("orator_workspace_stats", C.byref(blocks), C.byref(nbytes))
+    return blocks.value, nbytes.value
+
+
 class DeviceBuffer:
     """`nbytes` of device memory.  `ptr` is the device address as an int."""
 

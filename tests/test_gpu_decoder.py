@@ -76,6 +76,79 @@ def test_linear_pre_prompt_tiles(M, K, N):
     assert np.all(np.abs(got - ref) <= bound), np.max(np.abs(got - ref) / bound)
 
 
+def _placed(arr, off):
+    """arr on the device `off` elements past a 16-byte aligned allocation (off odd: rows
+    start at 2-byte alignment only); returns (buffer, device address)."""
+    flat = np.ascontiguousarray(arr).reshape(-1)
+    pad = np.zeros(off + flat.size, flat.dtype)
+    pad[off:] = flat
+    buf = up(pad)
+    return buf, buf.ptr + off * flat.itemsize
+
+
+# Any K and any alignment, as the reference's generic fallback (include/model/gemm.cuh:461-501,
+# src/model/asr_gemm.cu:188-214): K = 9 is the audio tower's first conv as a GEMM (Cin 1 x 3 x 3,
+# src/model/asr_audio_tower.cu:417-445), K = 13 an odd row, K = 4320 a long one that is a
+# multiple of 8 but whose operands are not 16-byte aligned.  M = 1 and M > 1, every entry point.
+@pytest.mark.parametrize("M,K,N,off", [(1, 9, 480, 0), (390, 9, 480, 0), (1, 13, 37, 1),
+                                       (77, 13, 300, 3), (1, 4320, 480, 1), (200, 4320, 480, 5),
+                                       (2048, 9, 128, 0), (5, 1, 7, 0)])
+@pytest.mark.parametrize("act,with_bias", [(0, False), (1, True)])
+def test_linear_any_k_any_alignment(M, K, N, off, act, with_bias):
+    from orator_amd import gemm
+    r = SplitMix64(M * 31 + K * 7 + N + off + act)
+    x = orc.to_bf16(r.normal((M, K)))
+    W = orc.to_bf16(r.normal((N, K), 0.05))
+    bias = r.normal(N) if with_bias else None
+    xd, Wd = orc.from_bf16(x).astype(np.float64), orc.from_bf16(W).astype(np.float64)
+    ref = xd @ Wd.T + (bias if with_bias else 0.0)
+    if act == 1:
+        ref = 0.5 * ref * (1 + np.vectorize(math.erf)(ref / math.sqrt(2)))
+    bound = 3e-5 * (np.abs(xd) @ np.abs(Wd).T + 1.0)
+    xb, xp = _placed(x, off)
+    wb, wp = _placed(W, off)
+    db = up(bias) if with_bias else None
+    for name, fn in (("LinearPre", asr_gemm.LinearPre), ("LaunchBf16Gemm", gemm.LaunchBf16Gemm)):
+        out = empty((M, N), np.float32)
+        say(name, "any K", M, K, N, off, act)
+        fn(xp, wp, db, out, M, K, N, act)
+        got = down(out, (M, N))
+        assert np.all(np.abs(got - ref) <= bound), (name, np.max(np.abs(got - ref) / bound))
+    # Linear (fp32 input, cast to bf16 by the library): the same bits as LinearPre on the
+    # bf16 rows
+    xf = orc.from_bf16(x)
+    fb, fp = _placed(xf, off)
+    out_f, out_p = empty((M, N), np.float32), empty((M, N), np.float32)
+    say("Linear any K", M, K, N, off)
+    asr_gemm.Linear(fp, wp, db, out_f, M, K, N, act)
+    asr_gemm.LinearPre(xp, wp, db, out_p, M, K, N, act)
+    np.testing.assert_array_equal(down(out_f, (M, N)), down(out_p, (M, N)))
+
+
+@pytest.mark.parametrize("M,K,I,off", [(1, 13, 300, 1), (40, 9, 64, 0), (33, 4320, 100, 3)])
+def test_linear_pre_swiglu_any_k(M, K, I, off):
+    """The gate|up projection with SwiGLU at any K / alignment: bit-identical to LinearPre +
+    SwiGLU + F32ToBf16, as at aligned shapes."""
+    from orator_amd import asr_ops
+    r = SplitMix64(M + 5 * K + I + off)
+    x = orc.to_bf16(r.normal((M, K)))
+    W = orc.to_bf16(r.normal((2 * I, K), 0.05))
+    xb, xp = _placed(x, off)
+    wb, wp = _placed(W, off)
+    gu = empty((M, 2 * I), np.float32)
+    say("linear_pre_swiglu any K", M, K, I, off)
+    asr_gemm.LinearPre(xp, wp, None, gu, M, K, 2 * I, 0)
+    g_u = down(gu, (M, 2 * I))
+    act = empty((M * I,), np.float32)
+    asr_ops.SwiGLU(up(np.ascontiguousarray(g_u[:, :I])), up(np.ascontiguousarray(g_u[:, I:])),
+                   act, M * I)
+    want = empty((M * I,), np.uint16)
+    asr_ops.F32ToBf16(act, want, M * I)
+    got = empty((M * I,), np.uint16)
+    asr_gemm.LinearPreSwiGLU(xp, wp, got, M, K, I)
+    np.testing.assert_array_equal(down(got, (M, I), np.uint16), down(want, (M, I), np.uint16))
+
+
 @pytest.mark.parametrize("M,K,I", [(2048, 2048, 6144), (503, 2048, 6144), (300, 1024, 6000),
                                    (5, 512, 1000), (1, 512, 300)])
 def test_linear_pre_swiglu_equals_three_calls(M, K, I):

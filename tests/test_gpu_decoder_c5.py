@@ -7,14 +7,20 @@ from the same seeds; src/model/asr_text_decoder.cu:457-617, :360-455, :698-889).
 Near ties.  The composition re-rounds activations to bf16 before every projection, so any
 two fp32 restatements that sum in different orders differ by whole bf16 steps and their
 logits drift apart.  The golden file measures that drift: a second CPU restatement whose
-linear layers are BLAS products (B) is run teacher-forced beside the oracle (A).  NOISE = the
-largest change of A's top-1 - top-2 margin that B's summation order causes at any of the 257
-steps (0.021 on max |logit| ~ 3; B itself picks another token at 6 steps, all with margins
-below 0.005).  A step is excused only when the oracle's margin there is below NOISE; every
-other step must give the oracle's token.  Checks:
+linear layers are BLAS products (B) is run teacher-forced beside the oracle (A).
+  * NOISE = the largest change of A's top-1 - top-2 margin that B's summation order causes at
+    any of the 257 steps (0.024 on max |logit| ~ 3.5; B itself picks another token than A at
+    5 steps, all with margins below 0.005).  A step is excused only when the oracle's margin
+    there is below NOISE, and at an excused step the device's token must still be one of the
+    oracle's near-tie candidates: among A's top-32, with A's logit within NOISE of A's top-1;
+    every other step must give the oracle's token.
+  * TOP_TOL = 1.25 x max |B - A| over A's top-32 logits at every step (max |B - A| = 0.019):
+    the device is a third fp32 summation order, held to the second one's deviation.
+Checks:
   * teacher-forced: the device decodes the oracle's token stream step by step; its argmax
-    (the library's ArgmaxBanned) must be the oracle's token at every non-excused step, and
-    its logits at the oracle's top-32 ids within 1e-2 * max |logit| of the oracle's;
+    (the library's ArgmaxBanned) must be the oracle's token at every non-excused step, a
+    near-tie candidate at excused steps, and its logits at the oracle's top-32 ids within
+    TOP_TOL of the oracle's;
   * free-running: DecodeGreedy with graph replay must emit exactly the oracle's tokens (the
     reference's 6-repeat stop applied to them); the streams may part only at an excused step
     (after which the inputs differ and nothing more is comparable);
@@ -63,8 +69,11 @@ def test_c5_greedy_token_ids_match_oracle():
     margins_b = (g["top_b"][:, 0] - g["top_b"][:, 1]).astype(np.float64)
     noise = float(np.max(np.abs(margins_b - margins)))
     excused = margins < noise
-    print(f"c5: NOISE {noise:.4e}; oracle steps with margin below it: "
+    top_tol = 1.25 * float(np.max(np.abs(g["top_b"] - g["top_a"])))
+    print(f"c5: NOISE {noise:.4e}; TOP_TOL {top_tol:.4e}; oracle steps with margin below NOISE: "
           f"{np.flatnonzero(excused).tolist()}", flush=True)
+    print(f"c5: steps where the BLAS-order twin's argmax differs from the oracle's: "
+          f"{np.flatnonzero(g['argmax_b'] != gold).tolist()}", flush=True)
 
     # ---- teacher-forced ----
     say("c5: prefill")
@@ -93,7 +102,16 @@ def test_c5_greedy_token_ids_match_oracle():
               f"|dev-oracle| top-32 {dtop[s]:.2e}{flag}")
     bad = [s for s in range(new + 1) if dev[s] != gold[s] and not excused[s]]
     assert not bad, f"token mismatch at non-excused steps {bad}"
-    assert max(dtop) <= LOGIT_TOL * float(np.max(g["maxabs_a"]))
+    # at an excused step the device's token is a near-tie candidate of the oracle's
+    for s in np.flatnonzero(dev != gold):
+        ids = g["top_ids"][s].tolist()
+        assert int(dev[s]) in ids, f"step {s}: device token {dev[s]} not in the oracle's top-32"
+        gap = float(g["top_a"][s][0] - g["top_a"][s][ids.index(int(dev[s]))])
+        print(f"c5 step {s}: device token's oracle logit is {gap:.4e} below the top-1")
+        assert gap <= noise, f"step {s}: device token {gap:.4e} below the oracle's top-1"
+    print(f"c5: max |dev - oracle| over top-32 logits {max(dtop):.4e} (TOP_TOL {top_tol:.4e}); "
+          f"device mismatch steps {np.flatnonzero(dev != gold).tolist()}", flush=True)
+    assert max(dtop) <= top_tol
 
     # ---- free-running greedy with graph replay ----
     say("c5: DecodeGreedy (graph replay)")

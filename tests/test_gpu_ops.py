@@ -81,6 +81,16 @@ def test_bf16_casts_bit_exact(n):
     df = empty((n,), np.float32)
     asr_ops.Bf16ToF32(db, df, n)
     np.testing.assert_array_equal(down(df, (n,)), orc.from_bf16(bits))
+    # the same at element offsets 1 and 3 (natural alignment only: the element-access path)
+    for off in (1, 3):
+        src = up(np.concatenate([np.zeros(off, np.float32), x]))
+        d16 = empty((n + off,), np.uint16)
+        asr_ops.F32ToBf16(src.ptr + 4 * off, d16.ptr + 2 * off, n)
+        got16 = down(d16, (n + off,), np.uint16)[off:]
+        np.testing.assert_array_equal(got16, bits)
+        d32 = empty((n + off,), np.float32)
+        asr_ops.Bf16ToF32(d16.ptr + 2 * off, d32.ptr + 4 * off, n)
+        np.testing.assert_array_equal(down(d32, (n + off,))[off:], orc.from_bf16(bits))
 
 
 def _argmax_gpu(x, b0=-1, b1=-1):

@@ -197,14 +197,67 @@ def test_prefill_bf16_q_input():
     assert np.max(np.abs(down(dout, q.shape) - ref)) <= TOL16
 
 
-def test_prefill_2048_bf16():
-    """The prefill throughput shape (2048 tokens), bf16 mode."""
-    T, Hkv, Dh = 2048, 8, 128
-    q, kc, vc = _layer_inputs(2048, T, 0)
-    ref = orc.gqa_prefill(q, kc, vc, 0, 1.0 / math.sqrt(Dh), threads=16)
-    say("prefill 2048 bf16")
-    got = _run(q, kc, vc, 0, T, da.PREFILL_BF16, Hkv)
-    assert np.max(np.abs(got - ref)) <= TOL16
+def _launcher_rw(T, Hq, Hkv, cus=256):
+    """The launcher's choice of row waves per workgroup and pairing (prefill_attn.hip
+    launch_g), so each case below names the instantiation it runs on a 256-CU MI355X."""
+    G = Hq // Hkv
+    tw = 32 // G
+    blocks4 = -(-T // (4 * tw))
+    blocks2 = -(-T // (2 * tw))
+    rw = 4 if blocks4 * Hkv >= 2 * cus else (1 if blocks2 * Hkv < cus else 2)
+    n_tblocks = -(-T // (rw * tw))
+    paired = rw > 1 and n_tblocks * Hkv >= 2 * cus
+    return rw, paired
+
+
+_ORACLE_CACHE: dict = {}
+
+
+def _large_case(T, Hq, Hkv):
+    key = (T, Hq, Hkv)
+    if key not in _ORACLE_CACHE:
+        _ORACLE_CACHE.clear()  # one shape at a time (the fp64 value of T = 4096 is large)
+        q, kc, vc = _layer_inputs(T * 7 + Hq + Hkv, T, 0, Hq=Hq, Hkv=Hkv)
+        scale = 1.0 / math.sqrt(128)
+        ref = orc.gqa_prefill(q, kc, vc, 0, scale, threads=16)
+        _ORACLE_CACHE[key] = (q, kc, vc, ref)
+    return _ORACLE_CACHE[key]
+
+
+# Every instantiation the launcher takes at long prompts, in both precision modes: RW = 2
+# row waves paired (T = 2048, G = 2: the decoder's own 2048-token prefill kernel), RW = 2
+# unpaired, RW = 4 paired (T = 4096), for GQA groups 1, 2 and 4.
+LARGE = [(2048, 16, 8), (2048, 8, 8), (2048, 16, 16), (2048, 16, 4),
+         (4096, 16, 8), (4096, 16, 16), (4096, 16, 4)]
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("T,Hq,Hkv", LARGE)
+def test_prefill_long_prompt_instantiations(T, Hq, Hkv, mode):
+    q, kc, vc, ref = _large_case(T, Hq, Hkv)
+    rw, paired = _launcher_rw(T, Hq, Hkv)
+    say(f"prefill T={T} Hq={Hq} Hkv={Hkv} mode={mode} (RW={rw}, paired={paired})")
+    got = _run(q, kc, vc, 0, T, mode, Hkv)
+    truth = t64.prefill(q, kc, vc, 0, 1.0 / math.sqrt(128)) if mode == da.PREFILL_FP32 else None
+    if mode == da.PREFILL_FP32:
+        check_fp32(got, ref, TOL32, truth=truth)
+    else:
+        err = float(np.max(np.abs(got - ref)))
+        print(f"bf16 max |g - r| = {err:.3e}")
+        assert err <= TOL16
+
+
+def test_prefill_instantiation_table():
+    """The cases above reach the instantiations they are named for (host-side rule)."""
+    got = {c: _launcher_rw(*c) for c in LARGE}
+    assert got[(2048, 16, 8)] == (2, True)
+    assert got[(2048, 8, 8)] == (2, False)
+    assert got[(2048, 16, 16)] == (2, True)
+    assert got[(2048, 16, 4)] == (2, True)
+    assert got[(4096, 16, 8)] == (4, True)
+    assert got[(4096, 16, 16)] == (4, True)
+    assert got[(4096, 16, 4)] == (4, True)
+    assert _launcher_rw(503, 16, 8) == (1, False)
 
 
 @pytest.mark.parametrize("S", [513, 4097])

@@ -1,7 +1,9 @@
-"""CPU test of the library's workspace bookkeeping (orator_amd/csrc/workspace_pool.hpp): a
-grown block is retired, never freed under queued work or a captured graph; each host thread
-has its own block per stream (as the reference's thread_local scratch,
-src/model/asr_gemm.cu:23-43); releasing a stream frees exactly its blocks."""
+"""CPU test of the library's workspace bookkeeping (orator_amd/csrc/workspace_pool.hpp), built
+with AddressSanitizer: blocks grow geometrically (1000 creeping requests retire a handful); a
+grown block is freed once the work queued before its retirement completes, never earlier, and
+never while a captured graph may replay over it; each host thread has its own block per stream
+(as the reference's thread_local scratch, src/model/asr_gemm.cu:23-43) and gives it back when
+it exits; releasing a stream frees exactly its blocks."""
 from __future__ import annotations
 
 import shutil

@@ -1,8 +1,10 @@
 """GPU: the allocation-free decode entry point (orator_gqa_decode_paged_noalloc, split partials
 in a static device array) against orator_gqa_decode_paged on the same inputs, through the C
 ABI: two calls in a row, the second smaller, outputs bit-identical (same kernels, same split
-plan) and within 1e-4 relative (floor 0.05) of the oracle; sizes past the static scratch are
-rejected on the host with ORATOR_ERR_CAPACITY."""
+plan) and within 1e-4 relative (floor 0.05) of the oracle; the no-alloc entry runs first, on a
+fresh stream, and the library's workspace holds exactly the blocks and bytes it held before it
+(so it cannot have been served from a block an earlier allocating call left behind); sizes past
+the static scratch are rejected on the host with ORATOR_ERR_CAPACITY."""
 from __future__ import annotations
 
 import math
@@ -15,6 +17,7 @@ from gpu_helpers import down, empty, say, up
 from helpers import SplitMix64, rel_err
 from orator_amd import _lib
 from orator_amd import decoder_attn as da
+from orator_amd.runtime import Stream, workspace_stats
 
 pytestmark = pytest.mark.gpu
 
@@ -42,11 +45,19 @@ def test_noalloc_matches_allocating_entry_twice():
         B = len(lens)
         dq, dk, dv, dt, dpos = up(q), up(kp), up(vp), up(table), up(pos)
         o_ref, o_na = empty((B, Hq, Dh), np.float32), empty((B, Hq, Dh), np.float32)
-        say("noalloc vs paged", seed, B, max(lens))
-        da.GqaDecodeAttnPaged(dq, dk, dv, dt, max_pages, ps, dpos, o_ref, B, Hq, Hkv, Dh, scale)
+        st = Stream()  # fresh: no workspace block exists for it yet
+        say("noalloc first, on a fresh stream", seed, B, max(lens))
+        before = workspace_stats()
         da.GqaDecodeAttnPagedNoAlloc(dq, dk, dv, dt, max_pages, ps, dpos, o_na, B, Hq, Hkv, Dh,
-                                     scale)
+                                     scale, st)
+        st.synchronize()
+        assert workspace_stats() == before, (before, workspace_stats())
+        say("paged (allocating) on the same stream", seed)
+        da.GqaDecodeAttnPaged(dq, dk, dv, dt, max_pages, ps, dpos, o_ref, B, Hq, Hkv, Dh, scale,
+                              st)
+        st.synchronize()
         got, ref = down(o_na, (B, Hq, Dh)), down(o_ref, (B, Hq, Dh))
+        st.close()
         np.testing.assert_array_equal(got, ref)
         truth = orc.gqa_decode_paged(q, kp, vp, table, ps, pos, scale, threads=8)
         assert rel_err(got, truth, 0.05) <= 1e-4
