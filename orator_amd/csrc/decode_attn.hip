@@ -31,6 +31,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 
@@ -566,6 +567,205 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   }
 }
 
+// Wide split kernel for many streams (B * Hkv pairs >= half the CUs): each (stream, kv head)
+// is cut into `parts` ranges of `split_len` keys (a multiple of 32, fixed by the capacity so
+// the page-table entries of every chunk are known before the position is), one workgroup of
+// kWideWaves waves per range.  Wave w takes the range's 32-key chunks w, w + 8, ... in a
+// ping-pong loop (the next chunk's K/V loads are in flight while the current one is
+// computed), so a workgroup keeps ~128 KB of K/V in flight for its whole life instead of
+// paying a dispatch, an entry round trip and a barrier per 64 KB.  The entry load reads the
+// position and the page-table entries of every chunk of the wave at once (lane 2k, 2k + 1:
+// chunk k; lane 63: the position).  Partials go to the split merge (range index = split).
+constexpr int kWideWaves = 8;
+constexpr int kWideMaxChunks = 31;  // chunks per wave: 2 table entries each in lanes 0..61
+
+template <int DH, int G>
+__global__ __launch_bounds__(64 * kWideWaves) __attribute__((amdgpu_waves_per_eu(2)))
+void gqa_decode_wide_kernel(DecodeArgs a, int split_len) {
+  using KV = uint16_t;
+  using CK = Chunk<DH, KV>;
+  constexpr int NW = kWideWaves;
+  constexpr int NT = 64 * NW;
+  __shared__ float red_o[NW][G][DH];
+  __shared__ float red_ml[NW][G][2];
+
+  const int kvh = blockIdx.x;
+  const int b = blockIdx.y;
+  const int part = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int p0 = part * split_len;  // first key of this range
+  const int lim = a.capacity - 1;
+  const bool paged = a.page_table != nullptr;
+  // entry load: lanes 2k, 2k + 1 the page-table entries of keys c_k, c_k + 16 of the wave's
+  // chunk k (c_k = p0 + 32 (wave + NW k)), lane 63 the stream's position
+  const int* esrc = g_decode_zero;
+  {
+    const int k = lane >> 1;
+    const int key = min(p0 + 32 * (wave + NW * k) + 16 * (lane & 1), lim) & ~15;
+    if (paged && lane < 2 * kWideMaxChunks)
+      esrc = a.page_table + static_cast<long>(b) * a.max_pages + (key >> a.page_shift);
+    if (lane == 63 && a.pos_mode == 0) esrc = a.pos + b;
+  }
+  const int eld = *esrc;
+  const int pos_b = a.pos_mode == 0 ? __builtin_amdgcn_readlane(eld, 63) : 0;
+  const int S = stream_keys(a, b, pos_b);
+  if (S <= 0) {
+    if (part == 0)
+      for (int idx = tid; idx < G * DH; idx += NT)
+        a.out[(static_cast<long>(b) * a.Hkv * G + kvh * G) * DH + idx] = 0.0f;
+    return;
+  }
+  if (p0 >= S) return;
+  const int n_parts = (S + split_len - 1) / split_len;
+  const int Hq = a.Hkv * G;
+  const int o = lane & 7;
+  float qr[G][CK::QPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float* qh = a.q + (static_cast<long>(b) * Hq + kvh * G + g) * DH + CK::EPV * o;
+#pragma unroll
+    for (int cc = 0; cc < CK::NCQ; ++cc)
+#pragma unroll
+      for (int e4 = 0; e4 < CK::EPV; e4 += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(qh + 8 * CK::EPV * cc + e4);
+        qr[g][cc * CK::EPV + e4] = x.x;
+        qr[g][cc * CK::EPV + e4 + 1] = x.y;
+        qr[g][cc * CK::EPV + e4 + 2] = x.z;
+        qr[g][cc * CK::EPV + e4 + 3] = x.w;
+      }
+  }
+  const long kv_base = (paged ? 0 : static_cast<long>(b) * a.stream_stride) +
+                       static_cast<long>(kvh) * DH;
+  const KV* kbase = static_cast<const KV*>(a.kpool) + kv_base;
+  const KV* vbase = static_cast<const KV*>(a.vpool) + kv_base;
+  const long rs = static_cast<long>(a.Hkv) * DH;
+  int new_key = -1;
+  if (a.k_new && S == pos_b + 1) new_key = S - 1;
+  const int S_cache = new_key >= 0 ? S - 1 : S;
+  const int r_end = min(p0 + split_len, S_cache);  // this range's cached keys: [p0, r_end)
+  // rows of keys c_k, c_k + 16 of chunk k (wave-uniform)
+  auto rows = [&](int k, long& r0, long& r1) {
+    const int c = p0 + 32 * (wave + NW * k);
+    const int j0 = min(c, lim) & ~15, j1 = min(c + 16, lim) & ~15;
+    if (paged) {
+      const int msk = (1 << a.page_shift) - 1;
+      r0 = static_cast<long>(__builtin_amdgcn_readlane(eld, 2 * k)) * (1L << a.page_shift) + (j0 & msk);
+      r1 = static_cast<long>(__builtin_amdgcn_readlane(eld, 2 * k + 1)) * (1L << a.page_shift) + (j1 & msk);
+    } else {
+      r0 = j0;
+      r1 = j1;
+    }
+  };
+  // chunks of this wave holding cached keys: c_k < r_end
+  const int first = p0 + 32 * wave;
+  const int n_ch = first < r_end ? (r_end - first + 32 * NW - 1) / (32 * NW) : 0;
+
+  float m[G], lpart[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    lpart[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+  }
+  if (n_ch > 0) {
+    CK A, Bb;
+    long r0, r1;
+    rows(0, r0, r1);
+    load_chunk<DH, KV>(A, kbase, vbase, r0, r1, rs, first, r_end, lane);
+    for (int k = 0;;) {
+      const int c = first + 32 * NW * k;
+      if (k + 1 < n_ch) {
+        rows(k + 1, r0, r1);
+        load_chunk<DH, KV>(Bb, kbase, vbase, r0, r1, rs, c + 32 * NW, r_end, lane);
+      }
+      process_chunk<DH, G, KV>(A, qr, m, lpart, acc, c, r_end, lane, a.scale_log2e);
+      if (++k >= n_ch) break;
+      const int c2 = first + 32 * NW * k;
+      if (k + 1 < n_ch) {
+        rows(k + 1, r0, r1);
+        load_chunk<DH, KV>(A, kbase, vbase, r0, r1, rs, c2 + 32 * NW, r_end, lane);
+      }
+      process_chunk<DH, G, KV>(Bb, qr, m, lpart, acc, c2, r_end, lane, a.scale_log2e);
+      if (++k >= n_ch) break;
+    }
+  }
+  // the appended key: folded in by the wave whose chunk slot holds it, then written
+  if (new_key >= p0 && new_key < p0 + split_len && ((new_key - p0) >> 5) % NW == wave) {
+    const float* kn = a.k_new + (static_cast<long>(b) * a.Hkv + kvh) * DH;
+    const float* vn = a.v_new + (static_cast<long>(b) * a.Hkv + kvh) * DH;
+    uint4 kw[CK::NCQ], vw;
+    append_key<DH, G, false>(kn, vn, qr, m, lpart, acc, lane, a.scale_log2e, kw, vw, nullptr,
+                             0.0f, nullptr);
+    long row, row_unused;
+    chunk_rows(a, b, 0, new_key & ~15, row, row_unused);
+    row += new_key & 15;
+    if (row >= 0 && row < a.pool_rows) {
+      uint16_t* kdst = const_cast<uint16_t*>(kbase) + row * rs;
+      uint16_t* vdst = const_cast<uint16_t*>(vbase) + row * rs;
+      if (lane < 8)
+#pragma unroll
+        for (int cc = 0; cc < CK::NCQ; ++cc)
+          *reinterpret_cast<uint4*>(kdst + 8 * CK::EPV * cc + CK::EPV * (lane & 7)) = kw[cc];
+      if (lane < CK::LPT) *reinterpret_cast<uint4*>(vdst + 8 * (lane % CK::LPT)) = vw;
+    }
+  }
+
+  // ---- wave partials -> LDS -> the range's partial (or the output) ----
+  const int r = lane / CK::LPT;
+#pragma unroll
+  for (int off = CK::LPT; off < kWave; off <<= 1)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float l = wave_sum(lpart[g]);
+    if (lane == 0) {
+      red_ml[wave][g][0] = m[g];
+      red_ml[wave][g][1] = l;
+    }
+  }
+  if (r == 0) {
+    const int dg = lane % CK::LPT;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float4* dst = reinterpret_cast<float4*>(&red_o[wave][g][8 * dg]);
+      dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+      dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * DH; idx += NT) {
+    const int g = idx / DH;
+    const int d = idx % DH;
+    float mx = red_ml[0][g][0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, red_ml[w][g][0]);
+    float ov = 0.0f, lv = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = fast_exp2(red_ml[w][g][0] - mx);
+      ov = fmaf(wt, red_o[w][g][d], ov);
+      lv = fmaf(wt, red_ml[w][g][1], lv);
+    }
+    const long bh = static_cast<long>(b) * Hq + kvh * G + g;
+    if (n_parts == 1) {
+      a.out[bh * DH + d] = ov * (1.0f / lv);
+    } else {
+      const long ps = bh * a.max_splits + part;
+      a.part_o[ps * DH + d] = ov;
+      if (d == 0) {
+        a.part_ml[ps * 2] = mx;
+        a.part_ml[ps * 2 + 1] = lv;
+      }
+    }
+  }
+}
+
 // Split merge: one workgroup per (stream, q head), after the split kernel; thread d owns
 // output dim d.  Splits' maxima, sums and partial rows are loaded 17 at a time and folded in
 // with an online max; the next 17 are in flight while the current ones are folded, so up to
@@ -695,6 +895,25 @@ int launch_kv(const DecodeArgs& args, int B, int Dh, int G, int split, hipStream
   return launch_dh_g<64, 4, KV>(args, B, split, stream);
 }
 
+template <int DH, int G>
+int launch_wide(const DecodeArgs& args, int B, int split_len, hipStream_t stream) {
+  const dim3 grid(args.Hkv, B, args.max_splits);
+  hipEvent_t ev0, ev_split, ev1;
+  take_timing_events(&ev0, &ev_split, &ev1);
+  if (ev0) (void)hipEventRecord(ev0, stream);
+  hipLaunchKernelGGL((gqa_decode_wide_kernel<DH, G>), grid, dim3(64 * kWideWaves), 0, stream,
+                     args, split_len);
+  int rc = check_launch("gqa_decode_wide_kernel");
+  if (ev_split) (void)hipEventRecord(ev_split, stream);
+  if (!rc && args.max_splits > 1) {
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(DH), 0,
+                       stream, args, split_len, args.Hkv * G);
+    rc = check_launch("gqa_decode_combine_kernel");
+  }
+  if (ev1) (void)hipEventRecord(ev1, stream);
+  return rc;
+}
+
 }  // namespace
 
 // Split length: 128 keys (one 32-key chunk per wave, 117 VGPRs, 4 waves/SIMD), measured
@@ -739,7 +958,20 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
     if (static_cast<long>(p.max_pages) * p.page_size < p.capacity)
       return fail(ORATOR_ERR_CAPACITY, "gqa_decode: capacity exceeds max_pages*page_size");
   }
-  const int split = choose_split(p.B, p.Hkv, G, p.capacity);
+  // Many streams: the wide kernel (a few long ranges per (stream, kv head), one workgroup
+  // each, enough ranges to give every CU a workgroup); otherwise 128-key splits.
+  const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const long pairs = static_cast<long>(p.B) * p.Hkv;
+  int wide_parts = static_cast<int>(std::max<long>((cus + pairs - 1) / pairs,
+                                                   (p.capacity + kWideMaxChunks * 256 - 1) /
+                                                       (kWideMaxChunks * 256)));
+  const int wide_len = ((p.capacity + wide_parts - 1) / wide_parts + 31) / 32 * 32;
+  wide_parts = (p.capacity + wide_len - 1) / wide_len;
+  // Ranges of >= 1536 keys (>= 6 chunks per wave): at B = 16 the wide kernel measured 50.5-51.6
+  // us per op against 52.9 at 4096 keys, but 19.7 / 29.7 against 18.3 / 29.2 us at 1024 / 2048
+  // (2 / 4 chunks per wave: its ramp and tail are not amortised).
+  const bool wide = !p.kv_f32 && p.pos_mode == 0 && !p.q_norm && G <= 2 && wide_len >= 1536;
+  const int split = wide ? wide_len : choose_split(p.B, p.Hkv, G, p.capacity);
   const int max_splits = (p.capacity + split - 1) / split;
   if (max_splits > 1024) return fail(ORATOR_ERR_CAPACITY, "gqa_decode: more than 1024 splits");
   const size_t part_o = static_cast<size_t>(p.B) * p.Hq * max_splits * p.Dh * sizeof(float);
@@ -784,6 +1016,13 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   args.rope = p.rope;
   args.eps = p.eps;
 
+  if (wide) {
+    if (p.Dh == 128)
+      return G == 1 ? launch_wide<128, 1>(args, p.B, split, stream)
+                    : launch_wide<128, 2>(args, p.B, split, stream);
+    return G == 1 ? launch_wide<64, 1>(args, p.B, split, stream)
+                  : launch_wide<64, 2>(args, p.B, split, stream);
+  }
   if (p.kv_f32) return launch_kv<float>(args, p.B, p.Dh, G, split, stream);
   return launch_kv<uint16_t>(args, p.B, p.Dh, G, split, stream);
 }

@@ -94,6 +94,42 @@ def test_append_paged_ragged_streams(lens):
     np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp_ref)
 
 
+# The wide split kernel (many streams and long contexts: each (stream, kv head) cut into two
+# ranges of 2080 keys at this capacity, 8 waves striding over 32-key chunks): appended keys at
+# the range boundary (lens 2080 / 2081: the new key is the last key of range 0 / the only key
+# of range 1), at chunk edges (32, 33, 2112), at the capacity (4160), and one-key streams.
+WIDE_LENS = [2080, 2081, 2079, 4160, 1, 32, 33, 2112, 4097, 3000, 64, 4159, 2, 1500, 4128, 2047]
+
+
+@pytest.mark.parametrize("Hq,Hkv,Dh", [(16, 8, 128), (8, 8, 128), (16, 8, 64)])
+def test_append_paged_wide_ranges(Hq, Hkv, Dh):
+    ps = 16
+    lens = WIDE_LENS
+    r = SplitMix64(Hq * 100 + Dh)
+    B = len(lens)
+    max_pages = max((n + ps - 1) // ps for n in lens)
+    n_pages = B * max_pages + 2
+    kp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    vp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    table = np.array(r.uniform(n_pages).argsort(), np.int32)[:B * max_pages].reshape(B, max_pages)
+    q, kn, vn = r.normal((B, Hq, Dh)), r.normal((B, Hkv, Dh)), r.normal((B, Hkv, Dh))
+    pos = np.array(lens, np.int32) - 1
+    scale = 1.0 / math.sqrt(Dh)
+    kp_ref, vp_ref = kp.copy(), vp.copy()
+    for b in range(B):
+        orc.kv_write_paged(kn[b][None], vn[b][None], kp_ref, vp_ref, table[b], ps, int(pos[b]))
+    ref = orc.gqa_decode_paged(q, kp_ref, vp_ref, table, ps, pos, scale, threads=8)
+    dk, dv = up(kp), up(vp)
+    dout = empty((B, Hq, Dh), np.float32)
+    say("append paged wide", Hq, Hkv, Dh)
+    da.GqaDecodeAttnAppendPaged(up(q), up(kn), up(vn), dk, dv, up(table), max_pages, ps, n_pages,
+                                up(pos), dout, B, Hq, Hkv, Dh, scale)
+    check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+               truth=t64.decode_paged(q, kp_ref, vp_ref, table, ps, pos, scale))
+    np.testing.assert_array_equal(down(dk, kp.shape, np.uint16), kp_ref)
+    np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp_ref)
+
+
 def test_append_equals_write_then_decode_on_device():
     """Same inputs through orator_kv_write_paged + orator_gqa_decode_paged: same cache bits,
     outputs equal to fp32 rounding (the appended key is folded in last)."""

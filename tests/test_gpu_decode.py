@@ -119,6 +119,26 @@ def test_decode_paged_ragged_streams(lens):
                truth=t64.decode_paged(q, kp, vp, table, ps, pos, scale))
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,Dh", [(16, 16, 8, 128), (32, 16, 8, 128), (16, 8, 8, 64)])
+def test_decode_paged_wide_ranges(B, Hq, Hkv, Dh):
+    """Many streams over long contexts take the wide split kernel (two 2080-key ranges per
+    (stream, kv head) at 16 streams, one whole-context range at 32): ragged lengths around the
+    range and chunk edges."""
+    base = [2080, 2081, 2079, 4160, 1, 32, 33, 2112, 4097, 3000, 64, 4159, 2, 1500, 4128, 2047]
+    lens = (base * 2)[:B]
+    ps = 16
+    q, kp, vp, table, pos = _paged_case(B * 7 + Dh, lens, Hq=Hq, Hkv=Hkv, Dh=Dh)
+    B, max_pages = table.shape
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_decode_paged(q, kp, vp, table, ps, pos, scale, threads=8)
+    dout = empty((B, Hq, Dh), np.float32)
+    say("decode paged wide", B, Hq, Hkv, Dh)
+    da.GqaDecodeAttnPaged(up(q), up(kp), up(vp), up(table), max_pages, ps, up(pos), dout, B, Hq,
+                          Hkv, Dh, scale)
+    check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+               truth=t64.decode_paged(q, kp, vp, table, ps, pos, scale))
+
+
 def test_decode_paged_equals_contiguous_for_identity_table():
     Hq, Hkv, Dh, ps, S = 16, 8, 128, 16, 1000
     q, kc, vc = _contig_case(12, S, 1024)
