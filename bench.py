@@ -160,6 +160,26 @@ def run_decode(steps: int, warmup: int):
     op_bytes = step_bytes / n_ops
     achieved = op_bytes / (avg_ms / 1e3) / 1e9
 
+    # ---- the access pattern's streaming ceiling: the same K/V bytes of every layer read by
+    # the read probe (the decode grid and loads, no arithmetic, no partials, no merge) ----
+    S_last = L_BASE + warmup + steps
+    sink = DeviceBuffer(4)
+    probe = lambda l: call("orator_decode_read_probe", kpools[l].ptr, vpools[l].ptr,
+                           tables[l].ptr, max_pages, PAGE, S_last, B, HKV, sink.ptr,
+                           stream.handle)
+    for l in range(LAYERS):
+        probe(l)
+    stream.synchronize()
+    p0, p1 = Event(), Event()
+    p0.record(stream)
+    for r in range(2):
+        for l in range(LAYERS):
+            probe(l)
+    p1.record(stream)
+    stream.synchronize()
+    probe_us = p0.elapsed_ms(p1) * 1e3 / (2 * LAYERS)
+    probe_gbs = B * 2 * S_last * HKV * DH * 2 / (probe_us * 1e-6) / 1e9
+
     # ---- spot parity of the last launch against the oracle (stream 0..1, layer 27) ----
     parity = spot_check(kpools[-1], vpools[-1], tables[-1], max_pages, qs, outs,
                         L_BASE + warmup + steps - 1, (warmup + steps - 1) % n_var, scale)
@@ -168,6 +188,7 @@ def run_decode(steps: int, warmup: int):
         "value_gbs": value_gbs, "kernel_avg_us": avg_ms * 1e3,
         "kernel_bytes": op_bytes, "achieved_gbs": achieved,
         "max_pages": max_pages, "parity": parity,
+        "read_probe_us": probe_us, "read_probe_gbs": probe_gbs,
     }
 
 
@@ -634,7 +655,8 @@ def main():
     copy = run_copy_bandwidth()
     log("copy:", copy)
     log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value_gbs']:.1f} GB/s; op "
-        f"{dec['kernel_avg_us']:.1f} us avg -> {dec['achieved_gbs']:.1f} GB/s; parity {dec['parity']}")
+        f"{dec['kernel_avg_us']:.1f} us avg -> {dec['achieved_gbs']:.1f} GB/s; read probe "
+        f"{dec['read_probe_us']:.1f} us ({dec['read_probe_gbs']:.1f} GB/s); parity {dec['parity']}")
     from orator_amd import decoder_attn as da
     pre = [run_prefill(503, da.PREFILL_BF16), run_prefill(503, da.PREFILL_FP32),
            run_prefill(2048, da.PREFILL_BF16), run_prefill(2048, da.PREFILL_FP32)]
@@ -672,14 +694,21 @@ def main():
                      # (split + merge kernels) at this workload, S = 4102.
                      "traffic": HBM_TRAFFIC_PER_OP,
                      "traffic_over_algorithmic": round(HBM_TRAFFIC_PER_OP / ALGORITHMIC_AT_TRAFFIC, 3),
-                     "kernel": "decode op = gqa_decode_kernel (split-K, 128-key splits) + "
-                               "gqa_decode_combine_kernel (split merge); average over the "
+                     "kernel": "decode op = gqa_decode_wide_kernel (each stream and kv head cut "
+                               "into two ~2070-key ranges, one 8-wave workgroup each) + "
+                               "gqa_decode_combine_kernel (range merge); average over the "
                                "timed region's back-to-back ops (HIP events on its stream)",
                      "kernel_avg_us": round(dec["kernel_avg_us"], 2),
                      "bytes_per_launch": int(dec["kernel_bytes"]),
                      "attainable_copy_gbs": copy["GBs_read_plus_write"],
                      "frac_of_attainable_copy": round(dec["achieved_gbs"] /
-                                                      copy["GBs_read_plus_write"], 4)},
+                                                      copy["GBs_read_plus_write"], 4),
+                     # the same K/V bytes read with the decode kernels' access pattern and
+                     # nothing else (orator_decode_read_probe over the 28 layers' pools)
+                     "attainable_read_gbs": round(dec["read_probe_gbs"], 1),
+                     "read_probe_us": round(dec["read_probe_us"], 2),
+                     "frac_of_attainable_read": round(dec["achieved_gbs"] /
+                                                      dec["read_probe_gbs"], 4)},
         "cpu_baseline": cpu,
         "parity": dec["parity"],
         "prefill": pre,

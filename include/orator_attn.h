@@ -162,6 +162,13 @@ int orator_gqa_decode_paged(const float* q, const uint16_t* kpool, const uint16_
                             const int* page_table, int max_pages, int page_size,
                             const int* d_pos, float* out, int B, int Hq, int Hkv, int Dh,
                             float scale, void* stream);
+/* Measurement hook (no reference counterpart): reads the K/V bytes of a paged decode over S keys
+ * per stream (head_dim 128, bf16, the first ceil(S / page_size) entries of each table row
+ * mapped) with the decode kernels' access pattern and nothing else, so its time is that
+ * pattern's streaming ceiling.  `sink`: a 4-byte device word the kernel may write. */
+int orator_decode_read_probe(const uint16_t* kpool, const uint16_t* vpool, const int* page_table,
+                             int max_pages, int page_size, int S, int B, int Hkv,
+                             unsigned* sink, void* stream);
 /* No counterpart in the reference: orator_gqa_decode_paged for callers that cannot allocate
  * (code under HIP graph capture, serving loops that forbid hipMalloc).  Same arguments and
  * results; the split partials live in a static 16 MiB device array per GPU instead of the

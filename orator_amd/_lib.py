@@ -123,6 +123,7 @@ SIGNATURES: dict[str, list] = {
     "orator_gqa_decode": [_p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p],
     "orator_gqa_decode_paged": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
     "orator_gqa_decode_paged_noalloc": [_p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+    "orator_decode_read_probe": [_p, _p, _p, _i, _i, _i, _i, _i, _p, _p],
     "orator_gqa_decode_append_qknorm": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _i, _f, _p, _p,
                                         _f, _p, _i, _p],
     "orator_gqa_decode_append_qknorm_paged": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _i, _i,

@@ -766,6 +766,40 @@ void gqa_decode_wide_kernel(DecodeArgs a, int split_len) {
   }
 }
 
+// Measurement: the decode operation's K/V bytes read with nothing else (no arithmetic, no
+// partials, no merge): grid (kv head, stream, 128-key split), 4 waves, each wave one 32-key
+// chunk of K and of V through the page table with the non-temporal loads the decode kernels
+// use.  Its time is the streaming ceiling of this access pattern on the device.
+__global__ __launch_bounds__(256) void decode_read_probe_kernel(const uint16_t* __restrict__ kp,
+                                                                const uint16_t* __restrict__ vp,
+                                                                const int* __restrict__ table,
+                                                                int max_pages, int page_shift,
+                                                                int S, int Hkv,
+                                                                unsigned* __restrict__ sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int c0 = (blockIdx.z * 4 + wave) * 32;  // first key of the wave's chunk
+  if (c0 >= S) return;
+  const int last = S - 1;
+  const int* pt = table + static_cast<long>(b) * max_pages;
+  const long rs = static_cast<long>(Hkv) * 128;
+  const int sub = lane >> 4, ch = lane & 15;  // 4 keys x 16 pieces of 16 bytes per load
+  unsigned acc = 0;
+  uint4 kv[8], vv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int key = min(c0 + 4 * i + sub, last);
+    const long row = static_cast<long>(pt[key >> page_shift]) * (1L << page_shift) +
+                     (key & ((1 << page_shift) - 1));
+    const long off = row * rs + kvh * 128 + 8 * ch;
+    kv[i] = load_nt(kp + off);
+    vv[i] = load_nt(vp + off);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc ^= kv[i].x ^ kv[i].w ^ vv[i].y ^ vv[i].z;
+  if (acc == 0x9e3779b9u && lane == 0) sink[0] = acc;  // keeps the loads; practically never
+}
+
 // Split merge: one workgroup per (stream, q head), after the split kernel; thread d owns
 // output dim d.  Splits' maxima, sums and partial rows are loaded 17 at a time and folded in
 // with an online max; the next 17 are in flight while the current ones are folded, so up to
@@ -1295,6 +1329,26 @@ int orator_gqa_attention(const float* q, const float* k, const float* v, float* 
   p.capacity = T;
   p.scale = scale;
   return launch_gqa_decode(p, nullptr);
+}
+
+// Measurement hook (no reference counterpart): the streaming-read ceiling of the paged decode
+// access pattern, S keys per stream (head_dim 128, bf16, every page of the first ceil(S /
+// page_size) table entries mapped).  `sink` is a 4-byte device word the kernel may write.
+int orator_decode_read_probe(const uint16_t* kpool, const uint16_t* vpool, const int* page_table,
+                             int max_pages, int page_size, int S, int B, int Hkv,
+                             unsigned* sink, void* stream) {
+  if (S <= 0 || B <= 0 || Hkv <= 0) return ORATOR_OK;
+  if (!kpool || !vpool || !page_table || !sink)
+    return fail(ORATOR_ERR_INVALID, "decode_read_probe: null pointer");
+  const int shift = ilog2_exact(page_size);
+  if (shift < 4) return fail(ORATOR_ERR_INVALID, "decode_read_probe: page_size must be 2^k >= 16");
+  if (static_cast<long>(max_pages) * page_size < S)
+    return fail(ORATOR_ERR_CAPACITY, "decode_read_probe: S exceeds max_pages * page_size");
+  if (B > 65535) return fail(ORATOR_ERR_UNSUPPORTED, "decode_read_probe: at most 65535 streams");
+  const dim3 grid(Hkv, B, (S + 127) / 128);
+  hipLaunchKernelGGL(decode_read_probe_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     kpool, vpool, page_table, max_pages, shift, S, Hkv, sink);
+  return check_launch("decode_read_probe_kernel");
 }
 
 // WindowAttnKernel (src/model/asr_audio_tower.cu:204-258): audio-tower self-attention, q/k/v

@@ -275,12 +275,59 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
   uint16_t* const vt = reinterpret_cast<uint16_t*>(wl);   // V tile [32][kVRowH]
   float* const rt = reinterpret_cast<float*>(wl + kVBytes);  // R^T [32][kRtRow]
 
+  const int n_tiles = (a.valid + 31) / 32;
+  const int P = 2 * T - 1;
+
+  // One tile's global operands, row-contiguous (8 lanes per 128-byte row): V and K rows
+  // j0 .. j0+31 and the P window base .. base+63.  Loaded through buffer resources whose
+  // range is the tensor: rows outside [0, T) / [0, P) read as zeros with no branch, so the
+  // compiler can count the next tile's loads and wait only for the current one's.
+  constexpr int kES = sizeof(IN);
+  const int row_bytes = static_cast<int>(rs) * kES;
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<IN*>(kp), 0, T * row_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<IN*>(vp), 0, T * row_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t prs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<IN*>(pp), 0, P * row_bytes, 0x00020000);
+  struct Tile {
+    uint4 v[4], k[4], p[8];
+  };
+  const int dcv = lane & 7, rv = lane >> 3;
+  const int lane_off = rv * row_bytes + (h * kRpDk + 8 * dcv) * kES;
+  auto bload8 = [&](__amdgpu_buffer_rsrc_t r, int off) -> uint4 {
+    if constexpr (kES == 2) {
+      return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    } else {
+      const float4 x = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+      const float4 y = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0));
+      return make_uint4(pack_h2(x.x, x.y), pack_h2(x.z, x.w), pack_h2(y.x, y.y), pack_h2(y.z, y.w));
+    }
+  };
+  auto load_kp = [&](Tile& t, int n) {
+    const int j0 = 32 * n;
+    const int base = T - 1 - (i0 + 31) + j0;  // may be negative: those rows read zeros
+#pragma unroll
+    for (int it = 0; it < 4; ++it) t.k[it] = bload8(krs, (j0 + 8 * it) * row_bytes + lane_off);
+#pragma unroll
+    for (int it = 0; it < 8; ++it) t.p[it] = bload8(prs, (base + 8 * it) * row_bytes + lane_off);
+  };
+  auto load_v = [&](Tile& t, int n) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+      t.v[it] = bload8(vrs, (32 * n + 8 * it) * row_bytes + lane_off);
+  };
+  // the wave's first tile is in flight while q is staged
+  Tile t;
+  if (wave < n_tiles) {
+    load_kp(t, wave);
+    load_v(t, wave);
+  }
+
   // (q_i + u) and (q_i + v) of the workgroup's 32 queries, formed once with row-contiguous
   // loads (8 lanes per row), staged in LDS ([2][32][kStRow]), and read back as this lane's B
   // operand per 16-dim k-step.  (A lane per query row, in every wave, touched a cache line
   // per lane and load.)
-  const int qi = i0 + col;
-  const bool q_ok = qi < T;
   uint4 qu[4], qv[4];
   {
     uint16_t* qst = reinterpret_cast<uint16_t*>(lds);
@@ -315,39 +362,13 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
   float m = -INFINITY, lsum = 0.0f;
-  const int n_tiles = (a.valid + 31) / 32;
-  const int P = 2 * T - 1;
-
-  // One tile's global operands, row-contiguous (8 lanes per 128-byte row): V and K rows
-  // j0 .. j0+31 and the P window base .. base+63 (zeros outside [0, T) / [0, P)).  The next
-  // tile's operands are loaded before the current one is processed.
-  struct Tile {
-    uint4 v[4], k[4], p[8];
-  };
-  const int dcv = lane & 7, rv = lane >> 3;
-  auto load_tile = [&](Tile& t, int n) {
-    const int j0 = 32 * n;
-    const int base = T - 1 - (i0 + 31) + j0;
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int j = j0 + 8 * it + rv;
-      t.v[it] = j < T ? load8_h(vp + j * rs + h * kRpDk + 8 * dcv) : make_uint4(0, 0, 0, 0);
-      t.k[it] = j < T ? load8_h(kp + j * rs + h * kRpDk + 8 * dcv) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const int pr = base + 8 * it + rv;
-      t.p[it] = (pr >= 0 && pr < P) ? load8_h(pp + static_cast<long>(pr) * rs + h * kRpDk + 8 * dcv)
-                                    : make_uint4(0, 0, 0, 0);
-    }
-  };
   const int tg = lane >> 4, ts = lane & 15;
   const uint16_t* vsrc0 = vt + (4 * (tg >> 1) + (ts >> 2)) * kVRowH + 16 * (tg & 1) + 4 * (ts & 3);
-  // tile n + W's operands are in flight while tile n is processed
-  Tile cur, nxt;
-  if (wave < n_tiles) load_tile(cur, wave);
-  for (int n = wave; n < n_tiles; n += kRpWaves) {
-    if (n + kRpWaves < n_tiles) load_tile(nxt, n + kRpWaves);
+  const float c = a.scale_log2e;
+  // One register set per wave: the next tile's K and P rows are loaded as soon as this tile's
+  // are in LDS, its V rows as soon as this tile's V is, so each load is in flight under the
+  // rest of the tile's work.
+  auto process = [&](Tile& cur, int n, int next) {
     const int j0 = 32 * n;
     wave_lds_sync();  // the previous tile's LDS reads precede this tile's writes
     // K rows and the P window -> wave-private LDS; MFMA A fragments (row j0 + col / base +
@@ -358,6 +379,7 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
 #pragma unroll
     for (int it = 0; it < 8; ++it)
       *reinterpret_cast<uint4*>(pst + (8 * it + rv) * kStRow + 8 * dcv) = cur.p[it];
+    if (next < n_tiles) load_kp(cur, next);
     wave_lds_sync();
     uint4 kf[4], pf0[4], pf1[4];
 #pragma unroll
@@ -368,11 +390,11 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
       pf1[ks] = *reinterpret_cast<const uint4*>(pst + (32 + col) * kStRow + d0);
     }
     wave_lds_sync();  // the fragments are read before V and R^T overwrite the staging
-    // V tile -> wave-private LDS, row-major (one 16-byte store per row piece); the PV
-    // operand V^T is read back with transposing reads
+    // V tile -> wave-private LDS, row-major; the PV operand V^T is read back transposed
 #pragma unroll
     for (int it = 0; it < 4; ++it)
       *reinterpret_cast<uint4*>(vt + (8 * it + rv) * kVRowH + 8 * dcv) = cur.v[it];
+    if (next < n_tiles) load_v(cur, next);
     // AC^T and R = P_window (q + v)^T
     f32x16_t s, r0, r1;
 #pragma unroll
@@ -391,15 +413,14 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
       rt[col * kRtRow + 32 + rr] = r1[e];
     }
     wave_lds_sync();  // R^T and V written by all lanes before any lane reads them
-    // scores: (AC + BD) * scale, key mask j >= valid, padding query columns masked
-    // (the uniform case is decided once per tile: as a per-element select it became a branch
-    // around every band read, 16 serialized LDS round trips)
+    // scores (log2 units): (AC + BD) * scale; keys >= valid masked on the one tile that
+    // holds them (padding query columns carry zero q rows: finite, never stored)
     float tmax = -INFINITY;
     if (a.uniform) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
-        const float x = (q_ok && j0 + jl < a.valid) ? 0.0f : -INFINITY;
+        const float x = j0 + jl < a.valid ? 0.0f : -INFINITY;
         s[e] = x;
         tmax = fmaxf(tmax, x);
       }
@@ -409,19 +430,31 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
       for (int e = 0; e < 16; ++e)
         bd[e] = rt[col * kRtRow + 8 * (e >> 2) + 4 * h2 + (e & 3) - col + 31];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
-        const float x = (q_ok && j0 + jl < a.valid) ? (s[e] + bd[e]) * a.scale_log2e : -INFINITY;
-        s[e] = x;
-        tmax = fmaxf(tmax, x);
+      for (int e = 0; e < 16; ++e) s[e] = (s[e] + bd[e]) * c;
+      if (j0 + 32 > a.valid) {  // uniform over the workgroup
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
+          if (j0 + jl >= a.valid) s[e] = -INFINITY;
+        }
       }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[e]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float mn = fmaxf(m, tmax);
-    const float mref = mn == -INFINITY ? 0.0f : mn;
-    const float corr = fast_exp2(m - mref);
-    m = mn;
-    float psum = 0.0f;
+    // reference max moved (and O, l rescaled) only when a score exceeds it by more than 2^8:
+    // weights stay <= 256 (exact in fp16's range), and most tiles skip the rescale
+    if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f)) {
+      const float mn = fmaxf(m, tmax);
+      const float corr = m == -INFINITY ? 0.0f : fast_exp2(m - mn);
+      m = mn;
+      lsum *= corr;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+    }
+    const float mref = m == -INFINITY ? 0.0f : m;
     uint4 pk[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -429,16 +462,11 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         pv[e] = fast_exp2(s[8 * st + e] - mref);
-        psum += pv[e];
+        lsum += pv[e];
       }
       pk[st] = make_uint4(pack_h2(pv[0], pv[1]), pack_h2(pv[2], pv[3]), pack_h2(pv[4], pv[5]),
                           pack_h2(pv[6], pv[7]));
     }
-    lsum = lsum * corr + psum;
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
     // A operand of O^T += V^T P^T: row = dim 32 dt + col, k = keys 16 st + 4 h2 + 8 (e / 4) +
     // e % 4, by ds_read_b64_tr_b16 of the row-major tile (16-lane group g covers dims
     // 16 (g & 1) .. of the 32-dim block and keys 4 (g >> 1) .., +8 for the second half)
@@ -452,8 +480,8 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(make_uint4(v0.x, v0.y, v1.x, v1.y)),
                                                        as_f16x8(pk[st]), o[dt], 0, 0, 0);
       }
-    cur = nxt;
-  }
+  };
+  for (int n = wave; n < n_tiles; n += kRpWaves) process(t, n, n + kRpWaves);
 
   // ---- merge the waves' partial softmax states ----
   lsum += __shfl_xor(lsum, 32);
@@ -502,6 +530,9 @@ int orator_relpos_attention_fast(const void* q, const void* k, const void* v, co
   if (Dk != kRpDk) return fail(ORATOR_ERR_UNSUPPORTED, "relpos_attention_fast: Dk must be 64");
   if (in_f16 < 0 || in_f16 > 2)
     return fail(ORATOR_ERR_INVALID, "relpos_attention_fast: in_f16 must be 0, 1 or 2");
+  // rows are addressed with 32-bit byte offsets (buffer loads): the P tensor [2T-1][H][64]
+  if (static_cast<long>(2 * T) * H * kRpDk * 4 >= (1L << 31))
+    return fail(ORATOR_ERR_UNSUPPORTED, "relpos_attention_fast: (2T-1) * H * 64 * 4 >= 2^31");
   // The reference masks keys >= valid_len with a finite -1e30 (conformer_layer.cu:140-143):
   // with no valid key every score is the same and the softmax averages V over all T keys.
   const bool none_valid = valid_len <= 0;
