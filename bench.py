@@ -41,11 +41,11 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
 
 LAYERS, B, HQ, HKV, DH, L_BASE, PAGE = 28, 16, 16, 8, 128, 4096, 16
-# HBM bytes per decode op measured with rocprofv3 --pmc at S = 4102 (FETCH_SIZE x 1.994 KiB +
-# WRITE_SIZE KiB, profiles/decode_b16_l4096_hbm_traffic.md) and the algorithmic bytes of the
-# same op, for the traffic / algorithmic ratio
-HBM_TRAFFIC_PER_OP = 277.8e6
-ALGORITHMIC_AT_TRAFFIC = 269.1e6
+# HBM bytes per decode op measured with rocprofv3 --pmc at S = 4097..4105 (FETCH_SIZE x 1.9943
+# KiB + WRITE_SIZE KiB, profiles/decode_b16_l4096_hbm_traffic.md) and the algorithmic bytes of
+# the same ops, for the traffic / algorithmic ratio
+HBM_TRAFFIC_PER_OP = 269.40e6
+ALGORITHMIC_AT_TRAFFIC = 269.04e6
 
 
 def parse():
@@ -690,8 +690,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4),
-                     # rocprofv3 FETCH_SIZE x 1.993 + WRITE_SIZE x 1.0 KiB per decode op
-                     # (split + merge kernels) at this workload, S = 4102.
+                     # rocprofv3 FETCH_SIZE x 1.9943 + WRITE_SIZE x 1.0 KiB per decode op
+                     # (wide split + merge kernels) at this workload, S = 4097..4105.
                      "traffic": HBM_TRAFFIC_PER_OP,
                      "traffic_over_algorithmic": round(HBM_TRAFFIC_PER_OP / ALGORITHMIC_AT_TRAFFIC, 3),
                      "kernel": "decode op = gqa_decode_wide_kernel (each stream and kv head cut "
