@@ -19,10 +19,13 @@
 //    probabilities move to the PV layout with one lane shuffle per key row.
 //  * PV, "row" layout: Dh/8 lanes per key, one 16-byte load each (whole contiguous rows
 //    per instruction); per-lane accumulators hold 8 dims x G heads.
-//  * waves merge in LDS at the end; splits are merged by a second small kernel (one memory
-//    round trip for up to 16 splits: all loads issued together, online max).  (A
-//    last-workgroup merge in the same launch needs a device-scope release fence per
-//    workgroup -- an L2 write-back on gfx950 -- and measured 7-10x slower.)
+//  * waves merge in LDS at the end.  Splits are merged either by a second small kernel (one
+//    memory round trip for up to 34 splits: loads issued together, online max), or, for
+//    small grids, inside the split launch by the last workgroup of each (stream, kv head)
+//    to finish: partials written and read as agent-scope atomics (coherent across the XCDs'
+//    L2s without the L2 write-back a device-scope release fence costs, which measured 7-10x
+//    slower) and an arrival counter.  One launch instead of two is what a single stream
+//    gains most from.
 //  * paged KV: each wave reads the two page-table entries of its chunk with uniform loads
 //    at entry, together with the stream's position; no workgroup-wide table and no barrier
 //    stand between the entry and the K/V loads.  Keys past the range load the last valid
@@ -54,6 +57,9 @@ struct DecodeArgs {
   float* out;
   float* part_o;       // [B*Hq][max_splits][DH]
   float* part_ml;      // [B*Hq][max_splits][2]
+  // [B*Hkv] arrival counters, zero between launches: when set, the split kernel's last
+  // workgroup of each (stream, kv head) merges the splits (no second launch)
+  unsigned* arrive;
   long stream_stride;
   int max_pages;
   int page_shift;
@@ -339,6 +345,89 @@ __device__ __forceinline__ void append_key(const float* kn, const float* vn,
   }
 }
 
+// ---- split merge: the combine kernel, or the split kernel's last workgroup ----
+// Splits' maxima, sums and partial rows are loaded kSplitBatch at a time and folded in with an
+// online max; the next batch is in flight while the current one is folded, so up to 34
+// splits (4352 keys at 128-key splits) cost one memory round trip.
+constexpr int kSplitBatch = 17;
+struct SplitBatch {
+  float m[kSplitBatch], l[kSplitBatch], o[kSplitBatch];
+};
+
+// Device-coherent (agent-scope) float store and load.  The XCDs' L2 caches are not coherent
+// with each other; agent-scope atomic accesses are (the store is complete at the coherent
+// level once the wave's store counter has drained, the load reads that level), without the
+// L2 write-back an agent-scope release fence costs.
+__device__ __forceinline__ void store_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Splits s0 .. s0 + kSplitBatch - 1 of partial row `base` (= (stream * Hq + q head) *
+// max_splits), dim d.  Slots past the launch's splits are clamped to its last (an in-range
+// address); slots past the stream's splits hold stale data and are excluded by the fold's
+// selects.  DEV: device-coherent loads (partials written by other workgroups of this launch).
+template <int DH, bool DEV>
+__device__ __forceinline__ void load_splits(SplitBatch& x, const DecodeArgs& a, long base, int s0,
+                                            int d) {
+#pragma unroll
+  for (int i = 0; i < kSplitBatch; ++i) {
+    const long ps = base + min(s0 + i, a.max_splits - 1);
+    if constexpr (DEV) {
+      x.m[i] = load_dev(a.part_ml + ps * 2);
+      x.l[i] = load_dev(a.part_ml + ps * 2 + 1);
+      x.o[i] = load_dev(a.part_o + ps * DH + d);
+    } else {
+      x.m[i] = a.part_ml[ps * 2];
+      x.l[i] = a.part_ml[ps * 2 + 1];
+      x.o[i] = a.part_o[ps * DH + d];
+    }
+  }
+}
+
+__device__ __forceinline__ void fold_splits(const SplitBatch& x, int s0, int n_splits, float& M,
+                                            float& L, float& acc) {
+  float mx = M;
+#pragma unroll
+  for (int i = 0; i < kSplitBatch; ++i)
+    if (s0 + i < n_splits) mx = fmaxf(mx, x.m[i]);
+  const float c_old = M == mx ? 1.0f : fast_exp2(M - mx);
+  acc *= c_old;
+  L *= c_old;
+#pragma unroll
+  for (int i = 0; i < kSplitBatch; ++i) {
+    if (s0 + i < n_splits) {
+      const float w = fast_exp2(x.m[i] - mx);
+      acc = fmaf(w, x.o[i], acc);
+      L = fmaf(w, x.l[i], L);
+    }
+  }
+  M = mx;
+}
+
+// The merged output of dim d over n_splits (>= 2) splits; A holds splits 0 .. kSplitBatch - 1
+// (loaded by the caller, so its loads can go out before n_splits is known).
+template <int DH, bool DEV>
+__device__ __forceinline__ float merge_splits(const DecodeArgs& a, long base, int d, int n_splits,
+                                              SplitBatch& A) {
+  SplitBatch Bb;
+  float M = -INFINITY, L = 0.0f, acc = 0.0f;
+  // ping-pong: the next batch's loads are issued before the current one is folded
+  for (int s0 = 0;;) {
+    if (s0 + kSplitBatch < n_splits) load_splits<DH, DEV>(Bb, a, base, s0 + kSplitBatch, d);
+    fold_splits(A, s0, n_splits, M, L, acc);
+    s0 += kSplitBatch;
+    if (s0 >= n_splits) break;
+    if (s0 + kSplitBatch < n_splits) load_splits<DH, DEV>(A, a, base, s0 + kSplitBatch, d);
+    fold_splits(Bb, s0, n_splits, M, L, acc);
+    s0 += kSplitBatch;
+    if (s0 >= n_splits) break;
+  }
+  return acc * (1.0f / L);
+}
+
 // Waves per split workgroup: bf16 splits of 256 / 512 keys give every wave one 32-key
 // chunk (8 / 16 waves); otherwise 4 waves.
 template <int SPLIT, typename KV, int G>
@@ -346,7 +435,9 @@ constexpr int decode_waves() {
   return (sizeof(KV) == 2 && G <= 2 && SPLIT >= 256 && SPLIT <= 512) ? SPLIT / 32 : 4;
 }
 
-template <int DH, int G, int SPLIT, typename KV, bool QKN>
+// FUSE: the splits are merged by the last workgroup of each (stream, kv head) to finish
+// (a.arrive set), else by the combine kernel.
+template <int DH, int G, int SPLIT, typename KV, bool QKN, bool FUSE>
 __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__((
     amdgpu_waves_per_eu(2))) void gqa_decode_kernel(DecodeArgs a) {
   static_assert(!QKN || (DH == 128 && sizeof(KV) == 2), "QK-norm folding: Dh 128, bf16 caches");
@@ -558,11 +649,49 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
       a.out[bh * DH + d] = ov * (1.0f / lv);
     } else {
       const long ps = bh * a.max_splits + split;
-      a.part_o[ps * DH + d] = ov;
-      if (d == 0) {
-        a.part_ml[ps * 2] = mx;
-        a.part_ml[ps * 2 + 1] = lv;
+      if constexpr (FUSE) {
+        store_dev(a.part_o + ps * DH + d, ov);
+        if (d == 0) {
+          store_dev(a.part_ml + ps * 2, mx);
+          store_dev(a.part_ml + ps * 2 + 1, lv);
+        }
+      } else {
+        a.part_o[ps * DH + d] = ov;
+        if (d == 0) {
+          a.part_ml[ps * 2] = mx;
+          a.part_ml[ps * 2 + 1] = lv;
+        }
       }
+    }
+  }
+  if constexpr (FUSE) {
+    if (n_splits == 1) return;
+    // ---- in-launch split merge: the last workgroup of (stream, kv head) to arrive ----
+    // Every thread's partial stores have completed at the coherent level (vmcnt 0) before
+    // the barrier; then one thread counts the workgroup in.  The workgroup whose add brings
+    // the count to n_splits reads the partials (issued after the add returned) and returns
+    // the counter to zero for the next launch.
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      unsigned* ctr = a.arrive + static_cast<long>(b) * a.Hkv + kvh;
+      const unsigned prev =
+          __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev + 1 == static_cast<unsigned>(n_splits);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    for (int idx = tid; idx < G * DH; idx += NT) {
+      const int g = idx / DH;
+      const int d = idx % DH;
+      const long bh = static_cast<long>(b) * Hq + kvh * G + g;
+      const long base = bh * a.max_splits;
+      SplitBatch A;
+      load_splits<DH, true>(A, a, base, 0, d);
+      a.out[bh * DH + d] = merge_splits<DH, true>(a, base, d, n_splits, A);
     }
   }
 }
@@ -800,14 +929,15 @@ __global__ __launch_bounds__(256) void decode_read_probe_kernel(const uint16_t* 
   if (acc == 0x9e3779b9u && lane == 0) sink[0] = acc;  // keeps the loads; practically never
 }
 
+__global__ __launch_bounds__(256) void zero_u32_kernel(unsigned* p) {
+  p[blockIdx.x * 256 + threadIdx.x] = 0u;
+}
+
 // Split merge: one workgroup per (stream, q head), after the split kernel; thread d owns
-// output dim d.  Splits' maxima, sums and partial rows are loaded 17 at a time and folded in
-// with an online max; the next 17 are in flight while the current ones are folded, so up to
-// 34 splits (4352 keys at 128-key splits) cost one memory round trip.
+// output dim d (the split fold above, plain loads).
 template <int DH>
 __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, int split_len,
                                                                 int Hq) {
-  constexpr int kBatch = 17;
   // x = kv head + Hkv * (q head within the group): the kv head is the fastest grid index, as
   // in the split kernel, so with 8 kv heads a head's merge runs on the XCD (workgroup index %
   // 8) that ran its splits.  Measured 0.9 us per op faster than q-head order (B = 16, L = 4096,
@@ -818,24 +948,10 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
   const long bh = static_cast<long>(b) * Hq + h;
   const long base = bh * a.max_splits;
   const int d = threadIdx.x;
-  float M = -INFINITY, L = 0.0f, acc = 0.0f;
-  struct Batch {
-    float m[kBatch], l[kBatch], o[kBatch];
-  };
   // Addresses use the launch's split count, not the stream's, so the first batch goes out
-  // together with the read of the stream's position instead of after it; slots past the
-  // stream's splits hold stale data and are excluded by selects (no arithmetic on them).
-  auto load = [&](Batch& x, int s0) {
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const long ps = base + min(s0 + i, a.max_splits - 1);  // in-range address for every i
-      x.m[i] = a.part_ml[ps * 2];
-      x.l[i] = a.part_ml[ps * 2 + 1];
-      x.o[i] = a.part_o[ps * DH + d];
-    }
-  };
-  Batch A, Bb;
-  load(A, 0);
+  // together with the read of the stream's position instead of after it.
+  SplitBatch A;
+  load_splits<DH, false>(A, a, base, 0, d);
   // the stream's position, read by lane 0 of each wave in a vector load that every thread
   // issues (the others read a zero word): as a uniform load behind the branch for an absent
   // position array, it and the pointer it needs cost two round trips before the batch's row
@@ -846,36 +962,21 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
   const int S = stream_keys(a, b, a.pos_mode == 0 ? __builtin_amdgcn_readlane(pos_ld, 0) : 0);
   const int n_splits = (S + split_len - 1) / split_len;
   if (n_splits <= 1) return;  // written directly by the split kernel
-  auto fold = [&](const Batch& x, int s0) {
-    float mx = M;
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i)
-      if (s0 + i < n_splits) mx = fmaxf(mx, x.m[i]);
-    const float c_old = M == mx ? 1.0f : fast_exp2(M - mx);
-    acc *= c_old;
-    L *= c_old;
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      if (s0 + i < n_splits) {
-        const float w = fast_exp2(x.m[i] - mx);
-        acc = fmaf(w, x.o[i], acc);
-        L = fmaf(w, x.l[i], L);
-      }
+  a.out[bh * DH + d] = merge_splits<DH, false>(a, base, d, n_splits, A);
+}
+
+template <int DH, int G, int SPLIT, typename KV, bool QKN>
+void launch_split_kernel(const DecodeArgs& args, dim3 grid, hipStream_t stream) {
+  constexpr int NT = 64 * decode_waves<SPLIT, KV, G>();
+  if constexpr (sizeof(KV) == 2) {
+    if (args.arrive) {
+      hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV, QKN, true>), grid, dim3(NT), 0,
+                         stream, args);
+      return;
     }
-    M = mx;
-  };
-  // ping-pong: the next batch's loads are issued before the current one is folded
-  for (int s0 = 0;;) {
-    if (s0 + kBatch < n_splits) load(Bb, s0 + kBatch);
-    fold(A, s0);
-    s0 += kBatch;
-    if (s0 >= n_splits) break;
-    if (s0 + kBatch < n_splits) load(A, s0 + kBatch);
-    fold(Bb, s0);
-    s0 += kBatch;
-    if (s0 >= n_splits) break;
   }
-  a.out[bh * DH + d] = acc * (1.0f / L);
+  hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV, QKN, false>), grid, dim3(NT), 0, stream,
+                     args);
 }
 
 template <int DH, int G, int SPLIT, typename KV>
@@ -887,17 +988,14 @@ int launch_split(const DecodeArgs& args, int B, hipStream_t stream) {
   bool launched = false;
   if constexpr (DH == 128 && sizeof(KV) == 2) {
     if (args.q_norm) {
-      hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV, true>), grid,
-                         dim3(64 * decode_waves<SPLIT, KV, G>()), 0, stream, args);
+      launch_split_kernel<DH, G, SPLIT, KV, true>(args, grid, stream);
       launched = true;
     }
   }
-  if (!launched)
-    hipLaunchKernelGGL((gqa_decode_kernel<DH, G, SPLIT, KV, false>), grid,
-                       dim3(64 * decode_waves<SPLIT, KV, G>()), 0, stream, args);
+  if (!launched) launch_split_kernel<DH, G, SPLIT, KV, false>(args, grid, stream);
   int rc = check_launch("gqa_decode_kernel");
   if (ev_split) (void)hipEventRecord(ev_split, stream);
-  if (!rc && args.max_splits > 1) {
+  if (!rc && args.max_splits > 1 && !args.arrive) {
     hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(DH), 0,
                        stream, args, SPLIT, args.Hkv * G);
     rc = check_launch("gqa_decode_combine_kernel");
@@ -950,6 +1048,11 @@ int launch_wide(const DecodeArgs& args, int B, int split_len, hipStream_t stream
 
 }  // namespace
 
+// In-launch split merge: at most this many split workgroups (larger grids run the combine
+// kernel, which measured faster there), and the counters a launch may use (B * Hkv).
+constexpr long kFuseMaxWorkgroups = 2048;
+static_assert(kFuseMaxWorkgroups <= kArriveCounters, "a fused launch has B * Hkv <= its splits");
+
 // Split length: 128 keys (one 32-key chunk per wave, 117 VGPRs, 4 waves/SIMD), measured
 // ahead of 256 (2 waves/SIMD) on every configs[2] case: B = 16 at 1K/2K/4K keys by 4-5%, a
 // single stream by 6-23%.  G = 4 keeps 4 heads of state per lane and runs 256-key splits.
@@ -962,6 +1065,27 @@ size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity) {
   const int split = 128;  // the shortest split choose_split() returns
   const size_t max_splits = (static_cast<size_t>(capacity) + split - 1) / split;
   return static_cast<size_t>(B) * Hq * max_splits * (Dh + 2) * sizeof(float);
+}
+
+// The stream's arrival counters (kArriveCounters, a fixed-size block of its own so it never
+// grows): zeroed by a fill kernel when the block is allocated; each fused launch's last
+// workgroups return the counters they used to zero.
+static int arrival_counters(hipStream_t stream, unsigned** out) {
+  bool fresh = false;
+  *out = static_cast<unsigned*>(
+      workspace(stream, kArriveCounters * sizeof(unsigned), kWsArrive, &fresh));
+  if (!*out) return ORATOR_ERR_HIP;
+  if (fresh) {
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(kArriveCounters / 256), dim3(256), 0, stream, *out);
+    return check_launch("zero_u32_kernel");
+  }
+  return ORATOR_OK;
+}
+
+int decode_workspace_reserve(int B, int Hq, int Dh, int capacity, hipStream_t stream) {
+  if (!workspace(stream, decode_workspace_bytes(B, Hq, Dh, capacity))) return ORATOR_ERR_HIP;
+  unsigned* unused = nullptr;
+  return arrival_counters(stream, &unused);
 }
 
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
@@ -1010,6 +1134,20 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (max_splits > 1024) return fail(ORATOR_ERR_CAPACITY, "gqa_decode: more than 1024 splits");
   const size_t part_o = static_cast<size_t>(p.B) * p.Hq * max_splits * p.Dh * sizeof(float);
   const size_t part_ml = static_cast<size_t>(p.B) * p.Hq * max_splits * 2 * sizeof(float);
+  // Small grids merge the splits inside the split launch (the last workgroup of each (stream,
+  // kv head) to finish): one launch instead of two, which is most of a single stream's time.
+  const long split_wgs = pairs * max_splits;
+  const bool fuse = !wide && !p.kv_f32 && max_splits > 1 && split_wgs <= kFuseMaxWorkgroups;
+  unsigned* arrive = nullptr;
+  if (fuse) {
+    if (p.scratch) {
+      arrive = p.arrive;  // the caller's counters (kArriveCounters, zero between launches)
+    } else {
+      // a fixed-size block, zeroed when it is allocated; each launch's last workgroups
+      // return the counters they used to zero
+      if (int rc = arrival_counters(stream, &arrive)) return rc;
+    }
+  }
   char* ws = nullptr;
   if (p.scratch) {
     if (part_o + part_ml > p.scratch_bytes)
@@ -1035,6 +1173,7 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   args.out = p.out;
   args.part_o = reinterpret_cast<float*>(ws);
   args.part_ml = reinterpret_cast<float*>(ws + part_o);
+  args.arrive = arrive;
   args.stream_stride = p.stream_stride;
   args.max_pages = p.max_pages;
   args.page_shift = page_shift;
@@ -1066,7 +1205,11 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
 // never passes the array's name to a kernel (on the host it is only a stand-in for the
 // symbol): the device address comes from hipGetSymbolAddress, once per device, with that
 // device current.
+// Layout: split partials, then kArriveCounters arrival counters of the in-launch split merge.
+// The counters start at zero (static storage is zero-initialized) and every launch that uses
+// them leaves them at zero.
 constexpr size_t kStaticScratchBytes = size_t{16} << 20;
+constexpr size_t kStaticPartialBytes = kStaticScratchBytes - kArriveCounters * sizeof(unsigned);
 static __device__ __align__(256) float scratch[kStaticScratchBytes / sizeof(float)];
 
 namespace {
@@ -1275,10 +1418,12 @@ int orator_gqa_decode_paged_noalloc(const float* q, const uint16_t* kpool, const
   if (!page_table) return fail(ORATOR_ERR_INVALID, "gqa_decode_paged_noalloc: null page table");
   // reject sizes past the scratch before touching the device
   const size_t need = decode_workspace_bytes(B, Hq, Dh, max_pages * page_size);
-  if (max_pages > 0 && page_size > 0 && need > kStaticScratchBytes)
+  if (max_pages > 0 && page_size > 0 && need > kStaticPartialBytes)
     return fail(ORATOR_ERR_CAPACITY,
                 "gqa_decode_paged_noalloc: B * Hq * splits * (Dh + 2) * 4 = " +
-                    std::to_string(need) + " bytes exceeds the 16 MiB static scratch");
+                    std::to_string(need) + " bytes exceeds the " +
+                    std::to_string(kStaticPartialBytes) +
+                    " bytes of the 16 MiB static scratch held for split partials");
   void* ptr = nullptr;
   if (int rc = static_scratch(&ptr)) return rc;
   DecodeProblem p{};
@@ -1297,7 +1442,8 @@ int orator_gqa_decode_paged_noalloc(const float* q, const uint16_t* kpool, const
   p.capacity = max_pages * page_size;
   p.scale = scale;
   p.scratch = ptr;
-  p.scratch_bytes = kStaticScratchBytes;
+  p.scratch_bytes = kStaticPartialBytes;
+  p.arrive = reinterpret_cast<unsigned*>(static_cast<char*>(ptr) + kStaticPartialBytes);
   return launch_gqa_decode(p, static_cast<hipStream_t>(stream));
 }
 

@@ -436,10 +436,10 @@ struct Decoder {
           (rc = check_hip(hipStreamSynchronize(s), "decoder sync")))
         return rc;
       ++emitted;
-      // the decode attention's split partials live in the capture stream's workspace
-      if ((rc = orator_workspace_reserve(
-               decode_workspace_bytes(1, c.num_q_heads, c.head_dim, c.max_seq_len),
-               capture_stream)))
+      // the decode attention's split partials and arrival counters live in the capture
+      // stream's workspace
+      if ((rc = decode_workspace_reserve(1, c.num_q_heads, c.head_dim, c.max_seq_len,
+                                         capture_stream)))
         return rc;
       graph_ban0 = eos0;
       graph_ban1 = eos1;

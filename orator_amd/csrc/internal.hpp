@@ -28,8 +28,10 @@ int check_launch(const char* what);
 // Slots are independent blocks: kWsGemm holds the split-K partials of the GEMMs, which may run
 // while a caller's slot-0 buffer (e.g. the bf16 cast of a Linear input) is being read.
 constexpr int kWsGemm = 1;
-constexpr int kWsMha = 2;  // key-split partials of the small-head masked MHA
-void* workspace(hipStream_t stream, size_t bytes, int slot = 0);
+constexpr int kWsMha = 2;     // key-split partials of the small-head masked MHA
+constexpr int kWsArrive = 3;  // arrival counters of the decode's in-launch split merge
+// *fresh (optional): the block was allocated by this call, its contents undefined.
+void* workspace(hipStream_t stream, size_t bytes, int slot = 0, bool* fresh = nullptr);
 // Frees every workspace block of `stream` (all threads, current and retired) after the
 // stream's queued work; for the owner of a stream about to be destroyed.
 int workspace_release(hipStream_t stream);
@@ -102,7 +104,11 @@ struct DecodeProblem {
   // workspace; a launch needing more fails with ORATOR_ERR_CAPACITY.
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  // With scratch: kArriveCounters arrival counters, zero between launches, for the split
+  // merge inside the split launch (small grids); nullptr runs the separate merge kernel.
+  unsigned* arrive = nullptr;
 };
+constexpr int kArriveCounters = 4096;
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
 // asr_ops::GqaAttention for any power-of-two Dh <= 1024 and any Hq multiple of Hkv
 // (attention_generic.hip); the split-K kernel serves Dh 64 / 128 with Hq / Hkv in {1, 2, 4}.
@@ -123,6 +129,9 @@ int launch_qk_norm_rope_kv(float* q, float* k, const float* v, long q_stride, lo
                            int max_pages, int page_size, int capacity, hipStream_t stream);
 // Workspace bytes a decode launch over B streams of `capacity` keys needs (split partials).
 size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity);
+// Sizes the stream's decode workspace (partials and arrival counters) for such launches ahead
+// of a graph capture.
+int decode_workspace_reserve(int B, int Hq, int Dh, int capacity, hipStream_t stream);
 
 // out[M][N] += in[M][K] W[N][K]^T: the residual add folded into the GEMM's store (M > 1); the
 // M = 1 GEMV writes tmp [N] and an add follows.

@@ -107,13 +107,13 @@ int device_cu_count() {
   return n;
 }
 
-void* workspace(hipStream_t stream, size_t bytes, int slot) {
+void* workspace(hipStream_t stream, size_t bytes, int slot, bool* fresh) {
   int dev = 0;
   if (check_hip(hipGetDevice(&dev), "hipGetDevice") != ORATOR_OK) return nullptr;
   std::string err;
   g_ws_guard.armed = true;
   void* p = ws_pool().get(WsKey{dev, stream, std::this_thread::get_id(), slot}, bytes,
-                          ws_capturing(stream), &err);
+                          ws_capturing(stream), &err, fresh);
   if (!p) (void)fail(ORATOR_ERR_HIP, err);
   return p;
 }

@@ -68,10 +68,13 @@ class WorkspacePool {
   }
 
   // The caller's block for key k, at least `bytes` long (nullptr and *err on failure).
-  // `capturing`: k.stream is being captured into a graph now.
-  void* get(const WsKey& k, size_t bytes, bool capturing, std::string* err) {
+  // `capturing`: k.stream is being captured into a graph now.  *fresh (optional) is set when
+  // the block was allocated by this call (its contents are undefined).
+  void* get(const WsKey& k, size_t bytes, bool capturing, std::string* err,
+            bool* fresh = nullptr) {
     std::lock_guard<std::mutex> lock(mu_);
     reap_locked();
+    if (fresh) *fresh = false;
     Entry& e = map_[k];
     if (capturing) e.captured = true;
     if (e.ptr && e.bytes >= bytes) return e.ptr;
@@ -84,6 +87,7 @@ class WorkspacePool {
     if (e.ptr) retire_locked(k.dev, k.stream, e.ptr, e.bytes, e.captured);
     e.ptr = p;
     e.bytes = n;
+    if (fresh) *fresh = true;
     return p;
   }
 

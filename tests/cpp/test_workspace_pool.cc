@@ -162,9 +162,13 @@ int main() {
     CHECK(pool.entries() == entries0);
   }
 
-  // another slot of the same stream and thread is a separate block
-  void* ps = pool.get(WsKey{0, s1, std::this_thread::get_id(), 1}, 100, false, nullptr);
-  CHECK(ps && ps != p2);
+  // another slot of the same stream and thread is a separate block; `fresh` tells a new block
+  // (whose contents the caller must initialise) from a reused one
+  bool fresh = false;
+  void* ps = pool.get(WsKey{0, s1, std::this_thread::get_id(), 1}, 100, false, nullptr, &fresh);
+  CHECK(ps && ps != p2 && fresh);
+  CHECK(pool.get(WsKey{0, s1, std::this_thread::get_id(), 1}, 64, false, nullptr, &fresh) == ps &&
+        !fresh);
   // another device is separate
   void* r = pool.get(WsKey{1, s1, std::this_thread::get_id()}, 10, false, nullptr);
   CHECK(r);

@@ -78,6 +78,29 @@ def test_decode_back_to_back_calls_reuse_combine_state():
                    truth=t64.decode(q, kc, vc, pos, 0.08838834764831845))
 
 
+@pytest.mark.parametrize("seq", [
+    # (lens, Hq, Hkv, Dh): small grids merge their splits inside the split launch, counting
+    # workgroups in per (stream, kv head); every launch must leave its counters at zero for
+    # the next one, whatever its shape
+    [([4097], 16, 8, 128), ([300, 1, 2500, 129, 4000], 16, 8, 128), ([4097], 16, 8, 128),
+     ([2000, 700], 16, 4, 128), ([1500], 8, 8, 64), ([1025] * 3, 16, 8, 128),
+     ([4097], 16, 8, 128)],
+])
+def test_decode_paged_in_launch_merge_back_to_back(seq):
+    for i, (lens, Hq, Hkv, Dh) in enumerate(seq):
+        ps = 16
+        q, kp, vp, table, pos = _paged_case(500 + i, lens, Hq, Hkv, Dh, ps)
+        B, max_pages = table.shape
+        scale = 1.0 / math.sqrt(Dh)
+        ref = orc.gqa_decode_paged(q, kp, vp, table, ps, pos, scale, threads=8)
+        dout = empty((B, Hq, Dh), np.float32)
+        say("decode in-launch merge", i, lens, Hq, Hkv, Dh)
+        da.GqaDecodeAttnPaged(up(q), up(kp), up(vp), up(table), max_pages, ps, up(pos), dout, B,
+                              Hq, Hkv, Dh, scale)
+        check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+                   truth=t64.decode_paged(q, kp, vp, table, ps, pos, scale))
+
+
 def test_decode_position_past_capacity_is_clamped():
     Hq, Hkv, Dh, cap = 16, 8, 128, 256
     q, kc, vc = _contig_case(10, cap, cap)

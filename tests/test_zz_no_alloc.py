@@ -1,7 +1,7 @@
 """GPU: the allocation-free decode entry point (orator_gqa_decode_paged_noalloc, split partials
 in a static device array) against orator_gqa_decode_paged on the same inputs, through the C
-ABI: two calls in a row, the second smaller, outputs bit-identical (same kernels, same split
-plan) and within 1e-4 relative (floor 0.05) of the oracle; the no-alloc entry runs first, on a
+ABI: three calls in a row, each smaller than the one before, outputs bit-identical (same
+kernels, same split plan) and within 1e-4 relative (floor 0.05) of the oracle; the no-alloc entry runs first, on a
 fresh stream, and the library's workspace holds exactly the blocks and bytes it held before it
 (so it cannot have been served from a block an earlier allocating call left behind); sizes past
 the static scratch are rejected on the host with ORATOR_ERR_CAPACITY."""
@@ -40,7 +40,9 @@ def test_noalloc_matches_allocating_entry_twice():
     scale = 1.0 / math.sqrt(Dh)
     # second call smaller (fewer streams, shorter contexts): stale partials of the first call
     # stay in the scratch and must not leak into it
-    for seed, lens in ((1, [4097 + i for i in range(16)]), (2, [700, 1, 129])):
+    # (the smaller calls are small grids: their splits are merged inside the split launch,
+    # with arrival counters in the scratch's last 16 KiB, left at zero by every launch)
+    for seed, lens in ((1, [4097 + i for i in range(16)]), (2, [700, 1, 129]), (3, [2000])):
         q, kp, vp, table, max_pages, ps, pos = _case(seed, lens)
         B = len(lens)
         dq, dk, dv, dt, dpos = up(q), up(kp), up(vp), up(table), up(pos)
