@@ -694,10 +694,11 @@ def main():
                      # (wide split + merge kernels) at this workload, S = 4097..4105.
                      "traffic": HBM_TRAFFIC_PER_OP,
                      "traffic_over_algorithmic": round(HBM_TRAFFIC_PER_OP / ALGORITHMIC_AT_TRAFFIC, 3),
-                     "kernel": "decode op = gqa_decode_wide_kernel (each stream and kv head cut "
-                               "into two ~2070-key ranges, one 8-wave workgroup each) + "
-                               "gqa_decode_combine_kernel (range merge); average over the "
-                               "timed region's back-to-back ops (HIP events on its stream)",
+                     "kernel": "decode op = gqa_decode_wide_kernel, one launch (each stream and kv "
+                               "head cut into a 2048-key and a 2112-key range, one 8-wave "
+                               "workgroup each; the last of the two to finish merges them); "
+                               "average over the timed region's back-to-back ops (HIP events "
+                               "on its stream)",
                      "kernel_avg_us": round(dec["kernel_avg_us"], 2),
                      "bytes_per_launch": int(dec["kernel_bytes"]),
                      "attainable_copy_gbs": copy["GBs_read_plus_write"],

@@ -697,9 +697,9 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
 }
 
 // Wide split kernel for many streams (B * Hkv pairs >= half the CUs): each (stream, kv head)
-// is cut into `parts` ranges of `split_len` keys (a multiple of 32, fixed by the capacity so
-// the page-table entries of every chunk are known before the position is), one workgroup of
-// kWideWaves waves per range.  Wave w takes the range's 32-key chunks w, w + 8, ... in a
+// is cut into `parts` ranges of `split_len` keys (a multiple of 256, fixed by the capacity so
+// the page-table entries of every chunk are known before the position is; the last range runs
+// to the capacity), one workgroup of kWideWaves waves per range.  Wave w takes the range's 32-key chunks w, w + 8, ... in a
 // ping-pong loop (the next chunk's K/V loads are in flight while the current one is
 // computed), so a workgroup keeps ~128 KB of K/V in flight for its whole life instead of
 // paying a dispatch, an entry round trip and a barrier per 64 KB.  The entry load reads the
@@ -708,7 +708,9 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
 constexpr int kWideWaves = 8;
 constexpr int kWideMaxChunks = 31;  // chunks per wave: 2 table entries each in lanes 0..61
 
-template <int DH, int G>
+// FUSE: the ranges are merged by the last workgroup of each (stream, kv head) to finish
+// (a.arrive set), else by the combine kernel.
+template <int DH, int G, bool FUSE>
 __global__ __launch_bounds__(64 * kWideWaves) __attribute__((amdgpu_waves_per_eu(2)))
 void gqa_decode_wide_kernel(DecodeArgs a, int split_len) {
   using KV = uint16_t;
@@ -747,7 +749,9 @@ void gqa_decode_wide_kernel(DecodeArgs a, int split_len) {
     return;
   }
   if (p0 >= S) return;
-  const int n_parts = (S + split_len - 1) / split_len;
+  // ranges of split_len keys, the last one (range max_splits - 1) running to the capacity
+  const int n_parts = min((S + split_len - 1) / split_len, a.max_splits);
+  const int p_end = part == a.max_splits - 1 ? a.capacity : p0 + split_len;
   const int Hq = a.Hkv * G;
   const int o = lane & 7;
   float qr[G][CK::QPL];
@@ -773,7 +777,7 @@ void gqa_decode_wide_kernel(DecodeArgs a, int split_len) {
   int new_key = -1;
   if (a.k_new && S == pos_b + 1) new_key = S - 1;
   const int S_cache = new_key >= 0 ? S - 1 : S;
-  const int r_end = min(p0 + split_len, S_cache);  // this range's cached keys: [p0, r_end)
+  const int r_end = min(p_end, S_cache);  // this range's cached keys: [p0, r_end)
   // rows of keys c_k, c_k + 16 of chunk k (wave-uniform)
   auto rows = [&](int k, long& r0, long& r1) {
     const int c = p0 + 32 * (wave + NW * k);
@@ -822,7 +826,7 @@ void gqa_decode_wide_kernel(DecodeArgs a, int split_len) {
     }
   }
   // the appended key: folded in by the wave whose chunk slot holds it, then written
-  if (new_key >= p0 && new_key < p0 + split_len && ((new_key - p0) >> 5) % NW == wave) {
+  if (new_key >= p0 && new_key < p_end && ((new_key - p0) >> 5) % NW == wave) {
     const float* kn = a.k_new + (static_cast<long>(b) * a.Hkv + kvh) * DH;
     const float* vn = a.v_new + (static_cast<long>(b) * a.Hkv + kvh) * DH;
     uint4 kw[CK::NCQ], vw;
@@ -886,11 +890,72 @@ void gqa_decode_wide_kernel(DecodeArgs a, int split_len) {
       a.out[bh * DH + d] = ov * (1.0f / lv);
     } else {
       const long ps = bh * a.max_splits + part;
-      a.part_o[ps * DH + d] = ov;
-      if (d == 0) {
-        a.part_ml[ps * 2] = mx;
-        a.part_ml[ps * 2 + 1] = lv;
+      if constexpr (FUSE) {
+        store_dev(a.part_o + ps * DH + d, ov);
+        if (d == 0) {
+          store_dev(a.part_ml + ps * 2, mx);
+          store_dev(a.part_ml + ps * 2 + 1, lv);
+        }
+      } else {
+        a.part_o[ps * DH + d] = ov;
+        if (d == 0) {
+          a.part_ml[ps * 2] = mx;
+          a.part_ml[ps * 2 + 1] = lv;
+        }
       }
+    }
+  }
+  if constexpr (FUSE) {
+    if (n_parts == 1) return;
+    // ---- in-launch range merge: the last workgroup of (stream, kv head) to arrive, as in
+    // the split kernel; its own range's partial is read back like the others, four ranges'
+    // loads in flight at a time ----
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      unsigned* ctr = a.arrive + static_cast<long>(b) * a.Hkv + kvh;
+      const unsigned prev =
+          __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev + 1 == static_cast<unsigned>(n_parts);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    for (int idx = tid; idx < G * DH; idx += NT) {
+      const int g = idx / DH;
+      const int d = idx % DH;
+      const long bh = static_cast<long>(b) * Hq + kvh * G + g;
+      const long base = bh * a.max_splits;
+      float M = -INFINITY, L = 0.0f, acc = 0.0f;
+      for (int s0 = 0; s0 < n_parts; s0 += 4) {
+        float pm[4], pl[4], po[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const long ps = base + min(s0 + i, n_parts - 1);
+          pm[i] = load_dev(a.part_ml + ps * 2);
+          pl[i] = load_dev(a.part_ml + ps * 2 + 1);
+          po[i] = load_dev(a.part_o + ps * DH + d);
+        }
+        float mx = M;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (s0 + i < n_parts) mx = fmaxf(mx, pm[i]);
+        const float c_old = M == mx ? 1.0f : fast_exp2(M - mx);
+        acc *= c_old;
+        L *= c_old;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (s0 + i < n_parts) {
+            const float w = fast_exp2(pm[i] - mx);
+            acc = fmaf(w, po[i], acc);
+            L = fmaf(w, pl[i], L);
+          }
+        }
+        M = mx;
+      }
+      a.out[bh * DH + d] = acc * (1.0f / L);
     }
   }
 }
@@ -960,7 +1025,8 @@ __global__ __launch_bounds__(DH) void gqa_decode_combine_kernel(DecodeArgs a, in
   const int pos_ld = *psrc;
   asm volatile("" ::: "memory");  // keeps the batch's loads here, ahead of the early return
   const int S = stream_keys(a, b, a.pos_mode == 0 ? __builtin_amdgcn_readlane(pos_ld, 0) : 0);
-  const int n_splits = (S + split_len - 1) / split_len;
+  // (the wide kernel's last range runs to the capacity: at most max_splits ranges)
+  const int n_splits = min((S + split_len - 1) / split_len, a.max_splits);
   if (n_splits <= 1) return;  // written directly by the split kernel
   a.out[bh * DH + d] = merge_splits<DH, false>(a, base, d, n_splits, A);
 }
@@ -1033,11 +1099,15 @@ int launch_wide(const DecodeArgs& args, int B, int split_len, hipStream_t stream
   hipEvent_t ev0, ev_split, ev1;
   take_timing_events(&ev0, &ev_split, &ev1);
   if (ev0) (void)hipEventRecord(ev0, stream);
-  hipLaunchKernelGGL((gqa_decode_wide_kernel<DH, G>), grid, dim3(64 * kWideWaves), 0, stream,
-                     args, split_len);
+  if (args.arrive)
+    hipLaunchKernelGGL((gqa_decode_wide_kernel<DH, G, true>), grid, dim3(64 * kWideWaves), 0,
+                       stream, args, split_len);
+  else
+    hipLaunchKernelGGL((gqa_decode_wide_kernel<DH, G, false>), grid, dim3(64 * kWideWaves), 0,
+                       stream, args, split_len);
   int rc = check_launch("gqa_decode_wide_kernel");
   if (ev_split) (void)hipEventRecord(ev_split, stream);
-  if (!rc && args.max_splits > 1) {
+  if (!rc && args.max_splits > 1 && !args.arrive) {
     hipLaunchKernelGGL((gqa_decode_combine_kernel<DH>), dim3(args.Hkv * G, B), dim3(DH), 0,
                        stream, args, split_len, args.Hkv * G);
     rc = check_launch("gqa_decode_combine_kernel");
@@ -1120,24 +1190,30 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   // each, enough ranges to give every CU a workgroup); otherwise 128-key splits.
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const long pairs = static_cast<long>(p.B) * p.Hkv;
-  int wide_parts = static_cast<int>(std::max<long>((cus + pairs - 1) / pairs,
-                                                   (p.capacity + kWideMaxChunks * 256 - 1) /
-                                                       (kWideMaxChunks * 256)));
-  const int wide_len = ((p.capacity + wide_parts - 1) / wide_parts + 31) / 32 * 32;
-  wide_parts = (p.capacity + wide_len - 1) / wide_len;
+  const int wide_parts = static_cast<int>(std::max<long>(
+      (cus + pairs - 1) / pairs, (p.capacity + kWideMaxChunks * 256 - 1) / (kWideMaxChunks * 256)));
+  // Ranges of a multiple of 256 keys (8 chunks: the same count for every wave), the last
+  // range taking the remainder up to the capacity.  B = 16, S = 4097..4105, capacity 4160:
+  // 2048 + 2112 keys, every wave 8 full chunks plus at most the short tail chunk, where
+  // 2080-key ranges gave one wave of each first range a ninth full chunk.
+  const int wide_len = p.capacity / wide_parts / 256 * 256;
+  const int wide_last = p.capacity - (wide_parts - 1) * wide_len;
   // Ranges of >= 1536 keys (>= 6 chunks per wave): at B = 16 the wide kernel measured 50.5-51.6
   // us per op against 52.9 at 4096 keys, but 19.7 / 29.7 against 18.3 / 29.2 us at 1024 / 2048
   // (2 / 4 chunks per wave: its ramp and tail are not amortised).
-  const bool wide = !p.kv_f32 && p.pos_mode == 0 && !p.q_norm && G <= 2 && wide_len >= 1536;
+  const bool wide = !p.kv_f32 && p.pos_mode == 0 && !p.q_norm && G <= 2 && wide_len >= 1536 &&
+                    wide_last <= kWideMaxChunks * 256;
   const int split = wide ? wide_len : choose_split(p.B, p.Hkv, G, p.capacity);
-  const int max_splits = (p.capacity + split - 1) / split;
+  const int max_splits = wide ? wide_parts : (p.capacity + split - 1) / split;
   if (max_splits > 1024) return fail(ORATOR_ERR_CAPACITY, "gqa_decode: more than 1024 splits");
   const size_t part_o = static_cast<size_t>(p.B) * p.Hq * max_splits * p.Dh * sizeof(float);
   const size_t part_ml = static_cast<size_t>(p.B) * p.Hq * max_splits * 2 * sizeof(float);
-  // Small grids merge the splits inside the split launch (the last workgroup of each (stream,
-  // kv head) to finish): one launch instead of two, which is most of a single stream's time.
+  // Small split grids and the wide kernel merge their partials inside the launch (the last
+  // workgroup of each (stream, kv head) to finish): one launch instead of two, which is most
+  // of a single stream's time and 1.8 us of the wide op's 50.7 (B = 16, L = 4096, same box).
   const long split_wgs = pairs * max_splits;
-  const bool fuse = !wide && !p.kv_f32 && max_splits > 1 && split_wgs <= kFuseMaxWorkgroups;
+  const bool fuse = !p.kv_f32 && max_splits > 1 &&
+                    (wide ? pairs <= kArriveCounters : split_wgs <= kFuseMaxWorkgroups);
   unsigned* arrive = nullptr;
   if (fuse) {
     if (p.scratch) {
