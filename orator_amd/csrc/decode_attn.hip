@@ -1137,19 +1137,22 @@ size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity) {
   return static_cast<size_t>(B) * Hq * max_splits * (Dh + 2) * sizeof(float);
 }
 
-// The stream's arrival counters (kArriveCounters, a fixed-size block of its own so it never
-// grows): zeroed by a fill kernel when the block is allocated; each fused launch's last
-// workgroups return the counters they used to zero.
-static int arrival_counters(hipStream_t stream, unsigned** out) {
+int zeroed_counters(hipStream_t stream, int slot, unsigned** out) {
   bool fresh = false;
   *out = static_cast<unsigned*>(
-      workspace(stream, kArriveCounters * sizeof(unsigned), kWsArrive, &fresh));
+      workspace(stream, kArriveCounters * sizeof(unsigned), slot, &fresh));
   if (!*out) return ORATOR_ERR_HIP;
   if (fresh) {
     hipLaunchKernelGGL(zero_u32_kernel, dim3(kArriveCounters / 256), dim3(256), 0, stream, *out);
     return check_launch("zero_u32_kernel");
   }
   return ORATOR_OK;
+}
+
+// The stream's arrival counters (kArriveCounters, a fixed-size block of its own so it never
+// grows); each fused launch's last workgroups return the counters they used to zero.
+static int arrival_counters(hipStream_t stream, unsigned** out) {
+  return zeroed_counters(stream, kWsArrive, out);
 }
 
 int decode_workspace_reserve(int B, int Hq, int Dh, int capacity, hipStream_t stream) {

@@ -30,6 +30,8 @@ int check_launch(const char* what);
 constexpr int kWsGemm = 1;
 constexpr int kWsMha = 2;     // key-split partials of the small-head masked MHA
 constexpr int kWsArrive = 3;  // arrival counters of the decode's in-launch split merge
+constexpr int kWsPrefill = 4;        // partials of the long-prompt prefill's cut blocks
+constexpr int kWsPrefillArrive = 5;  // its arrival counters
 // *fresh (optional): the block was allocated by this call, its contents undefined.
 void* workspace(hipStream_t stream, size_t bytes, int slot = 0, bool* fresh = nullptr);
 // Frees every workspace block of `stream` (all threads, current and retired) after the
@@ -109,6 +111,14 @@ struct DecodeProblem {
   unsigned* arrive = nullptr;
 };
 constexpr int kArriveCounters = 4096;
+// A block of kArriveCounters counters in workspace slot `slot` of the stream, zeroed by a fill
+// kernel when the block is allocated; the kernels using it return every counter to zero.
+int zeroed_counters(hipStream_t stream, int slot, unsigned** out);
+// Long-prompt bf16 prefill over a contiguous cache, one wave per SIMD with stream-K balance
+// (prefill_sk.hip); Dh 128, Hq / Hkv in {1, 2, 4}, Hkv * ceil(Tq / (128 / G)) <= kArriveCounters.
+int launch_prefill_sk(const float* q, const uint16_t* q_bf16, const uint16_t* kc,
+                      const uint16_t* vc, float* out, int Tq, int Hq, int Hkv,
+                      const int* d_pos0, int capacity, float scale, hipStream_t stream);
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
 // asr_ops::GqaAttention for any power-of-two Dh <= 1024 and any Hq multiple of Hkv
 // (attention_generic.hip); the split-K kernel serves Dh 64 / 128 with Hq / Hkv in {1, 2, 4}.

@@ -197,6 +197,53 @@ def test_prefill_bf16_q_input():
     assert np.max(np.abs(down(dout, q.shape) - ref)) <= TOL16
 
 
+# Long bf16 prompts over a contiguous cache take the stream-K kernel (prefill_attn.hip
+# launch_prefill: Tq >= 2048, GQA group 1 or 2): ragged last blocks, offsets into a longer
+# cache, capacity past the keys, q given in fp32 (rounded on the device) and in bf16.
+SK_CASES = [(2085, 100, 2300, 16, 8), (2048, 1000, 3100, 8, 8), (2111, 0, 2111, 16, 16)]
+
+
+@pytest.mark.parametrize("T,pos0,cap,Hq,Hkv", SK_CASES)
+def test_prefill_stream_k_cases(T, pos0, cap, Hq, Hkv):
+    q, kc, vc = _layer_inputs(T + pos0 + Hkv, T, pos0, Hq=Hq, Hkv=Hkv, cap=cap)
+    qb = orc.to_bf16(q)
+    scale = 1.0 / math.sqrt(128)
+    ref = orc.gqa_prefill(orc.from_bf16(qb), kc, vc, pos0, scale, threads=16)
+    dpos = up(np.array([pos0], np.int32))
+    for q_in in ("fp32", "bf16"):
+        say(f"prefill stream-K T={T} pos0={pos0} cap={cap} Hq={Hq} Hkv={Hkv} q={q_in}")
+        dout = empty(q.shape, np.float32)
+        if q_in == "fp32":
+            da.GqaCacheAttnEx(up(q), None, up(kc), up(vc), None, 0, 0, dout, T, Hq, Hkv, 128,
+                              dpos, cap, scale, da.PREFILL_BF16)
+        else:
+            da.GqaCacheAttnEx(None, up(qb), up(kc), up(vc), None, 0, 0, dout, T, Hq, Hkv, 128,
+                              dpos, cap, scale, da.PREFILL_BF16)
+        err = float(np.max(np.abs(down(dout, q.shape) - ref)))
+        print(f"bf16 max |g - r| = {err:.3e}")
+        assert err <= TOL16
+
+
+def test_prefill_stream_k_reference_redo():
+    """Scores that grow along the keys by far more than 2^64 (log2 units) past a segment's
+    first tile: the stream-K kernel's fixed softmax reference is exceeded and the segment is
+    redone with the maxima seen (without the redo the weights overflow to inf).  q = 1 and key j
+    = 12 j / T in every dim: score(t, j) = 1536 j / T / sqrt(128), up to 196 in log2 units."""
+    T, Hq, Hkv, Dh = 2048, 16, 8, 128
+    q = np.ones((T, Hq, Dh), np.float32)
+    kc = orc.to_bf16(np.repeat((12.0 * np.arange(T, dtype=np.float32) / T)[:, None, None],
+                               Hkv * Dh, axis=1).reshape(T, Hkv, Dh))
+    vc = orc.to_bf16(SplitMix64(21).normal((T, Hkv, Dh)))
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_prefill(q, kc, vc, 0, scale, threads=16)
+    say("prefill stream-K reference redo")
+    got = _run(q, kc, vc, 0, T, da.PREFILL_BF16, Hkv)
+    assert np.all(np.isfinite(got))
+    err = float(np.max(np.abs(got - ref)))
+    print(f"bf16 max |g - r| = {err:.3e}")
+    assert err <= TOL16
+
+
 def _launcher_rw(T, Hq, Hkv, cus=256):
     """The launcher's choice of row waves per workgroup and pairing (prefill_attn.hip
     launch_g), so each case below names the instantiation it runs on a 256-CU MI355X."""
@@ -224,9 +271,10 @@ def _large_case(T, Hq, Hkv):
     return _ORACLE_CACHE[key]
 
 
-# Every instantiation the launcher takes at long prompts, in both precision modes: RW = 2
-# row waves paired (T = 2048, G = 2: the decoder's own 2048-token prefill kernel), RW = 2
-# unpaired, RW = 4 paired (T = 4096), for GQA groups 1, 2 and 4.
+# Every instantiation the row-wave launcher takes at long prompts: RW = 2 row waves paired
+# (T = 2048, G = 2: the decoder's own 2048-token fp32 prefill kernel), RW = 2 unpaired, RW = 4
+# paired (T = 4096), for GQA groups 1, 2 and 4.  In bf16 mode the group 1 and 2 cases run the
+# stream-K kernel instead (G = 4 stays on the row-wave kernel).
 LARGE = [(2048, 16, 8), (2048, 8, 8), (2048, 16, 16), (2048, 16, 4),
          (4096, 16, 8), (4096, 16, 16), (4096, 16, 4)]
 
