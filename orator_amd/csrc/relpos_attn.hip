@@ -231,6 +231,23 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, r);
 }
 
+// Inline-asm v_mfma_f32_32x32x16_f16 for the score products.  The hardware does not interlock
+// them with other instructions; the wait states are placed by hand: s_nop 1 before each (an
+// operand written by a VALU instruction needs 2 wait states before an MFMA reads it), and
+// rp_mfma_result_guard() (12 wait states for an 8-pass MFMA) between the last of them and
+// the first VALU or LDS read of their results.  A chain accumulating into the same registers
+// needs none.
+typedef unsigned rp_u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void rp_mfma0(f32x16_t& d, uint4 a, uint4 b) {
+  const rp_u32x4_t x = __builtin_bit_cast(rp_u32x4_t, a), y = __builtin_bit_cast(rp_u32x4_t, b);
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(x), "v"(y));
+}
+__device__ __forceinline__ void rp_mfma(f32x16_t& d, uint4 a, uint4 b) {
+  const rp_u32x4_t x = __builtin_bit_cast(rp_u32x4_t, a), y = __builtin_bit_cast(rp_u32x4_t, b);
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(x), "v"(y));
+}
+__device__ __forceinline__ void rp_mfma_result_guard() { asm volatile("s_nop 7\n\ts_nop 4" ::); }
+
 struct RelPosArgs {
   const void *q, *k, *v, *p;
   const float *u, *vb;
@@ -260,7 +277,8 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
 
   const int h = blockIdx.x % a.H;
   const int i0 = (blockIdx.x / a.H) * 32;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar tile offsets
   const int col = lane & 31, h2 = lane >> 5;
   const int T = a.T, H = a.H;
   const long rs = static_cast<long>(H) * kRpDk;  // elements per token row
@@ -333,8 +351,10 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
     uint16_t* qst = reinterpret_cast<uint16_t*>(lds);
     for (int it = tid; it < 32 * 8; it += 64 * kRpWaves) {
       const int c = it >> 3, d0 = 8 * (it & 7);
+      // with no valid key (uniform) q + u and q + v are zero: every score is 0, the mask
+      // below leaves the T keys, and the softmax averages V
       uint4 hu = make_uint4(0, 0, 0, 0), hv = hu;
-      if (i0 + c < T) {
+      if (i0 + c < T && !a.uniform) {
         float x[8];
         load8_f(qp + (i0 + c) * rs + h * kRpDk + d0, x);
         const float* ub = a.u + h * kRpDk + d0;
@@ -396,15 +416,19 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
       *reinterpret_cast<uint4*>(vt + (8 * it + rv) * kVRowH + 8 * dcv) = cur.v[it];
     if (next < n_tiles) load_v(cur, next);
     // AC^T and R = P_window (q + v)^T
+    // (inline asm: the first k-step takes the inline constant 0 as its accumulator, where the
+    // compiler zeroed 48 registers with moves every tile; wait states by hand, see rp_mfma)
     f32x16_t s, r0, r1;
+    rp_mfma0(s, kf[0], qu[0]);
+    rp_mfma0(r0, pf0[0], qv[0]);
+    rp_mfma0(r1, pf1[0], qv[0]);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s[e] = r0[e] = r1[e] = 0.0f;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(kf[ks]), as_f16x8(qu[ks]), s, 0, 0, 0);
-      r0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(pf0[ks]), as_f16x8(qv[ks]), r0, 0, 0, 0);
-      r1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(pf1[ks]), as_f16x8(qv[ks]), r1, 0, 0, 0);
+    for (int ks = 1; ks < 4; ++ks) {
+      rp_mfma(s, kf[ks], qu[ks]);
+      rp_mfma(r0, pf0[ks], qv[ks]);
+      rp_mfma(r1, pf1[ks], qv[ks]);
     }
+    rp_mfma_result_guard();
     // R^T -> LDS; the lane's accumulator rows are 8i + 4*h2 + j (+32 for r1), column = col
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -416,15 +440,7 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
     // scores (log2 units): (AC + BD) * scale; keys >= valid masked on the one tile that
     // holds them (padding query columns carry zero q rows: finite, never stored)
     float tmax = -INFINITY;
-    if (a.uniform) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int jl = 8 * (e >> 2) + 4 * h2 + (e & 3);
-        const float x = j0 + jl < a.valid ? 0.0f : -INFINITY;
-        s[e] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    } else {
+    {
       float bd[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e)
@@ -495,22 +511,25 @@ __global__ __launch_bounds__(64 * kRpWaves) void relpos_fused_kernel(RelPosArgs 
     for (int e = 0; e < 16; ++e)
       o_lds(wave, 32 * dt + 8 * (e >> 2) + 4 * h2 + (e & 3), col) = o[dt][e];
   __syncthreads();
-  for (int idx = tid; idx < 32 * kRpDk; idx += 64 * kRpWaves) {
-    const int c = idx / kRpDk, d = idx % kRpDk;
-    const int i = i0 + c;
-    if (i >= T) continue;
-    float mx = -INFINITY;
+  // thread -> query column qc, dims d0 .. d0 + 3: the column's wave weights once, one float4
+  static_assert(32 * kRpDk == 4 * 64 * kRpWaves, "one float4 of the output per thread");
+  const int qc = tid >> 4, d0 = 4 * (tid & 15);
+  float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kRpWaves; ++w) mx = fmaxf(mx, mo_lds[w][0][c]);
-    const float mr = mx == -INFINITY ? 0.0f : mx;
-    float ov = 0.0f, lv = 0.0f;
+  for (int w = 0; w < kRpWaves; ++w) mx = fmaxf(mx, mo_lds[w][0][qc]);
+  const float mr = mx == -INFINITY ? 0.0f : mx;
+  float lv = 0.0f, ov[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int w = 0; w < kRpWaves; ++w) {
-      const float wt = fast_exp2(mo_lds[w][0][c] - mr);
-      ov = fmaf(wt, o_lds(w, d, c), ov);
-      lv = fmaf(wt, mo_lds[w][1][c], lv);
-    }
-    a.out[(static_cast<long>(i) * H + h) * kRpDk + d] = lv > 0.0f ? ov / lv : 0.0f;
+  for (int w = 0; w < kRpWaves; ++w) {
+    const float wt = fast_exp2(mo_lds[w][0][qc] - mr);
+    lv = fmaf(wt, mo_lds[w][1][qc], lv);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ov[e] = fmaf(wt, o_lds(w, d0 + e, qc), ov[e]);
+  }
+  if (i0 + qc < T) {
+    const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
+    *reinterpret_cast<float4*>(a.out + (static_cast<long>(i0 + qc) * H + h) * kRpDk + d0) =
+        make_float4(ov[0] * inv, ov[1] * inv, ov[2] * inv, ov[3] * inv);
   }
 }
 
