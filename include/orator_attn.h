@@ -172,9 +172,9 @@ int orator_decode_read_probe(const uint16_t* kpool, const uint16_t* vpool, const
 /* No counterpart in the reference: orator_gqa_decode_paged for callers that cannot allocate
  * (code under HIP graph capture, serving loops that forbid hipMalloc).  Same arguments and
  * results; the split partials (and the arrival counters of the in-launch split merge, its
- * last 16 KiB) live in a static 16 MiB device array per GPU instead of the library workspace,
+ * last 512 KiB) live in a static 16 MiB device array per GPU instead of the library workspace,
  * so the call allocates nothing.  Limit: B * Hq * ceil(max_pages * page_size / 128) * (Dh +
- * 2) * 4 bytes <= 16 MiB - 16 KiB (B = 16, Hq = 16, Dh = 128: 16000 keys), else
+ * 2) * 4 bytes <= 16 MiB - 512 KiB (B = 16, Hq = 16, Dh = 128: 15616 keys), else
  * ORATOR_ERR_CAPACITY.  Calls that overlap on one GPU share the array and race. */
 int orator_gqa_decode_paged_noalloc(const float* q, const uint16_t* kpool, const uint16_t* vpool,
                                     const int* page_table, int max_pages, int page_size,

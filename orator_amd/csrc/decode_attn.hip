@@ -428,6 +428,51 @@ __device__ __forceinline__ float merge_splits(const DecodeArgs& a, long base, in
   return acc * (1.0f / L);
 }
 
+// The merged output of dim d over n_splits (2 .. 64) splits of partial row `base`, for a
+// wave whose lanes all merge the same row (dims d): lane s loads split s's maximum and sum
+// (one load each for the wave, where every lane loading every split's took 2 per split), the
+// weights are formed once per split and broadcast by lane, and the partial rows are loaded
+// kWaveMergeBatch at a time, the next batch in flight while one is folded.
+constexpr int kWaveMergeBatch = 24;
+template <int DH>
+__device__ __forceinline__ float merge_splits_wave(const DecodeArgs& a, long base, int d,
+                                                   int n_splits, int lane) {
+  float o_a[kWaveMergeBatch], o_b[kWaveMergeBatch];
+  auto load_o = [&](float (&o)[kWaveMergeBatch], int s0) {
+#pragma unroll
+    for (int i = 0; i < kWaveMergeBatch; ++i)
+      o[i] = load_dev(a.part_o + (base + min(s0 + i, n_splits - 1)) * DH + d);
+  };
+  float ms = -INFINITY, ls = 0.0f;
+  if (lane < n_splits) {
+    ms = load_dev(a.part_ml + (base + lane) * 2);
+    ls = load_dev(a.part_ml + (base + lane) * 2 + 1);
+  }
+  load_o(o_a, 0);
+  if (kWaveMergeBatch < n_splits) load_o(o_b, kWaveMergeBatch);
+  const float mx = wave_max(ms);
+  const float w = lane < n_splits ? fast_exp2(ms - mx) : 0.0f;  // a split's -inf: weight 0
+  const float L = wave_sum(w * ls);
+  float acc = 0.0f;
+  auto fold = [&](const float (&o)[kWaveMergeBatch], int s0) {
+#pragma unroll
+    for (int i = 0; i < kWaveMergeBatch; ++i)
+      if (s0 + i < n_splits)  // uniform
+        acc = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s0 + i)), o[i], acc);
+  };
+  for (int s0 = 0;;) {
+    fold(o_a, s0);
+    s0 += kWaveMergeBatch;
+    if (s0 >= n_splits) break;
+    if (s0 + kWaveMergeBatch < n_splits) load_o(o_a, s0 + kWaveMergeBatch);
+    fold(o_b, s0);
+    s0 += kWaveMergeBatch;
+    if (s0 >= n_splits) break;
+    if (s0 + kWaveMergeBatch < n_splits) load_o(o_b, s0 + kWaveMergeBatch);
+  }
+  return acc * (1.0f / L);
+}
+
 // Waves per split workgroup: bf16 splits of 256 / 512 keys give every wave one 32-key
 // chunk (8 / 16 waves); otherwise 4 waves.
 template <int SPLIT, typename KV, int G>
@@ -472,6 +517,24 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   if (lane == 1 && paged) esrc = ptb + (wj0 >> a.page_shift);
   if (lane == 2 && paged) esrc = ptb + (wj1 >> a.page_shift);
   const int eld = *esrc;
+  // ---- q of the G heads, octet layout: lane owns dims 8*EPV*cc + EPV*o + e; loaded while
+  // the position is in flight (q does not depend on it) ----
+  const int o = lane & 7;
+  float qr[G][CK::QPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float* qh = a.q + (static_cast<long>(b) * a.Hkv * G + kvh * G + g) * DH + CK::EPV * o;
+#pragma unroll
+    for (int cc = 0; cc < CK::NCQ; ++cc)
+#pragma unroll
+      for (int e4 = 0; e4 < CK::EPV; e4 += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(qh + 8 * CK::EPV * cc + e4);
+        qr[g][cc * CK::EPV + e4] = x.x;
+        qr[g][cc * CK::EPV + e4 + 1] = x.y;
+        qr[g][cc * CK::EPV + e4 + 2] = x.z;
+        qr[g][cc * CK::EPV + e4 + 3] = x.w;
+      }
+  }
   const int pos_b = a.pos_mode == 0 ? __builtin_amdgcn_readlane(eld, 0) : 0;
   const int key0 = stream_key0(a, b);
   long wr0, wr1;
@@ -495,23 +558,6 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   const int n_splits = (S + SPLIT - 1) / SPLIT;
   const int Hq = a.Hkv * G;
 
-  // ---- q of the G heads, octet layout: lane owns dims 8*EPV*cc + EPV*o + e ----
-  const int o = lane & 7;
-  float qr[G][CK::QPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float* qh = a.q + (static_cast<long>(b) * Hq + kvh * G + g) * DH + CK::EPV * o;
-#pragma unroll
-    for (int cc = 0; cc < CK::NCQ; ++cc)
-#pragma unroll
-      for (int e4 = 0; e4 < CK::EPV; e4 += 4) {
-        const float4 x = *reinterpret_cast<const float4*>(qh + 8 * CK::EPV * cc + e4);
-        qr[g][cc * CK::EPV + e4] = x.x;
-        qr[g][cc * CK::EPV + e4 + 1] = x.y;
-        qr[g][cc * CK::EPV + e4 + 2] = x.z;
-        qr[g][cc * CK::EPV + e4 + 3] = x.w;
-      }
-  }
   const float* rope_cs = nullptr;  // (cos, sin) pairs of this stream's position (QKN)
   if constexpr (QKN) {
     rope_cs = a.rope + static_cast<long>(min(max(pos_b, 0), a.capacity - 1)) * DH;
@@ -675,7 +721,7 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-      unsigned* ctr = a.arrive + static_cast<long>(b) * a.Hkv + kvh;
+      unsigned* ctr = a.arrive + (static_cast<long>(b) * a.Hkv + kvh) * kCounterStride;
       const unsigned prev =
           __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const int last = prev + 1 == static_cast<unsigned>(n_splits);
@@ -689,9 +735,13 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
       const int d = idx % DH;
       const long bh = static_cast<long>(b) * Hq + kvh * G + g;
       const long base = bh * a.max_splits;
-      SplitBatch A;
-      load_splits<DH, true>(A, a, base, 0, d);
-      a.out[bh * DH + d] = merge_splits<DH, true>(a, base, d, n_splits, A);
+      if (n_splits <= kWave && DH % kWave == 0) {  // a wave's lanes share g: wave-wide merge
+        a.out[bh * DH + d] = merge_splits_wave<DH>(a, base, d, n_splits, lane);
+      } else {
+        SplitBatch A;
+        load_splits<DH, true>(A, a, base, 0, d);
+        a.out[bh * DH + d] = merge_splits<DH, true>(a, base, d, n_splits, A);
+      }
     }
   }
 }
@@ -914,7 +964,7 @@ void gqa_decode_wide_kernel(DecodeArgs a, int split_len) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-      unsigned* ctr = a.arrive + static_cast<long>(b) * a.Hkv + kvh;
+      unsigned* ctr = a.arrive + (static_cast<long>(b) * a.Hkv + kvh) * kCounterStride;
       const unsigned prev =
           __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const int last = prev + 1 == static_cast<unsigned>(n_parts);
@@ -1140,10 +1190,12 @@ size_t decode_workspace_bytes(int B, int Hq, int Dh, int capacity) {
 int zeroed_counters(hipStream_t stream, int slot, unsigned** out) {
   bool fresh = false;
   *out = static_cast<unsigned*>(
-      workspace(stream, kArriveCounters * sizeof(unsigned), slot, &fresh));
+      workspace(stream, static_cast<size_t>(kArriveCounters) * kCounterStride * sizeof(unsigned),
+                slot, &fresh));
   if (!*out) return ORATOR_ERR_HIP;
   if (fresh) {
-    hipLaunchKernelGGL(zero_u32_kernel, dim3(kArriveCounters / 256), dim3(256), 0, stream, *out);
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(kArriveCounters * kCounterStride / 256), dim3(256), 0,
+                       stream, *out);
     return check_launch("zero_u32_kernel");
   }
   return ORATOR_OK;
@@ -1288,7 +1340,8 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
 // The counters start at zero (static storage is zero-initialized) and every launch that uses
 // them leaves them at zero.
 constexpr size_t kStaticScratchBytes = size_t{16} << 20;
-constexpr size_t kStaticPartialBytes = kStaticScratchBytes - kArriveCounters * sizeof(unsigned);
+constexpr size_t kStaticPartialBytes =
+    kStaticScratchBytes - size_t{kArriveCounters} * kCounterStride * sizeof(unsigned);
 static __device__ __align__(256) float scratch[kStaticScratchBytes / sizeof(float)];
 
 namespace {

@@ -106,13 +106,19 @@ struct DecodeProblem {
   // workspace; a launch needing more fails with ORATOR_ERR_CAPACITY.
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
-  // With scratch: kArriveCounters arrival counters, zero between launches, for the split
+  // With scratch: kArriveCounters arrival counters (kCounterStride apart), zero between
+  // launches, for the split
   // merge inside the split launch (small grids); nullptr runs the separate merge kernel.
   unsigned* arrive = nullptr;
 };
 constexpr int kArriveCounters = 4096;
-// A block of kArriveCounters counters in workspace slot `slot` of the stream, zeroed by a fill
-// kernel when the block is allocated; the kernels using it return every counter to zero.
+// Counters are kCounterStride u32 apart, each on its own 128-byte line: agent-scope atomics on
+// one line are serialised where they are performed (the 264 adds of a B = 1 decode on one
+// line took ~2.5 us).
+constexpr int kCounterStride = 32;
+// A block of kArriveCounters counters (kCounterStride apart) in workspace slot `slot` of the
+// stream, zeroed by a fill kernel when the block is allocated; the kernels using it return
+// every counter to zero.
 int zeroed_counters(hipStream_t stream, int slot, unsigned** out);
 // Long-prompt bf16 prefill over a contiguous cache, one wave per SIMD with stream-K balance
 // (prefill_sk.hip); Dh 128, Hq / Hkv in {1, 2, 4}, Hkv * ceil(Tq / (128 / G)) <= kArriveCounters.

@@ -55,7 +55,7 @@ struct SkArgs {
   const int* pos0p;
   float* out;              // [Tq, Hq, Dh] fp32
   float* part;             // [gridDim.x][2 slots][kSkPartSlot]
-  unsigned* arrive;        // [Hkv][n_blocks], zero between launches
+  unsigned* arrive;        // [Hkv][n_blocks] kCounterStride apart, zero between launches
   int Tq, Hq, Hkv, capacity;
   int n_blocks;            // token blocks per kv head
   int wgs;                 // workgroups per kv head
@@ -630,7 +630,7 @@ void gqa_prefill_sk_kernel(SkArgs a) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (tid == 0) {
-          unsigned* ctr = a.arrive + static_cast<long>(kvh) * n + b;
+          unsigned* ctr = a.arrive + (static_cast<long>(kvh) * n + b) * kCounterStride;
           const unsigned prev =
               __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           const int last = prev + 1 == static_cast<unsigned>(w2 - w1 + 1);

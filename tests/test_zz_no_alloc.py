@@ -41,7 +41,8 @@ def test_noalloc_matches_allocating_entry_twice():
     # second call smaller (fewer streams, shorter contexts): stale partials of the first call
     # stay in the scratch and must not leak into it
     # (the smaller calls are small grids: their splits are merged inside the split launch,
-    # with arrival counters in the scratch's last 16 KiB, left at zero by every launch)
+    # with arrival counters in the scratch's last 512 KiB, one per 128-byte line, left at zero
+    # by every launch)
     for seed, lens in ((1, [4097 + i for i in range(16)]), (2, [700, 1, 129]), (3, [2000])):
         q, kp, vp, table, max_pages, ps, pos = _case(seed, lens)
         B = len(lens)
