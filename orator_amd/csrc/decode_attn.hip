@@ -1635,6 +1635,15 @@ int orator_decode_read_probe(const uint16_t* kpool, const uint16_t* vpool, const
 int orator_window_attention(const float* q, const float* k, const float* v, float* out,
                             const int* d_seg_start, const int* d_seg_end, int N, int H, int Dh,
                             float scale, void* stream) {
+  // 64-wide heads (the audio tower's): a workgroup per 32-query block and head over the
+  // union of the block's windows, on fp32 MFMA (range_attn.hip); 128-wide heads: every query
+  // as a stream of the split decode kernel below
+  if (Dh == 64 && N > 0 && H > 0) {
+    if (!q || !k || !v || !out || !d_seg_start || !d_seg_end)
+      return fail(ORATOR_ERR_INVALID, "window_attention: null pointer");
+    return launch_range_attention(q, k, v, out, d_seg_start, d_seg_end, N, H, Dh, 0, scale,
+                                  static_cast<hipStream_t>(stream));
+  }
   DecodeProblem p{};
   p.q = q;
   p.kpool = k;

@@ -126,6 +126,13 @@ int launch_prefill_sk(const float* q, const uint16_t* q_bf16, const uint16_t* kc
                       const uint16_t* vc, float* out, int Tq, int Hq, int Hkv,
                       const int* d_pos0, int capacity, float scale, hipStream_t stream);
 int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
+// Self-attention of fp32 [N, H, Dk] rows, Dk in {24, 32, 64}, on fp32 MFMA (range_attn.hip):
+// query i attends keys [seg_start[i], seg_end[i]) clamped into [0, N) (device arrays), or
+// without them keys [0, valid) (valid <= 0: a uniform softmax over all N keys); zeros for an
+// empty range.  q, k, v 16-byte aligned.
+int launch_range_attention(const float* q, const float* k, const float* v, float* out,
+                           const int* seg_start, const int* seg_end, int N, int H, int Dk,
+                           int valid, float scale, hipStream_t s);
 // asr_ops::GqaAttention for any power-of-two Dh <= 1024 and any Hq multiple of Hkv
 // (attention_generic.hip); the split-K kernel serves Dh 64 / 128 with Hq / Hkv in {1, 2, 4}.
 int launch_gqa_attention_generic(const float* q, const float* k, const float* v, float* out,
