@@ -35,6 +35,10 @@ COMMON_FLAGS = [
     "-I", str(ROOT / "include"),
     # Packed-fp32 selection is off for all device code (v_pk_*_f32 forms are avoided).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # The first 16 kernel-argument dwords arrive in SGPRs (the code object keeps the s_load
+    # prologue for firmware that does not preload): the decode step's per-token time measured
+    # 1.108 -> 1.101 ms, every GPU test passing on the preloading build.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 
