@@ -553,13 +553,31 @@ void gqa_prefill_sk_kernel(SkArgs a) {
     const int pw = (1 - grp) * 2 + rw;
     auto finish = [&]<int KD>() {
       constexpr int GD = 2 - KD;  // the half handed over
-      // m and l of every wave, then one 16-value accumulator block per pass: the values handed
-      // over (lane-contiguous float4s), a barrier, the partner's folded in, a barrier
+      // m and l of every wave and the 64 accumulator values each wave hands over (lane-
+      // contiguous float4s in a K ring stage of its own: the rings are idle once the rounds'
+      // loads have landed, and the next segment's first LDS-DMA waits behind the barrier at
+      // its start), one barrier, then the partner's half folded in: one barrier where a
+      // 16 KB area passed one 16-value block at a time needed eight
+      float4* const xo_mine = reinterpret_cast<float4*>(
+          wave == 0 ? &ks0[0][0][0] : wave == 1 ? &ks1[0][0][0] : wave == 2 ? &ks2[0][0][0]
+                                                                              : &ks3[0][0][0]);
+      const float4* const xo_part = reinterpret_cast<const float4*>(
+          pw == 0 ? &ks0[0][0][0] : pw == 1 ? &ks1[0][0][0] : pw == 2 ? &ks2[0][0][0]
+                                                                      : &ks3[0][0][0]);
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
         s_xml[wave][cb][lane] = m[cb];
         s_xml[wave][2 + cb][lane] = lsum[cb];
       }
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            xo_mine[((cb * 2 + i) * 4 + q4) * 64 + lane] =
+                make_float4(o[cb][GD + i][4 * q4], o[cb][GD + i][4 * q4 + 1],
+                            o[cb][GD + i][4 * q4 + 2], o[cb][GD + i][4 * q4 + 3]);
       float M[2], L[2], wo[2], wp[2];
       __syncthreads();
 #pragma unroll
@@ -575,23 +593,15 @@ void gqa_prefill_sk_kernel(SkArgs a) {
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-            s_xo[wave][q4][lane] =
-                make_float4(o[cb][GD + i][4 * q4], o[cb][GD + i][4 * q4 + 1],
-                            o[cb][GD + i][4 * q4 + 2], o[cb][GD + i][4 * q4 + 3]);
-          __syncthreads();
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
-            const float4 x = s_xo[pw][q4][lane];
+            const float4 x = xo_part[((cb * 2 + i) * 4 + q4) * 64 + lane];
             o[cb][KD + i][4 * q4] = wo[cb] * o[cb][KD + i][4 * q4] + wp[cb] * x.x;
             o[cb][KD + i][4 * q4 + 1] = wo[cb] * o[cb][KD + i][4 * q4 + 1] + wp[cb] * x.y;
             o[cb][KD + i][4 * q4 + 2] = wo[cb] * o[cb][KD + i][4 * q4 + 2] + wp[cb] * x.z;
             o[cb][KD + i][4 * q4 + 3] = wo[cb] * o[cb][KD + i][4 * q4 + 3] + wp[cb] * x.w;
           }
-          __syncthreads();  // the area is free for the next pass
-        }
 
       // ---- whole block: normalise and store; cut block: a partial, and the last
       // workgroup to finish the block merges the partials ----
