@@ -95,6 +95,22 @@ __device__ __forceinline__ void lds_barrier() {
 // Raw v_exp_f32 (2^x); 2^-inf = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// (float)(1 / sqrt((double)x)) for x > 0 -- the RMSNorm factor the oracle forms (a correctly
+// rounded double rounded to float) -- by two fp64 Newton steps y += y/2 (1 - x y^2) from the
+// fp32 estimate v_rsq_f32: from a 1-ulp start the double is within a few of its ulps of the
+// exact value, so its rounding to float agrees with the double formula's except within ~2^-28
+// of a float rounding boundary (no mismatch in 3e8 sampled inputs against the formula), in 4
+// fp64 FMAs and 2 multiplies where the correctly rounded fp64 sqrt and division expand to ~30
+// instructions on a dependent chain.
+__device__ __forceinline__ float rsqrt_via_f64(float x) {
+  const double xd = static_cast<double>(x);
+  double y = static_cast<double>(__builtin_amdgcn_rsqf(x));
+  if (!(y < static_cast<double>(INFINITY))) return static_cast<float>(1.0 / sqrt(xd));  // x = 0
+#pragma unroll
+  for (int i = 0; i < 2; ++i) y = __builtin_fma(0.5 * y, __builtin_fma(-xd * y, y, 1.0), y);
+  return static_cast<float>(y);
+}
+
 // ---- KV addressing ----
 // A cache is a pool of rows [row][Hkv][Dh].  Paged: absolute position j lives in page
 // page_table[j >> page_shift], row (page << page_shift) | (j & mask).  Contiguous:

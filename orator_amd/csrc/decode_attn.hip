@@ -83,8 +83,30 @@ struct DecodeArgs {
 // 128-dim head held in the octet layout: lane o of each 8-lane group owns dims 8o + e and
 // 64 + 8o + e (x[e], x[8 + e]), so every RoPE pair is lane-local; the sum of squares is
 // reduced over the octet.  Same operations as the fused QK-norm/RoPE kernel (no contraction).
-__device__ __forceinline__ void qk_norm_rope_octet(float (&x)[16], const float* w, float eps,
-                                                   const float* cs, int o) {
+// The operands are loaded by load_norm_rope (this lane's 16 weights and 8 (cos, sin) pairs,
+// 16-byte loads) so that a caller can have them in flight with other loads before it waits.
+struct NormRope {
+  float w[16];   // w[8o + e], w[64 + 8o + e]
+  float cs[16];  // cos, sin of pairs 8o .. 8o + 7
+};
+__device__ __forceinline__ void load_norm_rope(NormRope& nr, const float* w, const float* cs,
+                                               int o) {
+  const float4* w0 = reinterpret_cast<const float4*>(w + 8 * o);
+  const float4* w1 = reinterpret_cast<const float4*>(w + 64 + 8 * o);
+  const float4* c4 = reinterpret_cast<const float4*>(cs + 16 * o);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float4 a = w0[i], b = w1[i];
+    nr.w[4 * i] = a.x; nr.w[4 * i + 1] = a.y; nr.w[4 * i + 2] = a.z; nr.w[4 * i + 3] = a.w;
+    nr.w[8 + 4 * i] = b.x; nr.w[9 + 4 * i] = b.y; nr.w[10 + 4 * i] = b.z; nr.w[11 + 4 * i] = b.w;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 c = c4[i];
+    nr.cs[4 * i] = c.x; nr.cs[4 * i + 1] = c.y; nr.cs[4 * i + 2] = c.z; nr.cs[4 * i + 3] = c.w;
+  }
+}
+__device__ __forceinline__ void norm_rope_apply(float (&x)[16], const NormRope& nr, float eps) {
 #pragma clang fp contract(off)
   float ss = 0.0f;
 #pragma unroll
@@ -92,15 +114,20 @@ __device__ __forceinline__ void qk_norm_rope_octet(float (&x)[16], const float* 
   ss += dpp<0xB1>(ss);
   ss += dpp<0x4E>(ss);
   ss += dpp<0x141>(ss);
-  const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss / 128.0f + eps)));
+  const float inv = rsqrt_via_f64(ss / 128.0f + eps);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int j = 8 * o + e;
-    const float n0 = x[e] * inv * w[j], n1 = x[8 + e] * inv * w[j + 64];
-    const float c = cs[2 * j], s = cs[2 * j + 1];
+    const float n0 = x[e] * inv * nr.w[e], n1 = x[8 + e] * inv * nr.w[8 + e];
+    const float c = nr.cs[2 * e], s = nr.cs[2 * e + 1];
     x[e] = n0 * c - n1 * s;
     x[8 + e] = n1 * c + n0 * s;
   }
+}
+__device__ __forceinline__ void qk_norm_rope_octet(float (&x)[16], const float* w, float eps,
+                                                   const float* cs, int o) {
+  NormRope nr;
+  load_norm_rope(nr, w, cs, o);
+  norm_rope_apply(x, nr, eps);
 }
 
 // Number of keys stream b attends, clamped to the capacity; pos_b = pos[b] (pos_mode 0).
@@ -558,11 +585,16 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   const int n_splits = (S + SPLIT - 1) / SPLIT;
   const int Hq = a.Hkv * G;
 
+  // QK-norm folding: the q-norm weights and the position's RoPE pairs are loaded here, ahead
+  // of the wave's K/V chunk, and applied after the chunk's loads are issued: loads return in
+  // issue order, so the q-norm then runs while the chunk streams in (applied before the
+  // chunk's loads went out, it delayed them by the table read and the norm, ~1.1 us per
+  // layer at B = 1).
   const float* rope_cs = nullptr;  // (cos, sin) pairs of this stream's position (QKN)
+  NormRope qnr;
   if constexpr (QKN) {
     rope_cs = a.rope + static_cast<long>(min(max(pos_b, 0), a.capacity - 1)) * DH;
-#pragma unroll
-    for (int g = 0; g < G; ++g) qk_norm_rope_octet(qr[g], a.q_norm, a.eps, rope_cs, o);
+    load_norm_rope(qnr, a.q_norm, rope_cs, o);
   }
 
   const long kv_base = (a.page_table ? 0 : static_cast<long>(b) * a.stream_stride) +
@@ -597,17 +629,27 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
   }
   const int r = lane / CK::LPT;
 
+  auto apply_qnorm = [&]() {
+    if constexpr (QKN) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) norm_rope_apply(qr[g], qnr, a.eps);
+    }
+  };
   if constexpr (TPW == CK::CH) {
     // one chunk per wave (128-key splits): no second buffer
     if (w0 < w_end) {
       CK A;
       load_chunk<DH, KV>(A, kbase, vbase, wr0, wr1, rs, w0, w_end, lane);
+      apply_qnorm();
       process_chunk<DH, G, KV>(A, qr, m, lpart, acc, w0, w_end, lane, a.scale_log2e);
+    } else {
+      apply_qnorm();  // the appended key's score needs the normed q
     }
   } else if (w0 < w_end) {
     // Ping-pong buffers: the loads of one chunk are in flight while the other is computed.
     CK A, Bb;
     load_chunk<DH, KV>(A, kbase, vbase, wr0, wr1, rs, w0, w_end, lane);
+    apply_qnorm();
     int c = w0;
     while (true) {
       if (c + CK::CH < w_end) {
@@ -627,6 +669,8 @@ __global__ __launch_bounds__((64 * decode_waves<SPLIT, KV, G>())) __attribute__(
       c += CK::CH;
       if (c >= w_end) break;
     }
+  } else {
+    apply_qnorm();  // no cached keys in this wave's range: the appended key may still be its
   }
   if constexpr (sizeof(KV) == 2) {
     if (owns_new) {  // uniform over the wave

@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
     }
     const float sum = wave_sum(local);
     const float ms = sum / static_cast<float>(dim) + eps;
-    const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+    const float inv = rsqrt_via_f64(ms);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int d = lane * 4 + 256 * i;
@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
   }
   const float sum = wave_sum(local);
   const float ms = sum / static_cast<float>(dim) + eps;
-  const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+  const float inv = rsqrt_via_f64(ms);
   if (VEC) {
     for (int d = lane * 4; d < dim; d += 256) {
       const float4 v = *reinterpret_cast<const float4*>(xr + d);
@@ -404,7 +404,7 @@ __device__ __forceinline__ void qkv_row(const QkvArgs& a, int t, int hh, int lan
                   : a.k + t * a.kv_stride + static_cast<long>(h) * Dh;
   const float* w = is_q ? a.q_norm : a.k_norm;
   const float ss = wave_sum(x0 * x0 + x1 * x1);
-  const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss / Dh + a.eps)));
+  const float inv = rsqrt_via_f64(ss / Dh + a.eps);
   const float n0 = x0 * inv * w[lane], n1 = x1 * inv * w[lane + half];
   const float r0 = n0 * c - n1 * s;
   const float r1 = n1 * c + n0 * s;

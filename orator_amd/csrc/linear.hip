@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
     lds_barrier();
     const float sum = (red[0] + red[1]) + (red[2] + red[3]);
     const float ms = sum / static_cast<float>(K) + eps;
-    const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ms)));
+    const float inv = rsqrt_via_f64(ms);
     auto put = [&](int d, float4 v, float4 g) {
       *reinterpret_cast<uint2*>(xs + d) =
           make_uint2(pack_bf16x2(v.x * inv * g.x, v.y * inv * g.y),
