@@ -139,6 +139,11 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
     xr[i] = *reinterpret_cast<const float4*>(x + d);
     if constexpr (kAux) ar[i] = *reinterpret_cast<const float4*>(aux + d);
   }
+  // ACC: the residual this lane adds its output to, read now (only this launch writes these
+  // rows, at its end): read after the reduction it was one more memory round trip at the end
+  // of every o / down projection
+  float res = 0.0f;
+  if constexpr (ACC) res = out[min(row0 + min(lane, RO - 1), N - 1)];
 
   // the row's loads go out before the weights' (x and aux are not __restrict__, so this
   // fence also keeps the compiler from sinking them to their uses)
@@ -249,9 +254,8 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
         if constexpr (PAIR) up = acc[RO + r];
       }
     if constexpr (PAIR) v = (v / (1.0f + expf(-v))) * up;
-    float* o = out + row0 + lane;
-    if constexpr (ACC) v = *o + v;
-    *o = v;
+    if constexpr (ACC) v = res + v;
+    out[row0 + lane] = v;
   }
 }
 
