@@ -102,8 +102,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_bf16_kernel(
 // weight loads (U 16-byte chunks per lane and row: U = 4 holds a 2048-wide row, 12 a 6144-wide
 // one), are issued before the row is built, so the prologue runs under the weights' HBM
 // latency; longer rows ping-pong two batches.
-template <int MODE, int R, bool ACC, int U, bool PAIR>
-__global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const float* aux,
+template <int MODE, int R, bool ACC, int U, bool PAIR, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) void gemv_fused_kernel(const float* x, const float* aux,
                                                          float eps,
                                                          const uint16_t* __restrict__ W,
                                                          float* __restrict__ out, int K, int N) {
@@ -111,11 +111,13 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
   constexpr int RO = PAIR ? R / 2 : R;  // outputs per wave
   static_assert(!PAIR || R % 2 == 0, "paired rows");
   __shared__ __align__(16) uint16_t xs[kFusedMaxK];
-  __shared__ float red[4];
+  static_assert(NWV == 4 || NWV == 8, "4 or 8 waves per workgroup");
+  constexpr int XS = 4 * 64 * NWV;  // input elements per pass of the workgroup (4 per thread)
+  __shared__ float red[NWV];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int row0 = (blockIdx.x * 4 + wave) * RO;
+  const int row0 = (blockIdx.x * NWV + wave) * RO;
   const int nchunk = K >> 3;
   const u32x4_t* wr[R];
 #pragma unroll
@@ -127,7 +129,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
   // The input row (and the RMSNorm gain or the SwiGLU up values) is read into registers
   // before the first batch of weight loads: loads return in issue order, so the row issued
   // after the weights would wait out their HBM latency before the prologue could start.
-  constexpr int NX = U == 4 ? 2 : 6;  // float4 per thread held: K <= 2048 / 6144 (then the loop)
+  constexpr int NX = (U == 4 ? 2048 : 6144) / XS;  // float4 per thread held: K <= 2048 / 6144
   constexpr bool kAux = MODE == kGemvInRmsNorm || MODE == kGemvInSwiglu;
   // Both the row and the weights are loaded without branches (indices clamped in range; the
   // values past the end are never used): a branch per load leaves the wait before the
@@ -135,7 +137,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
   float4 xr[NX], ar[NX];
 #pragma unroll
   for (int i = 0; i < NX; ++i) {
-    const int d = min(4 * tid + 1024 * i, K - 4);
+    const int d = min(4 * tid + XS * i, K - 4);
     xr[i] = *reinterpret_cast<const float4*>(x + d);
     if constexpr (kAux) ar[i] = *reinterpret_cast<const float4*>(aux + d);
   }
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
     float local = 0.0f;
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const int d = 4 * tid + 1024 * i;
+      const int d = 4 * tid + XS * i;
       if (d < K) {
         const float4 v = xr[i];
         local += v.x * v.x;
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
         local += v.w * v.w;
       }
     }
-    for (int d = 4 * tid + 1024 * NX; d < K; d += 1024) {
+    for (int d = 4 * tid + XS * NX; d < K; d += XS) {
       const float4 v = *reinterpret_cast<const float4*>(x + d);
       local += v.x * v.x;
       local += v.y * v.y;
@@ -183,7 +185,8 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
     const float ws = wave_sum(local);
     if (lane == 0) red[wave] = ws;
     lds_barrier();
-    const float sum = (red[0] + red[1]) + (red[2] + red[3]);
+    float sum = (red[0] + red[1]) + (red[2] + red[3]);
+    if constexpr (NWV == 8) sum += (red[4] + red[5]) + (red[6] + red[7]);
     const float ms = sum / static_cast<float>(K) + eps;
     const float inv = rsqrt_via_f64(ms);
     auto put = [&](int d, float4 v, float4 g) {
@@ -193,8 +196,8 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
     };
 #pragma unroll
     for (int i = 0; i < NX; ++i)
-      if (4 * tid + 1024 * i < K) put(4 * tid + 1024 * i, xr[i], ar[i]);
-    for (int d = 4 * tid + 1024 * NX; d < K; d += 1024)
+      if (4 * tid + XS * i < K) put(4 * tid + XS * i, xr[i], ar[i]);
+    for (int d = 4 * tid + XS * NX; d < K; d += XS)
       put(d, *reinterpret_cast<const float4*>(x + d), *reinterpret_cast<const float4*>(aux + d));
   } else {
     auto put = [&](int d, float4 v, float4 u) {
@@ -211,8 +214,8 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const float* x, const f
     };
 #pragma unroll
     for (int i = 0; i < NX; ++i)
-      if (4 * tid + 1024 * i < K) put(4 * tid + 1024 * i, xr[i], ar[i]);
-    for (int d = 4 * tid + 1024 * NX; d < K; d += 1024)
+      if (4 * tid + XS * i < K) put(4 * tid + XS * i, xr[i], ar[i]);
+    for (int d = 4 * tid + XS * NX; d < K; d += XS)
       put(d, *reinterpret_cast<const float4*>(x + d),
           kAux ? *reinterpret_cast<const float4*>(aux + d) : make_float4(0.0f, 0.0f, 0.0f, 0.0f));
   }
@@ -282,8 +285,10 @@ int launch_fused_u(const float* x, const float* aux, float eps, const uint16_t* 
     hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC, U, false>), dim3((N + 7) / 8), dim3(256),
                        0, s, x, aux, eps, W, out, K, N);
   } else {
-    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 1, ACC, U, false>), dim3((N + 3) / 4), dim3(256),
-                       0, s, x, aux, eps, W, out, K, N);
+    // one row per wave, 8 waves per workgroup: half the workgroups each rebuilding the input
+    // row (the 2048-wide qkv and o projections)
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 1, ACC, U, false, 8>), dim3((N + 7) / 8),
+                       dim3(512), 0, s, x, aux, eps, W, out, K, N);
   }
   return check_launch("gemv_fused_kernel");
 }
