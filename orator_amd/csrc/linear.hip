@@ -277,8 +277,8 @@ int launch_fused_u(const float* x, const float* aux, float eps, const uint16_t* 
     hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC, U, true>), dim3((N + 3) / 4), dim3(256),
                        0, s, x, aux, eps, W, out, K, N);
   } else if (N >= 32768) {
-    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 4, ACC, U, false>), dim3((N + 15) / 16),
-                       dim3(256), 0, s, x, aux, eps, W, out, K, N);
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 4, ACC, U, false, 8>), dim3((N + 31) / 32),
+                       dim3(512), 0, s, x, aux, eps, W, out, K, N);
   } else if (N >= 8192 || U == 12) {
     // two rows per wave also for the long rows (K > 2048: the down projection): half the
     // workgroups each building the 6144-wide input row (1.151 -> 1.137 ms per decode token)
