@@ -279,11 +279,13 @@ int launch_fused_u(const float* x, const float* aux, float eps, const uint16_t* 
   } else if (N >= 32768) {
     hipLaunchKernelGGL((gemv_fused_kernel<MODE, 4, ACC, U, false, 8>), dim3((N + 31) / 32),
                        dim3(512), 0, s, x, aux, eps, W, out, K, N);
-  } else if (N >= 8192 || U == 12) {
-    // two rows per wave also for the long rows (K > 2048: the down projection): half the
-    // workgroups each building the 6144-wide input row (1.151 -> 1.137 ms per decode token)
+  } else if (N >= 8192) {
     hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC, U, false>), dim3((N + 7) / 8), dim3(256),
                        0, s, x, aux, eps, W, out, K, N);
+  } else if (U == 12) {
+    // the long rows (K > 2048: the down projection): 8 rows per workgroup, one per wave
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 1, ACC, U, false, 8>), dim3((N + 7) / 8),
+                       dim3(512), 0, s, x, aux, eps, W, out, K, N);
   } else {
     // one row per wave, 8 waves per workgroup: half the workgroups each rebuilding the input
     // row (the 2048-wide qkv and o projections)
