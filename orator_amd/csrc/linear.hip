@@ -265,30 +265,30 @@ __global__ __launch_bounds__(64 * NWV) void gemv_fused_kernel(const float* x, co
 template <int MODE, bool ACC, int U>
 int launch_fused_u(const float* x, const float* aux, float eps, const uint16_t* W, float* out,
                    int K, int N, bool pair, hipStream_t s) {
-  // rows per wave: enough waves to cover the chip for small N, fewer input-row rebuilds
-  // (one per workgroup) for the vocabulary-sized projection
+  // Rows per wave and waves per workgroup: enough waves to cover the chip, one input-row
+  // rebuild per workgroup.  8-wave workgroups halve the rebuilds (each re-reads the fp32 row
+  // and, for RMSNorm, its gain through L2) and give the one-row waves more company per CU;
+  // measured against 4-wave ones on the decode step (same box, alternating runs): qkv / o
+  // 1.062 -> 1.055 ms per token, lm_head 1.056 -> 1.051, down (one 6144-wide row per wave
+  // instead of two) 1.051 -> 1.038, gate|up (one gate/up pair per wave instead of two)
+  // 1.038 -> 1.026.
   if (pair && U == 4) {
-    // two gate|up output pairs per wave (4 weight rows): the 6144-pair projection is 768
-    // workgroups, one round at 3 per CU (one pair per wave needed 1536, a 5-per-CU round
-    // plus a sparse tail)
-    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 4, ACC, U, true>), dim3((N + 7) / 8), dim3(256),
-                       0, s, x, aux, eps, W, out, K, N);
+    // the 6144-pair gate|up projection: one pair per wave, 768 workgroups of 8 waves
+    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC, U, true, 8>), dim3((N + 7) / 8),
+                       dim3(512), 0, s, x, aux, eps, W, out, K, N);
   } else if (pair) {
     hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC, U, true>), dim3((N + 3) / 4), dim3(256),
                        0, s, x, aux, eps, W, out, K, N);
   } else if (N >= 32768) {
+    // the vocabulary-sized projection: 4 rows per wave, 32 rows per workgroup
     hipLaunchKernelGGL((gemv_fused_kernel<MODE, 4, ACC, U, false, 8>), dim3((N + 31) / 32),
                        dim3(512), 0, s, x, aux, eps, W, out, K, N);
   } else if (N >= 8192) {
     hipLaunchKernelGGL((gemv_fused_kernel<MODE, 2, ACC, U, false>), dim3((N + 7) / 8), dim3(256),
                        0, s, x, aux, eps, W, out, K, N);
-  } else if (U == 12) {
-    // the long rows (K > 2048: the down projection): 8 rows per workgroup, one per wave
-    hipLaunchKernelGGL((gemv_fused_kernel<MODE, 1, ACC, U, false, 8>), dim3((N + 7) / 8),
-                       dim3(512), 0, s, x, aux, eps, W, out, K, N);
   } else {
-    // one row per wave, 8 waves per workgroup: half the workgroups each rebuilding the input
-    // row (the 2048-wide qkv and o projections)
+    // one row per wave, 8 rows per workgroup: the 2048-wide qkv and o projections, and the
+    // 6144-wide rows of the down projection
     hipLaunchKernelGGL((gemv_fused_kernel<MODE, 1, ACC, U, false, 8>), dim3((N + 7) / 8),
                        dim3(512), 0, s, x, aux, eps, W, out, K, N);
   }
