@@ -28,7 +28,6 @@ int check_launch(const char* what);
 // Slots are independent blocks: kWsGemm holds the split-K partials of the GEMMs, which may run
 // while a caller's slot-0 buffer (e.g. the bf16 cast of a Linear input) is being read.
 constexpr int kWsGemm = 1;
-constexpr int kWsMha = 2;     // key-split partials of the small-head masked MHA
 constexpr int kWsArrive = 3;  // arrival counters of the decode's in-launch split merge
 constexpr int kWsPrefill = 4;        // partials of the long-prompt prefill's cut blocks
 constexpr int kWsPrefillArrive = 5;  // its arrival counters

@@ -162,6 +162,32 @@ def test_decode_paged_wide_ranges(B, Hq, Hkv, Dh):
                truth=t64.decode_paged(q, kp, vp, table, ps, pos, scale))
 
 
+def test_decode_paged_wide_merge_three_and_four_ranges():
+    """Wide-kernel grids of 4 ranges (8 streams) and 3 ranges (12 streams) per (stream, kv
+    head), whose last range merges the others' partials inside the launch: streams ending in
+    every range (1 .. 4 ranges used), each launch against the oracle, and the first case run
+    again after the second (the pair blocks' partial words then hold two earlier launches')
+    with bit-identical output."""
+    Hq, Hkv, Dh, ps = 16, 8, 128, 16
+    cases = [[8200, 6150, 4100, 2050, 1, 8192, 5000, 3000],
+             [6000, 1, 1792, 1793, 3584, 3585, 5999, 100, 4000, 2500, 17, 5376]]
+    outs = []
+    for i, lens in enumerate(cases + cases[:1]):
+        q, kp, vp, table, pos = _paged_case(900 + i % 2, lens, Hq, Hkv, Dh, ps)
+        B, max_pages = table.shape
+        scale = 1.0 / math.sqrt(Dh)
+        dout = empty((B, Hq, Dh), np.float32)
+        say("decode wide merge", i, B, max_pages * ps)
+        da.GqaDecodeAttnPaged(up(q), up(kp), up(vp), up(table), max_pages, ps, up(pos), dout, B,
+                              Hq, Hkv, Dh, scale)
+        got = down(dout, (B, Hq, Dh))
+        outs.append(got)
+        if i < 2:
+            ref = orc.gqa_decode_paged(q, kp, vp, table, ps, pos, scale, threads=8)
+            check_fp32(got, ref, TOL, truth=t64.decode_paged(q, kp, vp, table, ps, pos, scale))
+    np.testing.assert_array_equal(outs[2], outs[0])
+
+
 def test_decode_paged_equals_contiguous_for_identity_table():
     Hq, Hkv, Dh, ps, S = 16, 8, 128, 16, 1000
     q, kc, vc = _contig_case(12, S, 1024)
