@@ -153,7 +153,10 @@ int orator_qk_norm_rope_kv_write_table(float* q, float* k, const float* v, long 
 /* GqaDecodeAttnKernel (src/model/asr_text_decoder.cu:149-213, launch :416-418):
  * q [Hq, Dh] fp32 attends the S = *d_pos + 1 keys of the bf16 cache kc/vc.
  * `capacity` (the cache's max_seq_len) sizes the split-K grid; S is clamped to it.
- * Any S is supported (the reference stops at 2048). */
+ * Any S is supported (the reference stops at 2048).  Any Dh in [1, 1024] and any Hq multiple
+ * of Hkv (as the reference): Dh 64 / 128 with Hq/Hkv in {1,2,4} run on the split-K kernels,
+ * other shapes on a generic kernel; the same holds for every decode entry point below except
+ * the QK-norm folding ones (Dh 128, Hq/Hkv in {1,2,4}). */
 int orator_gqa_decode(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int Hq,
                       int Hkv, int Dh, const int* d_pos, int capacity, float scale, void* stream);
 /* Batched paged decode: stream b's q [Hq, Dh] attends d_pos[b] + 1 keys through page-table
@@ -219,9 +222,9 @@ int orator_gqa_decode_append_paged(const float* q, const float* k_new, const flo
                                    void* stream);
 
 /* WindowAttnKernel (src/model/asr_audio_tower.cu:204-258, launch :573-575): the audio tower's
- * self-attention, q/k/v fp32 [N, H, Dh] with Dh in {64, 128}; query i attends keys
- * [seg_start[i], seg_end[i]) (device int arrays, clamped into [0, N)); online softmax, zeros
- * for an empty window.  The kernel has no reference launcher: the parameters mirror its
+ * self-attention, q/k/v fp32 [N, H, Dh] (Dh in [1, 1024]; 64 and 128 on the fast kernels);
+ * query i attends keys [seg_start[i], seg_end[i]) (device int arrays, clamped into [0, N));
+ * online softmax, zeros for an empty window.  The kernel has no reference launcher: the parameters mirror its
  * arguments. */
 int orator_window_attention(const float* q, const float* k, const float* v, float* out,
                             const int* d_seg_start, const int* d_seg_end, int N, int H, int Dh,
@@ -406,7 +409,9 @@ int orator_build_pos_emb(float* pe, int T, int d_model);
 
 /* GqaCacheAttnKernel (src/model/asr_text_decoder.cu:88-142, launch :537-541): query row t
  * (absolute position *d_pos0 + t) of q [Tq, Hq, Dh] attends keys [0, pos0 + t] of the bf16
- * cache.  fp32 mode.  `capacity` = the cache's max_seq_len (keys past it are not read). */
+ * cache.  fp32 mode.  `capacity` = the cache's max_seq_len (keys past it are not read).
+ * Any Dh in [1, 1024] and any Hq multiple of Hkv (the reference: Dh <= 256): Dh 128 with
+ * Hq/Hkv in {1,2,4} runs on the MFMA kernels, other shapes on a generic fp32 kernel. */
 int orator_gqa_prefill(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int Tq,
                        int Hq, int Hkv, int Dh, const int* d_pos0, int capacity, float scale,
                        void* stream);

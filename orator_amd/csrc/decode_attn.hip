@@ -1265,8 +1265,10 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (p.Hq % p.Hkv) return fail(ORATOR_ERR_INVALID, "gqa_decode: Hq must be a multiple of Hkv");
   if (p.B > 65535) return fail(ORATOR_ERR_UNSUPPORTED, "gqa_decode: at most 65535 streams / rows");
   const int G = p.Hq / p.Hkv;
-  if (!(p.Dh == 64 || p.Dh == 128) || !(G == 1 || G == 2 || G == 4))
-    return fail(ORATOR_ERR_UNSUPPORTED, "gqa_decode: supported Dh {64,128}, Hq/Hkv {1,2,4}");
+  // head sizes and groups the split-K kernels are not built for run on the generic kernel
+  const bool generic = !(p.Dh == 64 || p.Dh == 128) || !(G == 1 || G == 2 || G == 4);
+  if (generic && p.Dh > 1024)
+    return fail(ORATOR_ERR_UNSUPPORTED, "gqa_decode: head size above 1024");
   if (p.capacity <= 0) return fail(ORATOR_ERR_INVALID, "gqa_decode: capacity must be > 0");
   if (p.k_new) {
     if (!p.v_new || p.kv_f32 || p.pos_mode != 0)
@@ -1277,6 +1279,8 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
   if (p.q_norm && (!p.k_norm || !p.rope || !p.k_new || p.Dh != 128 || p.kv_f32))
     return fail(ORATOR_ERR_INVALID,
                 "gqa_decode: QK-norm folding needs k_norm, the RoPE table, an appended row, Dh 128");
+  if (p.q_norm && generic)
+    return fail(ORATOR_ERR_UNSUPPORTED, "gqa_decode: QK-norm folding needs Hq/Hkv in {1,2,4}");
   int page_shift = 0;
   if (p.page_table) {
     page_shift = ilog2_exact(p.page_size);
@@ -1285,6 +1289,7 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream) {
     if (static_cast<long>(p.max_pages) * p.page_size < p.capacity)
       return fail(ORATOR_ERR_CAPACITY, "gqa_decode: capacity exceeds max_pages*page_size");
   }
+  if (generic) return launch_decode_generic(p, page_shift, stream);
   // Many streams: the wide kernel (a few long ranges per (stream, kv head), one workgroup
   // each, enough ranges to give every CU a workgroup); otherwise 128-key splits.
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;

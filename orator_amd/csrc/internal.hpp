@@ -132,11 +132,22 @@ int launch_gqa_decode(const DecodeProblem& p, hipStream_t stream);
 int launch_range_attention(const float* q, const float* k, const float* v, float* out,
                            const int* seg_start, const int* seg_end, int N, int H, int Dk,
                            int valid, float scale, hipStream_t s);
-// asr_ops::GqaAttention for any power-of-two Dh <= 1024 and any Hq multiple of Hkv
-// (attention_generic.hip); the split-K kernel serves Dh 64 / 128 with Hq / Hkv in {1, 2, 4}.
+// The generic attention kernel (attention_generic.hip) for the shapes the fast kernels are not
+// built for: any Dh in [1, 1024], any Hq multiple of Hkv.
+// asr_ops::GqaAttention: fp32 self-attention over T rows.
 int launch_gqa_attention_generic(const float* q, const float* k, const float* v, float* out,
                                  int T, int Hq, int Hkv, int Dh, float scale, bool causal,
                                  hipStream_t s);
+// Prefill over a bf16 cache (contiguous, or paged through one page-table row with 2^page_shift
+// keys per page): row t attends keys [0, min(*d_pos0 + t + 1, capacity)); q fp32, or bf16
+// when q is null.
+int launch_prefill_generic(const float* q, const uint16_t* q_bf16, const uint16_t* kpool,
+                           const uint16_t* vpool, const int* page_table, int max_pages,
+                           int page_shift, float* out, int Tq, int Hq, int Hkv, int Dh,
+                           const int* d_pos0, int capacity, float scale, hipStream_t s);
+// Decode of a DecodeProblem (no QK-norm folding; the appended key, if any, is attended from
+// k_new / v_new -- the caller writes it to the cache).
+int launch_decode_generic(const DecodeProblem& p, int page_shift, hipStream_t s);
 // (cos, sin) of RoPE pair j (head_dim 128, base theta) for positions [0, n_pos): out[(p * 64 +
 // j) * 2 + {0, 1}], the values the fused QK-norm/RoPE kernels form.
 int launch_rope_table(float* out, int n_pos, float theta, hipStream_t s);

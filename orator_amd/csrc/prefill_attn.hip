@@ -722,12 +722,25 @@ int launch_prefill(const float* q, const uint16_t* q_bf16, const uint16_t* kpool
     return fail(ORATOR_ERR_INVALID, "gqa_prefill: null pointer");
   if (Hq % Hkv) return fail(ORATOR_ERR_INVALID, "gqa_prefill: Hq must be a multiple of Hkv");
   const int G = Hq / Hkv;
-  if (Dh != kDh || !(G == 1 || G == 2 || G == 4))
-    return fail(ORATOR_ERR_UNSUPPORTED, "gqa_prefill: supported Dh 128, Hq/Hkv {1,2,4}");
   if (mode != ORATOR_PREFILL_FP32 && mode != ORATOR_PREFILL_BF16)
     return fail(ORATOR_ERR_INVALID, "gqa_prefill: unknown precision mode");
   if (capacity <= 0) return fail(ORATOR_ERR_INVALID, "gqa_prefill: capacity must be > 0");
   if (!(scale > 0.0f)) return fail(ORATOR_ERR_INVALID, "gqa_prefill: scale must be > 0");
+  if (Dh != kDh || !(G == 1 || G == 2 || G == 4)) {
+    // head sizes and groups the MFMA kernels are not built for: the generic kernel (fp32
+    // arithmetic in either mode), any Dh up to 1024
+    if (Dh > 1024) return fail(ORATOR_ERR_UNSUPPORTED, "gqa_prefill: head size above 1024");
+    int shift = 0;
+    if (page_table) {
+      shift = ilog2_exact(page_size);
+      if (shift < 0 || max_pages <= 0)
+        return fail(ORATOR_ERR_INVALID, "gqa_prefill: page_size must be a power of two");
+      if (static_cast<long>(max_pages) * page_size < capacity)
+        return fail(ORATOR_ERR_CAPACITY, "gqa_prefill: capacity exceeds max_pages*page_size");
+    }
+    return launch_prefill_generic(q, q_bf16, kpool, vpool, page_table, max_pages, shift, out, Tq,
+                                  Hq, Hkv, Dh, d_pos0, capacity, scale, stream);
+  }
   // the LDS page-row table of a paged cache covers 16384 keys; contiguous rows are arithmetic
   if (page_table && capacity > 16 * kMaxRowGroups)
     return fail(ORATOR_ERR_UNSUPPORTED, "gqa_prefill: paged caches hold at most 16384 keys");

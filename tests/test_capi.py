@@ -63,12 +63,16 @@ def test_null_pointers_rejected():
 def test_unsupported_decode_shapes_rejected():
     lib = _lib.lib()
     args = (FAKE, FAKE, FAKE, FAKE)
-    # Dh = 96 is not built
-    assert lib.orator_gqa_decode(*args, 16, 8, 96, FAKE, 64, 0.1, None) == _lib.ORATOR_ERR_UNSUPPORTED
+    # any head size up to 1024 and any group run (the generic kernel); past 1024 is rejected
+    assert lib.orator_gqa_decode(*args, 16, 8, 2048, FAKE, 64, 0.1, None) == _lib.ORATOR_ERR_UNSUPPORTED
+    assert lib.orator_gqa_prefill(*args, 4, 16, 8, 1032, FAKE, 64, 0.1,
+                                  None) == _lib.ORATOR_ERR_UNSUPPORTED
     # Hq not a multiple of Hkv
     assert lib.orator_gqa_decode(*args, 12, 8, 128, FAKE, 64, 0.1, None) == _lib.ORATOR_ERR_INVALID
-    # group size 8 is not built
-    assert lib.orator_gqa_decode(*args, 64, 8, 128, FAKE, 64, 0.1, None) == _lib.ORATOR_ERR_UNSUPPORTED
+    # QK-norm folding: Dh 128 and groups {1, 2, 4} only
+    assert lib.orator_gqa_decode_append_qknorm(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64, 8, 128,
+                                               FAKE, 64, 0.1, FAKE, FAKE, 1e-6, FAKE, 64,
+                                               None) == _lib.ORATOR_ERR_UNSUPPORTED
     # paged: page size must be a power of two >= 16
     assert lib.orator_gqa_decode_paged(FAKE, FAKE, FAKE, FAKE, 8, 24, FAKE, FAKE, 1, 16, 8, 128,
                                        0.1, None) == _lib.ORATOR_ERR_INVALID
@@ -142,7 +146,7 @@ def test_noalloc_decode_rejects_sizes_past_static_scratch():
 def test_prefill_validation():
     """orator_gqa_prefill_ex rejects, before touching the device: a paged cache past the
     16384 keys its LDS page-row table holds, a page size that is not a power of two >= 16, a
-    capacity beyond max_pages * page_size, group sizes and head sizes that are not built."""
+    capacity beyond max_pages * page_size, head sizes past 1024."""
     lib = _lib.lib()
     PF32 = 0
 
@@ -155,6 +159,9 @@ def test_prefill_validation():
     assert call(FAKE, 64, 24, 16, 8, 128, 1024) == _lib.ORATOR_ERR_INVALID
     assert call(FAKE, 64, 8, 16, 8, 128, 512) == _lib.ORATOR_ERR_INVALID
     assert call(FAKE, 16, 32, 16, 8, 128, 1024) == _lib.ORATOR_ERR_CAPACITY
-    assert call(None, 0, 0, 64, 8, 128, 1024) == _lib.ORATOR_ERR_UNSUPPORTED  # group size 8
-    assert call(None, 0, 0, 16, 8, 64, 1024) == _lib.ORATOR_ERR_UNSUPPORTED   # Dh 64
+    assert call(None, 0, 0, 16, 8, 2048, 1024) == _lib.ORATOR_ERR_UNSUPPORTED  # Dh > 1024
     assert call(None, 0, 0, 12, 8, 128, 1024) == _lib.ORATOR_ERR_INVALID      # Hq % Hkv
+    # the generic kernel's paged form: a page size that is not a power of two, a capacity
+    # beyond the table (group 8 and Dh 64 are accepted: generic shapes)
+    assert call(FAKE, 64, 24, 64, 8, 128, 1024) == _lib.ORATOR_ERR_INVALID
+    assert call(FAKE, 16, 32, 16, 8, 64, 1024) == _lib.ORATOR_ERR_CAPACITY

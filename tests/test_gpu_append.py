@@ -221,3 +221,52 @@ def test_append_paged_page_sizes(ps):
                truth=t64.decode_paged(q, kp_ref, vp_ref, table, ps, pos, scale))
     np.testing.assert_array_equal(down(dk, kp.shape, np.uint16), kp_ref)
     np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp_ref)
+
+
+@pytest.mark.parametrize("Hq,Hkv,Dh", [(12, 4, 96), (8, 1, 256), (6, 6, 40)])
+def test_append_paged_generic_shapes(Hq, Hkv, Dh):
+    """Head sizes and groups the split-K kernels are not built for (GQA group 3 and 8, Dh 96 /
+    256 / 40) on the generic path: attention with the appended key read from the fp32 rows
+    (bf16-rounded), then the rows written to the cache; ragged streams, a page beyond the
+    pool (not written, still attended as the fused kernels do)."""
+    ps = 16
+    lens = [1, 300, 1025, 17]
+    r = SplitMix64(Hq * 1000 + Dh)
+    B = len(lens)
+    max_pages = max((n + ps - 1) // ps for n in lens)
+    n_pages = B * max_pages + 2
+    kp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    vp = orc.to_bf16(r.normal((n_pages, ps, Hkv, Dh)))
+    table = np.array(r.uniform(n_pages).argsort(), np.int32)[:B * max_pages].reshape(B, max_pages)
+    q, kn, vn = r.normal((B, Hq, Dh)), r.normal((B, Hkv, Dh)), r.normal((B, Hkv, Dh))
+    pos = np.array(lens, np.int32) - 1
+    scale = 1.0 / math.sqrt(Dh)
+    kp_ref, vp_ref = kp.copy(), vp.copy()
+    for b in range(B):
+        orc.kv_write_paged(kn[b][None], vn[b][None], kp_ref, vp_ref, table[b], ps, int(pos[b]))
+    ref = orc.gqa_decode_paged(q, kp_ref, vp_ref, table, ps, pos, scale, threads=8)
+    dk, dv = up(kp), up(vp)
+    dout = empty((B, Hq, Dh), np.float32)
+    say("append paged generic", Hq, Hkv, Dh)
+    da.GqaDecodeAttnAppendPaged(up(q), up(kn), up(vn), dk, dv, up(table), max_pages, ps, n_pages,
+                                up(pos), dout, B, Hq, Hkv, Dh, scale)
+    check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+               truth=t64.decode_paged(q, kp_ref, vp_ref, table, ps, pos, scale))
+    np.testing.assert_array_equal(down(dk, kp.shape, np.uint16), kp_ref)
+    np.testing.assert_array_equal(down(dv, vp.shape, np.uint16), vp_ref)
+    # a new row whose page lies past the pool: attended from the rows, not written
+    table2 = table.copy()
+    table2[3, (lens[3] - 1) // ps] = n_pages + 5
+    kp2 = kp_ref.copy()
+    kp2[table[3, (lens[3] - 1) // ps], (lens[3] - 1) % ps] = orc.to_bf16(kn[3])
+    vp2 = vp_ref.copy()
+    vp2[table[3, (lens[3] - 1) // ps], (lens[3] - 1) % ps] = orc.to_bf16(vn[3])
+    ref2 = orc.gqa_decode_paged(q[3:4], kp2, vp2, table[3:4], ps, pos[3:4], scale)
+    dk2, dv2 = up(kp_ref), up(vp_ref)
+    dout2 = empty((1, Hq, Dh), np.float32)
+    say("append paged generic, page past the pool")
+    da.GqaDecodeAttnAppendPaged(up(q[3:4]), up(kn[3:4]), up(vn[3:4]), dk2, dv2, up(table2[3:4]),
+                                max_pages, ps, n_pages, up(pos[3:4]), dout2, 1, Hq, Hkv, Dh, scale)
+    check_fp32(down(dout2, (1, Hq, Dh)), ref2, TOL,
+               truth=t64.decode_paged(q[3:4], kp2, vp2, table[3:4], ps, pos[3:4], scale))
+    np.testing.assert_array_equal(down(dk2, kp.shape, np.uint16), kp_ref)

@@ -264,3 +264,34 @@ def test_decode_contiguous_16k_context():
     da.GqaDecodeAttn(up(q), up(kc), up(vc), dout, Hq, Hkv, Dh, up(np.array([S - 1], np.int32)), S,
                      scale)
     check_fp32(down(dout, (Hq, Dh)), ref, TOL, truth=t64.decode(q, kc, vc, S - 1, scale))
+
+
+@pytest.mark.parametrize("Hq,Hkv,Dh,S,cap", [(12, 4, 80, 701, 1024), (8, 1, 256, 33, 64),
+                                             (3, 3, 1024, 130, 256), (16, 2, 48, 2049, 2100)])
+def test_decode_generic_shapes(Hq, Hkv, Dh, S, cap):
+    """GqaDecodeAttnKernel takes any Dh and group (blockDim = Dh): the shapes the split-K
+    kernels are not built for run on the generic kernel, contiguous cache, against the oracle."""
+    q, kc, vc = _contig_case(S * 7 + Dh, S, cap, Hq, Hkv, Dh)
+    dout = empty((Hq, Dh), np.float32)
+    scale = 1.0 / math.sqrt(Dh)
+    say("decode generic", Hq, Hkv, Dh, S)
+    da.GqaDecodeAttn(up(q), up(kc), up(vc), dout, Hq, Hkv, Dh, up(np.array([S - 1], np.int32)),
+                     cap, scale)
+    ref = orc.gqa_decode(q, kc, vc, S - 1, scale)
+    check_fp32(down(dout, (Hq, Dh)), ref, TOL, truth=t64.decode(q, kc, vc, S - 1, scale))
+
+
+def test_decode_paged_generic_shapes():
+    """Paged batched decode with group 3 and Dh 72 (generic kernel): ragged streams."""
+    Hq, Hkv, Dh, ps = 9, 3, 72, 16
+    lens = [1, 16, 17, 500, 1024, 77]
+    q, kp, vp, table, pos = _paged_case(77, lens, Hq=Hq, Hkv=Hkv, Dh=Dh, ps=ps)
+    B, max_pages = table.shape
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_decode_paged(q, kp, vp, table, ps, pos, scale, threads=8)
+    dout = empty((B, Hq, Dh), np.float32)
+    say("decode paged generic")
+    da.GqaDecodeAttnPaged(up(q), up(kp), up(vp), up(table), max_pages, ps, up(pos), dout, B, Hq,
+                          Hkv, Dh, scale)
+    check_fp32(down(dout, (B, Hq, Dh)), ref, TOL,
+               truth=t64.decode_paged(q, kp, vp, table, ps, pos, scale))

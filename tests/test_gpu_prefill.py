@@ -329,3 +329,54 @@ def test_decode_equals_last_prefill_row(S):
     check_fp32(dec, ref, TOL32, truth=truth)
     check_fp32(pre, ref, TOL32, truth=truth)
     assert rel_err(pre, dec, FLOOR) <= 2 * TOL32
+
+
+@pytest.mark.parametrize("T,Hq,Hkv,Dh,pos0", [(37, 12, 4, 80, 5), (20, 8, 1, 256, 0),
+                                              (9, 6, 6, 48, 100), (33, 16, 8, 64, 0),
+                                              (3, 2, 1, 1024, 7), (5, 3, 3, 1, 2)])
+def test_prefill_generic_shapes(T, Hq, Hkv, Dh, pos0):
+    """Head sizes and groups the MFMA kernels are not built for (the reference's kernel takes
+    any Dh <= 256 and any group): Hq/Hkv 3 and 8, Dh 80 / 256 / 48 / 64 / 1024 / 1, a pos0
+    offset -- the generic kernel, fp32 mode, against the oracle at the kernel gate."""
+    r = SplitMix64(T * 31 + Dh)
+    S = pos0 + T
+    kc = orc.to_bf16(r.normal((S, Hkv, Dh)))
+    vc = orc.to_bf16(r.normal((S, Hkv, Dh)))
+    q = r.normal((T, Hq, Dh))
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_prefill(q, kc, vc, pos0, scale)
+    say("prefill generic", T, Hq, Hkv, Dh, pos0)
+    got = _run(q, kc, vc, pos0, S, da.PREFILL_FP32, Hkv)
+    check_fp32(got, ref, TOL32, truth=t64.prefill(q, kc, vc, pos0, scale))
+
+
+def test_prefill_generic_paged_and_bf16_mode():
+    """The generic kernel through a page table (16-key pages, shuffled) and in bf16 mode with
+    a bf16 q (the q_bf16 argument): Hq/Hkv = 3, Dh = 96."""
+    T, Hq, Hkv, Dh, pos0, ps = 41, 6, 2, 96, 30, 16
+    r = SplitMix64(4242)
+    S = pos0 + T
+    n_pages = (S + ps - 1) // ps + 2
+    table = np.array(r.uniform(n_pages).argsort()[: (S + ps - 1) // ps], np.int32)
+    kc = orc.to_bf16(r.normal((S, Hkv, Dh)))
+    vc = orc.to_bf16(r.normal((S, Hkv, Dh)))
+    kp = np.zeros((n_pages, ps, Hkv, Dh), np.uint16)
+    vp = np.zeros_like(kp)
+    for j in range(S):
+        kp[table[j // ps], j % ps] = kc[j]
+        vp[table[j // ps], j % ps] = vc[j]
+    q = r.normal((T, Hq, Dh))
+    scale = 1.0 / math.sqrt(Dh)
+    ref = orc.gqa_prefill(q, kc, vc, pos0, scale)
+    say("prefill generic paged")
+    got = _run(q, kc, vc, pos0, S, da.PREFILL_FP32, Hkv, page=(kp, vp, table, ps))
+    check_fp32(got, ref, TOL32, truth=t64.prefill(q, kc, vc, pos0, scale))
+    # bf16 mode with q given as bf16 bits: the generic kernel reads the rounded q
+    qb = orc.to_bf16(q)
+    ref_b = orc.gqa_prefill(orc.from_bf16(qb), kc, vc, pos0, scale)
+    dout = empty(q.shape, np.float32)
+    say("prefill generic bf16 q")
+    da.GqaCacheAttnEx(None, up(qb), up(kc), up(vc), None, 0, 0, dout, T, Hq, Hkv, Dh,
+                      up(np.array([pos0], np.int32)), S, scale, da.PREFILL_BF16)
+    check_fp32(down(dout, q.shape), ref_b, TOL32,
+               truth=t64.prefill(orc.from_bf16(qb), kc, vc, pos0, scale))

@@ -28,7 +28,9 @@ def windows(N, width):
                                           (390, 16, 64, "full"), (390, 16, 64, "w104"),
                                           (1500, 16, 64, "w104"), (300, 8, 128, "ragged"),
                                           (300, 8, 64, "ragged"), (150, 4, 64, "clamp"),
-                                          (257, 16, 64, "empty")])
+                                          (257, 16, 64, "empty"),
+                                          # head sizes of the generic kernel
+                                          (200, 4, 32, "ragged"), (210, 2, 80, "w104")])
 def test_window_attention_vs_oracle(N, H, Dh, kind):
     r = SplitMix64(N * 3 + H + Dh)
     q, k, v = r.normal((N, H, Dh)), r.normal((N, H, Dh)), r.normal((N, H, Dh))
