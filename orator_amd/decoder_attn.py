@@ -5,7 +5,9 @@ The reference keeps these kernels file-static inside src/model/asr_text_decoder.
 the functions here take the same arguments as those kernels' launches (:412-418,
 :534-541), plus the cache capacity the host already knows (AsrTextConfig.max_seq_len).
 Paged variants add a page table; with contiguous in-order pages they address exactly the
-reference layout [max_seq_len, Hkv, Dh].
+reference layout [max_seq_len, Hkv, Dh].  As the reference's kernels, the attention
+launchers take any head size (up to 1024) and any Hq that is a multiple of Hkv; the
+QK-norm-folded forms take Dh 128 and Hq / Hkv in {1, 2, 4}.
 """
 from __future__ import annotations
 
