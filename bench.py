@@ -44,7 +44,7 @@ LAYERS, B, HQ, HKV, DH, L_BASE, PAGE = 28, 16, 16, 8, 128, 4096, 16
 # HBM bytes per decode op measured with rocprofv3 --pmc at S = 4097..4105 (FETCH_SIZE x 1.9943
 # KiB + WRITE_SIZE KiB, profiles/decode_b16_l4096_hbm_traffic.md) and the algorithmic bytes of
 # the same ops, for the traffic / algorithmic ratio
-HBM_TRAFFIC_PER_OP = 269.40e6
+HBM_TRAFFIC_PER_OP = 269.36e6
 ALGORITHMIC_AT_TRAFFIC = 269.04e6
 
 
@@ -691,7 +691,8 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4),
                      # rocprofv3 FETCH_SIZE x 1.9943 + WRITE_SIZE x 1.0 KiB per decode op
-                     # (wide split + merge kernels) at this workload, S = 4097..4105.
+                     # (one launch of the wide split kernel, its ranges merged in the launch)
+                     # at this workload, S = 4097..4105.
                      "traffic": HBM_TRAFFIC_PER_OP,
                      "traffic_over_algorithmic": round(HBM_TRAFFIC_PER_OP / ALGORITHMIC_AT_TRAFFIC, 3),
                      "kernel": "decode op = gqa_decode_wide_kernel, one launch (each stream and kv "
